@@ -1,0 +1,222 @@
+"""Benchmark: one full cost -> matching -> matched-loss forward + backward step
+of MaskMatchingFunction on the headline configuration (BASELINE.json
+B=16, Q=200, 256x256 bf16 mask logits, G ~ U[5,100], C=133 +
+no-object), synthetic inputs resident in HBM.
+
+Prints ONE JSON line (rank 0).  `value` = milliseconds per step (lower is
+better).  `roofline` = the dominant kernel's algorithmic bytes per launch over
+its average launch duration, measured with HIP events recorded by the library
+on the launch stream during the timed steps.  `cpu_baseline` = the float64
+oracle (a port of the reference algorithm; the reference's own CPU path is not
+buildable here) timed on a bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg3_dense_headline")
+    ap.add_argument("--cpu-sample-queries", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def prof_lib():
+    import mask_loss_amd
+    lib = ctypes.CDLL(mask_loss_amd.HIP_LIBRARY)
+    lib.ml_profile_enable.argtypes = [ctypes.c_int]
+    lib.ml_profile_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
+                                    ctypes.POINTER(ctypes.c_double)]
+    return lib
+
+
+def read_prof(lib, name):
+    n = ctypes.c_int64(0)
+    t = ctypes.c_double(0.0)
+    if lib.ml_profile_read(name.encode(), ctypes.byref(n), ctypes.byref(t)) != 0:
+        return 0, 0.0
+    return n.value, t.value
+
+
+def cpu_baseline(cfg, x_cpu, p2g_gpu, total_gpu, q_sample):
+    """Float64 oracle on image 0 with the first q_sample queries (cost, forward
+    losses, backward) + the C assignment restatement on every image's GPU cost
+    matrix; scaled to one full step."""
+    import numpy as np
+    from oracle import assign as OA
+    from oracle import mask_oracle as O
+    k = cfg.kwargs
+    qs = min(q_sample, cfg.Q)
+    z = x_cpu["mask_logits"][:, :1, :qs].astype(np.float64)
+    tgt = x_cpu["mask_targets"][:1]
+    zc = x_cpu["cls_logits"][:, :1, :qs].astype(np.float64)
+    ct = x_cpu["cls_targets"][:1]
+    t0 = time.perf_counter()
+    sep = O.pairwise_mask_loss_forward(z, tgt, zc, ct, k["smooth"], k["sigmoid_scale"],
+                                       k["dice_scale"], k["cls_scale"], k["background_index"],
+                                       k["uncertainty_gamma"], k["uncertainty_gamma_min"], 0.0,
+                                       -1.0, 0.0, -1.0, True, True)
+    p2g = p2g_gpu[:, :1, :qs]
+    O.matching_forward_losses(sep, p2g, z, zc, tgt.shape, force_cls=True,
+                              void_class_index=cfg.C, use_softmax=True)
+    O.matching_backward(np.ones(1), np.ones(1), np.ones(1), z, tgt, zc, ct, p2g,
+                        background_index=0, force_cls=True, void_class_index=cfg.C,
+                        use_softmax=True)
+    t_img = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    L, B, Q, G = total_gpu.shape
+    OA.assign_batch(total_gpu.reshape(L * B, Q, G), 1e30, 1, 0, nthreads=1)
+    t_match = time.perf_counter() - t0
+    scale = (cfg.L * cfg.B * cfg.Q) / qs
+    ms = (t_img * scale + t_match) * 1e3
+    return {
+        "value": round(ms, 1), "unit": "ms/step", "cores": 1, "kind": "port",
+        "sample": (f"float64 NumPy oracle on 1 image x {qs} of {cfg.Q} queries (cost + matched "
+                   f"loss fwd/bwd, {t_img:.1f} s) scaled x{scale:.0f}, plus the C assignment "
+                   f"restatement on all {L * B} GPU cost matrices ({t_match * 1e3:.1f} ms)"),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not built)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import mask_loss_amd
+    from mask_loss_amd import synth
+    from mask_loss_amd.functions import MaskMatchingFunction
+
+    cfg = synth.BY_NAME[a.config]
+    dev = torch.device("cuda:0")
+    x = synth.make_torch(cfg, dev, logits_on_device_rng=True)
+    z = x["mask_logits"].requires_grad_(True)
+    zc = x["cls_logits"].requires_grad_(True)
+    args = synth.call_args(cfg, dict(x, mask_logits=z, cls_logits=zc))
+
+    state = {}
+
+    def step():
+        z.grad = None
+        zc.grad = None
+        p2g, pr, m, d, c = MaskMatchingFunction.apply(*args)
+        (m.sum() + d.sum() + c.sum()).backward()
+        state["p2g"] = p2g
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    lib = prof_lib()
+    lib.ml_profile_reset()
+    lib.ml_profile_enable(1)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(a.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    lib.ml_profile_enable(0)
+    ms = e0.elapsed_time(e1) / a.steps
+
+    kernels = {}
+    for name in ["prep", "pair_cost", "assign", "layer", "bwd_mask", "bwd_cls"]:
+        n, t = read_prof(lib, name)
+        if n:
+            kernels[name] = {"launches": n, "avg_us": round(1e3 * t / n, 2)}
+    lib.ml_profile_reset()
+
+    p2g = state["p2g"]
+    M = int((p2g >= 0).sum().item())
+    e = z.element_size()
+    K = cfg.H * cfg.W
+    LBQ = cfg.L * cfg.B * cfg.Q
+    Ht, Wt = cfg.H * cfg.scale, cfg.W * cfg.scale
+    Cp = cfg.C + 1
+    bytes_alg = {
+        "pair_cost": e * K * LBQ + 2 * cfg.B * K,        # logits once + compact labels
+        "bwd_mask": e * K * (M + LBQ),                   # matched rows read + all grads written
+        "assign": 4 * LBQ * Cp,                          # class logits
+    }
+    step_bytes = e * K * (LBQ + M + LBQ) + 8 * cfg.B * Ht * Wt + 12 * LBQ * Cp
+    dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
+    dom_bytes = bytes_alg.get(dom)
+    achieved = dom_bytes / (kernels[dom]["avg_us"] * 1e-6) / 1e9 if dom_bytes else None
+    roofline = {
+        "kernel": dom,
+        "bound": "hbm",
+        "achieved": round(achieved, 1) if achieved else None,
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+        "traffic": None,
+        "algorithmic_bytes": dom_bytes,
+        "avg_launch_us": kernels[dom]["avg_us"],
+    }
+    step_roof = {
+        "algorithmic_bytes": step_bytes,
+        "hbm_floor_us": round(step_bytes / HBM_PEAK_GBS / 1e3, 1),
+        "frac": round(step_bytes / HBM_PEAK_GBS / 1e3 / (ms * 1e3), 4),
+    }
+
+    cpu = None
+    if not a.no_cpu_baseline:
+        qs = min(a.cpu_sample_queries, cfg.Q)
+        x_cpu = {  # the same inputs, image 0, first qs queries
+            "mask_logits": z.detach()[:, :1, :qs].float().cpu().numpy(),
+            "mask_targets": x["mask_targets"][:1].cpu().numpy(),
+            "cls_logits": zc.detach()[:, :1, :qs].float().cpu().numpy(),
+            "cls_targets": x["cls_targets"][:1].cpu().numpy(),
+        }
+        sep = mask_loss_amd.mask_loss.pairwise_mask_loss_forward(
+            z.detach(), x["mask_targets"], zc.detach(), x["cls_targets"], 1.0, 1.0, 1.0, 1.0, 0,
+            1.0, 0.05, 0.0, -1.0, 0.0, -1.0, True, True)
+        total = ((sep[0] + sep[1]) + sep[2]).double().cpu().numpy()
+        cpu = cpu_baseline(cfg, x_cpu, p2g.cpu().numpy(), total, qs)
+
+    out = {
+        "metric": "ms per cost+match+loss fwd/bwd step (B=16,Q=200,256²); % MFMA/HBM roofline",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "images_per_s": round(cfg.B * cfg.L / (ms * 1e-3), 1),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == "bfloat16" else "f32",
+        "data": "synthetic (label maps from the NumPy recipe, logits from the device RNG)",
+        "config": {"workload": cfg.name, "L": cfg.L, "B": cfg.B, "Q": cfg.Q, "H": cfg.H,
+                   "W": cfg.W, "G": list(cfg.G), "C": cfg.C + 1, "matched": M,
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "step_roofline": step_roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

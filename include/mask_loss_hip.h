@@ -1,0 +1,154 @@
+/*
+ * mask_loss_hip.h -- C ABI of the MI355X (gfx950) mask-cost / assignment /
+ * matched-loss library (libmask_loss_hip.so).
+ *
+ * Plain pointers, sizes and a hipStream_t; no framework types.  Every entry
+ * point enqueues work on `stream` and returns without synchronising.  All
+ * device pointers must be device-accessible, contiguous, row-major.
+ * Return value: ML_OK (0) or an ML_E* code; ml_last_error() returns the
+ * message of the last failure on the calling thread.
+ *
+ * Scratch memory is never allocated inside: callers query the size with the
+ * matching *_workspace_size() function and pass a device buffer of at least
+ * that many bytes (256-byte aligned).
+ *
+ * Reference interface replaced by each entry point (AndyBarcia/mask_loss):
+ *   ml_pairwise_mask_loss_forward   src/cuda/pw_mask.cu:314-501
+ *                                   (bound at src/bindings.cpp:164)
+ *   ml_mask_matching_forward        src/cpu/matching.cpp:592-752
+ *                                   (bound at src/bindings.cpp:165)
+ *   ml_mask_matching_backward       src/cuda/mask_matching_backward.cu:378-621
+ *                                   (bound at src/bindings.cpp:166)
+ *   ml_pairwise_label_loss_forward  src/cuda/pw_sigmoid_label_loss.cu:108-187 and
+ *                                   src/cuda/pw_softmax_label_loss.cu:105-173
+ *                                   (bound at src/bindings.cpp:167-168)
+ */
+#ifndef MASK_LOSS_HIP_H
+#define MASK_LOSS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ml_stream_t; /* == hipStream_t */
+
+enum {
+  ML_OK = 0,
+  ML_EINVAL = 1,     /* invalid argument (shape, range, flag combination) */
+  ML_EWORKSPACE = 2, /* workspace too small */
+  ML_ELAUNCH = 3,    /* HIP launch / runtime error */
+  ML_EUNSUPPORTED = 4
+};
+
+enum { ML_F32 = 0, ML_BF16 = 1, ML_F16 = 2 };
+
+/* Strategy ids, reference src/cpu/matching.cpp:60-65. */
+enum { ML_GLOBAL = 0, ML_ROUND = 1, ML_GREEDY = 2, ML_PSEUDO_GREEDY = 3 };
+
+/* Shapes of one call.  mask logits (L,B,Q,H,W); targets (B,Ht,Wt) int64 label
+ * map; cls logits (L,B,Q,C); cls targets (B,GT_total) int64 (-1 padding). */
+typedef struct ml_shape {
+  int64_t L, B, Q, H, W, Ht, Wt, C, GT_total;
+} ml_shape;
+
+/* Loss / matching options; field meaning follows the positional arguments of
+ * mask_matching (src/bindings.cpp:84-111, src/cpu/matching.cpp:592-617). */
+typedef struct ml_params {
+  float smooth, sigmoid_scale, dice_scale, cls_scale;
+  int64_t background_index;
+  float uncertainty_gamma, uncertainty_gamma_min;
+  double inf_thresh, num_masks;
+  int32_t force_unmatched_class_to_background;
+  int32_t force_unmatched_masks_to_empty;
+  int64_t topk_matches, strategy_id;
+  float mask_gamma, mask_alpha, cls_gamma, cls_alpha;
+  int64_t void_class_index;
+  int32_t use_softmax_label_loss;
+  int32_t normalize_uncertainty;
+} ml_params;
+
+/* Per-query statistics saved by the forward for the fused backward:
+ * stats[(l*B+b)*Q+q][ML_STAT_*] (float). */
+enum {
+  ML_STAT_S = 0,    /* uncertainty normaliser after normalise/clamp */
+  ML_STAT_P = 1,    /* sum_j N2 w p */
+  ML_STAT_I = 2,    /* sum_j w p n  for the matched GT (0 if unmatched) */
+  ML_STAT_T = 3,    /* sum_j w n    for the matched GT (0 if unmatched) */
+  ML_STATS = 4
+};
+/* Per-layer block appended after the per-query stats: layer[l][ML_LAYER_*]. */
+enum { ML_LAYER_INV_MASK_DEN = 0, ML_LAYER_INV_CLS_DEN = 1, ML_LAYERS = 2 };
+size_t ml_stats_floats(const ml_shape* s);
+
+const char* ml_last_error(void);
+int ml_version(void);
+
+/* ---- pairwise mask + label cost (3, L, B, Q, GT_out) float ---------------- */
+size_t ml_pairwise_mask_loss_workspace_size(const ml_shape* s, const ml_params* p,
+                                            int mask_dtype);
+int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p,
+                                  int mask_dtype, const void* mask_logits,
+                                  const int64_t* mask_targets, int cls_dtype,
+                                  const void* cls_logits, const int64_t* cls_targets,
+                                  float* separate_costs, void* workspace,
+                                  size_t workspace_bytes, ml_stream_t stream);
+
+/* ---- full matching forward: costs -> assignment -> per-layer means -------- */
+size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p,
+                                       int mask_dtype);
+/* pred_to_gt / pred_round: (L,B,Q) int64; layer_means: (3,L) float
+ * [mask, dice, cls]; separate_costs: (3,L,B,Q,GT_out) float or NULL;
+ * stats: ml_stats_floats() floats or NULL. */
+int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
+                             const void* mask_logits, const int64_t* mask_targets,
+                             int cls_dtype, const void* cls_logits,
+                             const int64_t* cls_targets, int64_t* pred_to_gt,
+                             int64_t* pred_round, float* layer_means,
+                             float* separate_costs, float* stats, void* workspace,
+                             size_t workspace_bytes, ml_stream_t stream);
+
+/* ---- matching backward ------------------------------------------------------
+ * grad_{mask,dice,cls}: (L,) float upstream gradients of the layer means.
+ * grad_mask_logits: (L,B,Q,H,W) in mask_dtype; grad_cls_logits: (L,B,Q,C) in
+ * cls_dtype.  stats == NULL recomputes the per-query statistics from the
+ * logits (the reference's two-pass backward); otherwise the statistics saved
+ * by ml_mask_matching_forward are used and the logits are read once. */
+size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,
+                                                int mask_dtype);
+int ml_mask_matching_backward(const ml_shape* s, const ml_params* p,
+                              const float* grad_mask, const float* grad_dice,
+                              const float* grad_cls, int mask_dtype,
+                              const void* mask_logits, const int64_t* mask_targets,
+                              int cls_dtype, const void* cls_logits,
+                              const int64_t* cls_targets, const int64_t* pred_to_gt,
+                              const float* stats, void* grad_mask_logits,
+                              void* grad_cls_logits, void* workspace,
+                              size_t workspace_bytes, ml_stream_t stream);
+
+/* ---- pairwise label cost (L,B,Q,GT_out) float; use_softmax selects the
+ * softmax-CE form, otherwise sigmoid-BCE with (gamma, alpha). -------------- */
+int ml_pairwise_label_loss_forward(int64_t L, int64_t B, int64_t Q, int64_t C,
+                                   int64_t GT_total, int cls_dtype,
+                                   const void* cls_logits, const int64_t* cls_targets,
+                                   int64_t background_index, float scale, float gamma,
+                                   float alpha, int use_softmax, float* out,
+                                   ml_stream_t stream);
+
+/* ---- instrumentation (no counterpart in the reference) ---------------------
+ * When enabled, every kernel launch of this library is bracketed by HIP events
+ * recorded on its own stream.  ml_profile_read() waits for those events and
+ * returns, for kernel family `name` ("prep", "pair_cost", "assign", "layer",
+ * "bwd_mask", "bwd_cls", "label_cost"), the number of launches and their
+ * summed duration in milliseconds since the last reset. */
+int ml_profile_enable(int enable);
+int ml_profile_read(const char* name, int64_t* launches, double* total_ms);
+int ml_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MASK_LOSS_HIP_H */

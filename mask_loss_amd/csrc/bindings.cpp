@@ -1,0 +1,356 @@
+// PyTorch-ROCm extension module `mask_loss`: the reference's operator surface
+// (src/bindings.cpp:157-169, all-positional arguments) over the C ABI of
+// libmask_loss_hip.so (include/mask_loss_hip.h).  Tensors are validated the
+// way the reference validates them (device + contiguous, shapes, ranges),
+// outputs and workspaces come from PyTorch's caching allocator, and every
+// launch goes to the current HIP stream.  There is no CPU implementation:
+// host tensors raise, as in the reference (src/cuda/utils.h:4-6,
+// src/cpu/matching.cpp:618).
+#include <ATen/hip/HIPContext.h>
+#include <torch/extension.h>
+
+#include <vector>
+
+#include "../../include/mask_loss_hip.h"
+
+namespace {
+
+#define ML_CHECK_INPUT(x)                                              \
+  TORCH_CHECK((x).is_cuda(), #x " must be a CUDA tensor");             \
+  TORCH_CHECK((x).is_contiguous(), #x " must be contiguous")
+
+int dtype_code(const torch::Tensor& t, const char* name) {
+  switch (t.scalar_type()) {
+    case torch::kFloat32: return ML_F32;
+    case torch::kBFloat16: return ML_BF16;
+    case torch::kFloat16: return ML_F16;
+    default: TORCH_CHECK(false, name, " must be float32, bfloat16 or float16");
+  }
+  return -1;
+}
+
+void ml_ok(int rc) { TORCH_CHECK(rc == ML_OK, ml_last_error()); }
+
+ml_stream_t cur_stream() { return (ml_stream_t)at::hip::getCurrentHIPStream().stream(); }
+
+torch::Tensor workspace(size_t bytes, const torch::Tensor& like) {
+  return torch::empty({(int64_t)std::max<size_t>(bytes, 256)},
+                      like.options().dtype(torch::kUInt8));
+}
+
+ml_shape make_shape(const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+                    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets) {
+  TORCH_CHECK(mask_logits.dim() == 5, "mask_logits must be (L,B,Q,H,W)");
+  TORCH_CHECK(mask_targets.dim() == 3, "mask_targets must be (B,H_t,W_t)");
+  TORCH_CHECK(cls_logits.dim() == 4, "cls_logits must be (L,B,Q,C)");
+  TORCH_CHECK(cls_targets.dim() == 2, "cls_targets must be (B,GT)");
+  TORCH_CHECK(mask_targets.scalar_type() == torch::kLong, "mask_targets must be int64");
+  TORCH_CHECK(cls_targets.scalar_type() == torch::kLong, "cls_targets must be int64");
+  ml_shape s;
+  s.L = mask_logits.size(0);
+  s.B = mask_logits.size(1);
+  s.Q = mask_logits.size(2);
+  s.H = mask_logits.size(3);
+  s.W = mask_logits.size(4);
+  s.Ht = mask_targets.size(1);
+  s.Wt = mask_targets.size(2);
+  s.C = cls_logits.size(3);
+  s.GT_total = cls_targets.size(1);
+  TORCH_CHECK(mask_targets.size(0) == s.B, "Batch size mismatch between logits and targets");
+  TORCH_CHECK(cls_targets.size(0) == s.B, "Batch size mismatch between logits and cls targets");
+  TORCH_CHECK(cls_logits.size(0) == s.L && cls_logits.size(1) == s.B && cls_logits.size(2) == s.Q,
+              "cls_logits must match mask logits dimensions");
+  const auto dev = mask_logits.device();
+  TORCH_CHECK(mask_targets.device() == dev && cls_logits.device() == dev &&
+                  cls_targets.device() == dev,
+              "all tensors must be on the same device");
+  return s;
+}
+
+ml_params make_params(double smooth, double sigmoid_scale, double dice_scale, double cls_scale,
+                      int64_t background_index, double ug, double ug_min, double inf_thresh,
+                      double num_masks, bool force_cls, bool force_masks, int64_t topk,
+                      int64_t strategy, double mask_gamma, double mask_alpha, double cls_gamma,
+                      double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize) {
+  ml_params p;
+  p.smooth = (float)smooth;
+  p.sigmoid_scale = (float)sigmoid_scale;
+  p.dice_scale = (float)dice_scale;
+  p.cls_scale = (float)cls_scale;
+  p.background_index = background_index;
+  p.uncertainty_gamma = (float)ug;
+  p.uncertainty_gamma_min = (float)ug_min;
+  p.inf_thresh = inf_thresh;
+  p.num_masks = num_masks;
+  p.force_unmatched_class_to_background = force_cls;
+  p.force_unmatched_masks_to_empty = force_masks;
+  p.topk_matches = topk;
+  p.strategy_id = strategy;
+  p.mask_gamma = (float)mask_gamma;
+  p.mask_alpha = (float)mask_alpha;
+  p.cls_gamma = (float)cls_gamma;
+  p.cls_alpha = (float)cls_alpha;
+  p.void_class_index = void_idx;
+  p.use_softmax_label_loss = use_softmax;
+  p.normalize_uncertainty = normalize;
+  return p;
+}
+
+int64_t gt_out_of(int64_t GT_total, int64_t bg) {
+  return GT_total - ((bg >= 0 && bg < GT_total) ? 1 : 0);
+}
+
+// --------------------------------------------------------------------------
+// pairwise_mask_loss_forward  (src/bindings.cpp:164, src/cuda/pw_mask.cu:314)
+// --------------------------------------------------------------------------
+torch::Tensor pairwise_mask_loss_forward(const torch::Tensor& mask_logits,
+                                         const torch::Tensor& mask_targets,
+                                         const torch::Tensor& cls_logits,
+                                         const torch::Tensor& cls_targets, double smooth,
+                                         double sigmoid_scale, double dice_scale,
+                                         double cls_scale, int64_t background_index, double ug,
+                                         double ug_min, double mask_gamma, double mask_alpha,
+                                         double cls_gamma, double cls_alpha, bool use_softmax,
+                                         bool normalize) {
+  ML_CHECK_INPUT(mask_logits);
+  ML_CHECK_INPUT(mask_targets);
+  ML_CHECK_INPUT(cls_logits);
+  ML_CHECK_INPUT(cls_targets);
+  const ml_shape s = make_shape(mask_logits, mask_targets, cls_logits, cls_targets);
+  const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
+                                  ug, ug_min, 1e30, -1.0, false, false, 1, 0, mask_gamma,
+                                  mask_alpha, cls_gamma, cls_alpha, -1, use_softmax, normalize);
+  const int64_t GT_out = gt_out_of(s.GT_total, background_index);
+  const int mdt = dtype_code(mask_logits, "mask_logits");
+  const int cdt = dtype_code(cls_logits, "cls_logits");
+  if (GT_out == 0)  // reference returns (L,B,Q,0) here (pw_mask.cu:402-404)
+    return torch::zeros({s.L, s.B, s.Q, 0}, mask_logits.options().dtype(torch::kFloat32));
+  auto out = torch::empty({3, s.L, s.B, s.Q, GT_out}, mask_logits.options().dtype(torch::kFloat32));
+  const size_t wsb = ml_pairwise_mask_loss_workspace_size(&s, &p, mdt);
+  TORCH_CHECK(wsb > 0 || s.B == 0, "unsupported shape");
+  auto ws = workspace(wsb, mask_logits);
+  ml_ok(ml_pairwise_mask_loss_forward(&s, &p, mdt, mask_logits.data_ptr(),
+                                      mask_targets.data_ptr<int64_t>(), cdt, cls_logits.data_ptr(),
+                                      cls_targets.data_ptr<int64_t>(), out.data_ptr<float>(),
+                                      ws.data_ptr(), ws.numel(), cur_stream()));
+  return out;
+}
+
+// --------------------------------------------------------------------------
+// mask_matching  (src/bindings.cpp:165, src/cpu/matching.cpp:592)
+// --------------------------------------------------------------------------
+std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
+                                         const torch::Tensor& mask_targets,
+                                         const torch::Tensor& cls_logits,
+                                         const torch::Tensor& cls_targets, const ml_params& p,
+                                         bool want_stats) {
+  ML_CHECK_INPUT(mask_logits);
+  ML_CHECK_INPUT(mask_targets);
+  ML_CHECK_INPUT(cls_logits);
+  ML_CHECK_INPUT(cls_targets);
+  const ml_shape s = make_shape(mask_logits, mask_targets, cls_logits, cls_targets);
+  const int mdt = dtype_code(mask_logits, "mask_logits");
+  const int cdt = dtype_code(cls_logits, "cls_logits");
+  auto i64 = mask_logits.options().dtype(torch::kLong);
+  auto f32 = mask_logits.options().dtype(torch::kFloat32);
+  auto pred_to_gt = torch::empty({s.L, s.B, s.Q}, i64);
+  auto pred_round = torch::empty({s.L, s.B, s.Q}, i64);
+  auto means = torch::empty({3, s.L}, f32);
+  torch::Tensor stats;
+  if (want_stats) stats = torch::empty({(int64_t)ml_stats_floats(&s)}, f32);
+  const size_t wsb = ml_mask_matching_workspace_size(&s, &p, mdt);
+  auto ws = workspace(wsb, mask_logits);
+  TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, "unsupported shape for mask_matching");
+  ml_ok(ml_mask_matching_forward(
+      &s, &p, mdt, mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt,
+      cls_logits.data_ptr(), cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
+      pred_round.data_ptr<int64_t>(), means.data_ptr<float>(), nullptr,
+      want_stats ? stats.data_ptr<float>() : nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
+  // means follow the logits dtype (src/cuda/mask_matching_forward.cu:580-583);
+  // the fused entry keeps them in float32
+  const auto out_dt = want_stats ? torch::kFloat32 : mask_logits.scalar_type();
+  std::vector<torch::Tensor> r = {pred_to_gt, pred_round, means[0].to(out_dt),
+                                  means[1].to(out_dt), means[2].to(out_dt)};
+  if (want_stats) r.push_back(stats);
+  return r;
+}
+
+std::vector<torch::Tensor> mask_matching(
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets, double smooth,
+    double sigmoid_scale, double dice_scale, double cls_scale, int64_t background_index, double ug,
+    double ug_min, double inf_thresh, double num_masks, bool force_cls, bool force_masks,
+    int64_t topk, int64_t strategy, double mask_gamma, double mask_alpha, double cls_gamma,
+    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize) {
+  const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
+                                  ug, ug_min, inf_thresh, num_masks, force_cls, force_masks, topk,
+                                  strategy, mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
+                                  use_softmax, normalize);
+  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, false);
+}
+
+// The reference's MaskMatchingFunction passes normalize_uncertainty a second
+// time after uncertainty_gamma_min (functions/mask/matching.py:198-224); this
+// overload accepts that 25-argument call.
+std::vector<torch::Tensor> mask_matching_wrapper_order(
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets, double smooth,
+    double sigmoid_scale, double dice_scale, double cls_scale, int64_t background_index, double ug,
+    double ug_min, bool normalize_early, double inf_thresh, double num_masks, bool force_cls,
+    bool force_masks, int64_t topk, int64_t strategy, double mask_gamma, double mask_alpha,
+    double cls_gamma, double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize) {
+  (void)normalize_early;
+  return mask_matching(mask_logits, mask_targets, cls_logits, cls_targets, smooth, sigmoid_scale,
+                       dice_scale, cls_scale, background_index, ug, ug_min, inf_thresh, num_masks,
+                       force_cls, force_masks, topk, strategy, mask_gamma, mask_alpha, cls_gamma,
+                       cls_alpha, void_idx, use_softmax, normalize);
+}
+
+// Same as mask_matching, plus a sixth output: the per-query statistics the
+// fused backward uses to read every logit once.
+std::vector<torch::Tensor> mask_matching_fused(
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets, double smooth,
+    double sigmoid_scale, double dice_scale, double cls_scale, int64_t background_index, double ug,
+    double ug_min, double inf_thresh, double num_masks, bool force_cls, bool force_masks,
+    int64_t topk, int64_t strategy, double mask_gamma, double mask_alpha, double cls_gamma,
+    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize) {
+  const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
+                                  ug, ug_min, inf_thresh, num_masks, force_cls, force_masks, topk,
+                                  strategy, mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
+                                  use_softmax, normalize);
+  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, true);
+}
+
+// --------------------------------------------------------------------------
+// mask_matching_backward  (src/bindings.cpp:166, mask_matching_backward.cu:378)
+// --------------------------------------------------------------------------
+std::vector<torch::Tensor> backward_impl(
+    const torch::Tensor& g_mask, const torch::Tensor& g_dice, const torch::Tensor& g_cls,
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets,
+    const torch::Tensor& pred_to_gt, const ml_params& p, const torch::Tensor* stats) {
+  ML_CHECK_INPUT(mask_logits);
+  ML_CHECK_INPUT(mask_targets);
+  ML_CHECK_INPUT(cls_logits);
+  ML_CHECK_INPUT(cls_targets);
+  ML_CHECK_INPUT(pred_to_gt);
+  const ml_shape s = make_shape(mask_logits, mask_targets, cls_logits, cls_targets);
+  TORCH_CHECK(pred_to_gt.scalar_type() == torch::kLong, "pred_to_gt must be int64");
+  TORCH_CHECK(pred_to_gt.dim() == 3 && pred_to_gt.size(0) == s.L && pred_to_gt.size(1) == s.B &&
+                  pred_to_gt.size(2) == s.Q,
+              "pred_to_gt must have shape (L,B,Q)");
+  auto f32 = mask_logits.options().dtype(torch::kFloat32);
+  auto gm = g_mask.to(f32).contiguous();
+  auto gd = g_dice.to(f32).contiguous();
+  auto gc = g_cls.to(f32).contiguous();
+  TORCH_CHECK(gm.numel() == s.L && gd.numel() == s.L && gc.numel() == s.L,
+              "upstream gradients must have shape (L,)");
+  const int mdt = dtype_code(mask_logits, "mask_logits");
+  const int cdt = dtype_code(cls_logits, "cls_logits");
+  auto grad_mask = torch::empty_like(mask_logits);
+  auto grad_cls = torch::empty_like(cls_logits);
+  if (stats) {
+    ML_CHECK_INPUT(*stats);
+    TORCH_CHECK(stats->numel() == (int64_t)ml_stats_floats(&s), "stats size mismatch");
+  }
+  const size_t wsb = ml_mask_matching_backward_workspace_size(&s, &p, mdt);
+  auto ws = workspace(wsb, mask_logits);
+  ml_ok(ml_mask_matching_backward(
+      &s, &p, gm.data_ptr<float>(), gd.data_ptr<float>(), gc.data_ptr<float>(), mdt,
+      mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt, cls_logits.data_ptr(),
+      cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
+      stats ? stats->data_ptr<float>() : nullptr, grad_mask.data_ptr(), grad_cls.data_ptr(),
+      ws.data_ptr(), ws.numel(), cur_stream()));
+  return {grad_mask, grad_cls};
+}
+
+std::vector<torch::Tensor> mask_matching_backward(
+    const torch::Tensor& g_mask, const torch::Tensor& g_dice, const torch::Tensor& g_cls,
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets,
+    const torch::Tensor& pred_to_gt, double smooth, double sigmoid_scale, double dice_scale,
+    double cls_scale, int64_t background_index, double ug, double ug_min, double num_masks,
+    bool force_cls, bool force_masks, double mask_gamma, double mask_alpha, double cls_gamma,
+    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize) {
+  const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
+                                  ug, ug_min, 1e30, num_masks, force_cls, force_masks, 1, 0,
+                                  mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
+                                  use_softmax, normalize);
+  return backward_impl(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logits, cls_targets,
+                       pred_to_gt, p, nullptr);
+}
+
+std::vector<torch::Tensor> mask_matching_backward_fused(
+    const torch::Tensor& g_mask, const torch::Tensor& g_dice, const torch::Tensor& g_cls,
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets,
+    const torch::Tensor& pred_to_gt, double smooth, double sigmoid_scale, double dice_scale,
+    double cls_scale, int64_t background_index, double ug, double ug_min, double num_masks,
+    bool force_cls, bool force_masks, double mask_gamma, double mask_alpha, double cls_gamma,
+    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize,
+    const torch::Tensor& stats) {
+  const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
+                                  ug, ug_min, 1e30, num_masks, force_cls, force_masks, 1, 0,
+                                  mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
+                                  use_softmax, normalize);
+  return backward_impl(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logits, cls_targets,
+                       pred_to_gt, p, &stats);
+}
+
+// --------------------------------------------------------------------------
+// pairwise label losses (src/bindings.cpp:167-168)
+// --------------------------------------------------------------------------
+torch::Tensor label_impl(const torch::Tensor& logits, const torch::Tensor& targets,
+                         int64_t background_index, double scale, double gamma, double alpha,
+                         bool use_softmax) {
+  ML_CHECK_INPUT(logits);
+  ML_CHECK_INPUT(targets);
+  TORCH_CHECK(logits.dim() == 4, "logits must be (L,B,Q,C)");
+  TORCH_CHECK(targets.dim() == 2, "targets must be (B,GT)");
+  TORCH_CHECK(targets.scalar_type() == torch::kLong, "targets must be int64");
+  TORCH_CHECK(logits.size(1) == targets.size(0), "batch size mismatch between logits and targets");
+  const int64_t L = logits.size(0), B = logits.size(1), Q = logits.size(2), C = logits.size(3);
+  const int64_t GT_total = targets.size(1);
+  const int64_t GT_out = gt_out_of(GT_total, background_index);
+  auto out = torch::empty({L, B, Q, GT_out}, logits.options().dtype(torch::kFloat32));
+  if (GT_out == 0) return out;
+  ml_ok(ml_pairwise_label_loss_forward(L, B, Q, C, GT_total, dtype_code(logits, "logits"),
+                                       logits.data_ptr(), targets.data_ptr<int64_t>(),
+                                       background_index, (float)scale, (float)gamma, (float)alpha,
+                                       use_softmax, out.data_ptr<float>(), cur_stream()));
+  return out;
+}
+
+torch::Tensor forward_pw_sigmoid_label_loss(const torch::Tensor& logits,
+                                            const torch::Tensor& targets,
+                                            int64_t background_index, double scale, double gamma,
+                                            double alpha) {
+  return label_impl(logits, targets, background_index, scale, gamma, alpha, false);
+}
+
+torch::Tensor forward_pw_softmax_label_loss(const torch::Tensor& logits,
+                                            const torch::Tensor& targets,
+                                            int64_t background_index, double scale) {
+  return label_impl(logits, targets, background_index, scale, 0.0, -1.0, true);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("pairwise_mask_loss_forward", &pairwise_mask_loss_forward,
+        "Dice+Sigmoid+label pairwise cost forward (HIP, gfx950)");
+  m.def("mask_matching", &mask_matching, "Mask matching: cost, assignment, loss forward (HIP)");
+  m.def("mask_matching", &mask_matching_wrapper_order,
+        "Mask matching, argument order used by MaskMatchingFunction (HIP)");
+  m.def("mask_matching_backward", &mask_matching_backward, "Mask matching backward (HIP)");
+  m.def("mask_matching_fused", &mask_matching_fused,
+        "Mask matching forward that also returns per-query statistics (HIP)");
+  m.def("mask_matching_backward_fused", &mask_matching_backward_fused,
+        "Mask matching backward using saved per-query statistics (HIP)");
+  m.def("forward_pw_sigmoid_label_loss", &forward_pw_sigmoid_label_loss,
+        "Pairwise sigmoid label cost forward (HIP)");
+  m.def("forward_pw_softmax_label_loss", &forward_pw_softmax_label_loss,
+        "Pairwise softmax label cost forward (HIP)");
+  m.attr("__backend__") = "hip-gfx950";
+}

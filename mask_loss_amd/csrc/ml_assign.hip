@@ -1,0 +1,775 @@
+// Per-image finalize + assignment + matched-loss forward partials.
+//
+// One workgroup (4 waves) per (layer, image):
+//   1. per-query statistics: uncertainty normaliser S and mass P (from the
+//      ones column of the cost contraction), label-loss row terms, unmatched
+//      penalties (src/cuda/mask_matching_forward.cu:125-277);
+//   2. every (query, column) cost: bce, dice (src/cuda/pw_mask.cu:299-305),
+//      label cost (src/cuda/pw_sigmoid_label_loss.cu:76-105,
+//      src/cuda/pw_softmax_label_loss.cu:84-102), total = (bce+dice)+cls as
+//      float (src/cpu/matching.cpp:665), column validity
+//      (src/cpu/matching.cpp:497-511);
+//   3. assignment on wave 0 in float64 (src/cpu/matching.cpp:95-463): the
+//      e-maxx shortest augmenting path with the reference's operation order
+//      cur = (c - u[i0]) - v[j], strict '<' updates and lowest-index argmin,
+//      so it returns the reference's assignment bit for bit on the same cost
+//      matrix;
+//   4. pred_round ranking by (cost, query) (src/cpu/matching.cpp:533-565),
+//      per-image matched-loss sums (src/cuda/mask_matching_forward.cu:63-71)
+//      and per-query statistics for the fused backward.
+#include "ml_internal.h"
+
+namespace ml {
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ double wave_min_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmin(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float cls_elem(const void* p, int dt, int64_t i) {
+  if (dt == ML_F32) return ((const float*)p)[i];
+  const uint16_t h = ((const uint16_t*)p)[i];
+  if (dt == ML_BF16) return __uint_as_float(((uint32_t)h) << 16);
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Reference float32 formulas for one label logit (mask_matching_forward.cu:195-218).
+struct ClsTerm {
+  float neg, pos;
+};
+__device__ __forceinline__ ClsTerm cls_terms(float z, const ElemParams& ep) {
+  const Sig s = sig_terms(z);
+  float mn, mp;
+  focal_mods(s, ep, mn, mp);
+  ClsTerm t;
+  t.neg = ep.an * mn * s.cn;
+  t.pos = ep.ap * mp * s.cp;
+  return t;
+}
+
+struct SmemLayout {
+  size_t rowS, rowP, clsA, clsPen, mPen, dPen, contrib, colok, vcols, preds, p, way, u, hrows,
+      asg, costL, total;
+};
+
+__host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, bool cost_in_lds) {
+  SmemLayout s;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    size_t r = o;
+    o += (bytes + 15) & ~size_t(15);
+    return r;
+  };
+  s.rowS = take(Q * 4);
+  s.rowP = take(Q * 4);
+  s.clsA = take(Q * 4);
+  s.clsPen = take(Q * 4);
+  s.mPen = take(Q * 4);
+  s.dPen = take(Q * 4);
+  s.contrib = take(Q * 4 * 4);
+  s.colok = take((GTo + 1) * 4);
+  s.vcols = take((GTo + 1) * 4);
+  s.preds = take((Q + 1) * 4);
+  s.p = take((Q + 1) * 4);
+  s.way = take((Q + 1) * 4);
+  s.u = take((Q + 1) * 8);
+  s.hrows = take((Q + 1) * 4);
+  s.asg = take((Q + 1) * 4);
+  s.costL = o;
+  if (cost_in_lds) take(GTo * Q * 4);
+  s.total = o;
+  return s;
+}
+
+struct Ctx {
+  const AssignArgs* a;
+  int64_t lb, l, b;
+  int G;
+  const float* rowS;
+  const float* rowP;
+  const float* clsA;
+};
+
+// bce, dice, cls of (q, column c) from the K-split partials.
+__device__ void pair_costs(const Ctx& x, int64_t q, int64_t c, float& bce, float& dice,
+                           float& cls) {
+  const AssignArgs& a = *x.a;
+  const int slot = a.slot_of_col[x.b * a.GT_out + c];
+  if (slot < 0) {
+    bce = INFINITY;
+    dice = INFINITY;
+  } else {
+    const int64_t rt = q / a.rows, row = q % a.rows;
+    float num = 0.f, I = 0.f, T = 0.f;
+    for (int64_t ks = 0; ks < a.KS; ++ks) {
+      const float* P = a.partials +
+                       ((ks * (a.L * a.B) + x.lb) * a.rtiles + rt) * 3 * a.rows * a.nslot;
+      num += P[(0 * a.rows + row) * a.nslot + slot];
+      I += P[(1 * a.rows + row) * a.nslot + slot];
+      T += P[(2 * a.rows + row) * a.nslot + slot];
+    }
+    bce = num / x.rowS[q] * a.sigmoid_scale;
+    dice = (1.f - (2.f * I + a.smooth) / (x.rowP[q] + T + a.smooth)) * a.dice_scale;
+  }
+  const int64_t act = c + (c >= a.bg ? 1 : 0);
+  const int64_t y = a.cls_targets[x.b * a.GT_total + act];
+  if (y < 0 || y >= a.C) {
+    cls = INFINITY;
+  } else {
+    const float zy = cls_elem(a.cls_logits, a.cls_dtype, (x.lb * a.Q + q) * a.C + y);
+    if (a.use_softmax) {
+      cls = (x.clsA[q] - zy) * a.cls_scale;
+    } else {
+      const ClsTerm t = cls_terms(zy, a.cls_ep);
+      cls = (x.clsA[q] + (t.pos - t.neg)) * (1.f / (float)a.C) * a.cls_scale;
+    }
+  }
+}
+
+__device__ __forceinline__ bool cost_ok(double c, double thr) { return isfinite(c) && c < thr; }
+
+// ---------------------------------------------------------------------------
+// e-maxx Hungarian on one wave.  Rows = hrows[0..M) (GT columns), columns =
+// preds[0..n) (queries).  asg[k] = row index assigned to column k, or -1.
+// Mirrors src/cpu/matching.cpp:95-186 operation by operation.
+// ---------------------------------------------------------------------------
+template <int NJ>
+__device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds, int n,
+                               const int* hrows, int M, double thr, double BIG, int* p, int* way,
+                               double* u, int* asg) {
+  const int lane = threadIdx.x & 63;
+  for (int k = lane; k < n; k += 64) asg[k] = -1;
+  wave_sync();
+  if (M == 0 || n == 0 || n < M) return true;
+  for (int j = lane; j <= n; j += 64) p[j] = 0;
+  for (int i = lane; i <= M; i += 64) u[i] = 0.0;
+  double v[NJ];
+  int pj[NJ];
+  int predj[NJ];
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) {
+    v[t] = 0.0;
+    pj[t] = 0;
+    const int j = 1 + lane + 64 * t;
+    predj[t] = j <= n ? preds[j - 1] : 0;
+  }
+  wave_sync();
+  bool ok = true;
+  for (int i = 1; i <= M && ok; ++i) {
+    double minv[NJ];
+    int wy[NJ];
+    unsigned used = 0;  // bit t: column 1+lane+64t visited
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      minv[t] = INFINITY;
+      wy[t] = 0;
+    }
+    int j0 = 0;
+    int i0 = i;
+    for (;;) {
+      const int col = hrows[i0 - 1];
+      const double ui0 = u[i0];
+      const float* crow = cost + (int64_t)col * ldq;
+      double lmin = INFINITY;
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) {
+        const int j = 1 + lane + 64 * t;
+        if (j <= n && !((used >> t) & 1u)) {
+          const double raw = (double)crow[predj[t]];
+          const double cij = cost_ok(raw, thr) ? raw : BIG;
+          const double cur = cij - ui0 - v[t];
+          if (cur < minv[t]) {
+            minv[t] = cur;
+            wy[t] = j0;
+          }
+          lmin = fmin(lmin, minv[t]);
+        }
+      }
+      const double delta = wave_min_d(lmin);
+      if (!isfinite(delta)) {
+        ok = false;
+        break;
+      }
+      int j1 = 0;
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) {
+        if (j1 == 0) {
+          const int j = 1 + lane + 64 * t;
+          const bool hit = j <= n && !((used >> t) & 1u) && minv[t] == delta;
+          const uint64_t m = __ballot(hit);
+          if (m) j1 = 1 + (__ffsll((unsigned long long)m) - 1) + 64 * t;
+        }
+      }
+      if (j1 == 0) {  // unreachable with finite costs; keeps the walk below bounded
+        ok = false;
+        break;
+      }
+      // potentials: used columns (and column 0 -> current row i), others' minv
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) {
+        const int j = 1 + lane + 64 * t;
+        if (j <= n) {
+          if ((used >> t) & 1u) {
+            u[pj[t]] += delta;
+            v[t] -= delta;
+          } else {
+            minv[t] -= delta;
+          }
+        }
+      }
+      if (lane == 0) u[i] += delta;
+      // mark j1 used
+      const int o_lane = (j1 - 1) & 63, o_t = (j1 - 1) >> 6;
+      if (lane == o_lane) used |= 1u << o_t;
+      j0 = j1;
+      wave_sync();
+      const int pj0 = p[j0];
+      if (pj0 == 0) break;
+      i0 = pj0;
+    }
+    if (!ok) break;
+    // augment along way[]
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      const int j = 1 + lane + 64 * t;
+      if (j <= n) way[j] = wy[t];
+    }
+    wave_sync();
+    if (lane == 0) {
+      p[0] = i;
+      way[0] = 0;
+      int jj = j0;
+      int steps = 0;
+      do {
+        const int j1 = way[jj];
+        p[jj] = p[j1];
+        jj = j1;
+      } while (jj != 0 && ++steps <= n);
+    }
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      const int j = 1 + lane + 64 * t;
+      pj[t] = j <= n ? p[j] : 0;
+    }
+  }
+  if (ok) {
+    for (int j = 1 + lane; j <= n; j += 64)
+      if (p[j] > 0) asg[j - 1] = p[j] - 1;
+  }
+  wave_sync();
+  return ok;
+}
+
+// Greedy over preds[0..n) with per-column capacities (src/cpu/matching.cpp:193-229).
+// Column order = vcols[0..nv); ties -> earlier column (strict '<').
+__device__ void greedy_wave(const float* cost, int64_t ldq, const int* preds, int n,
+                            const int* vcols, int nv, int* cap, int* p2g, double thr) {
+  const int lane = threadIdx.x & 63;
+  for (int k = 0; k < n; ++k) {
+    const int q = preds[k];
+    if (p2g[q] >= 0) continue;
+    double best = INFINITY;
+    int bidx = 1 << 30;
+    for (int t = lane; t < nv; t += 64) {
+      const int c = vcols[t];
+      if (cap[c] <= 0) continue;
+      const double cv = (double)cost[(int64_t)c * ldq + q];
+      if (!cost_ok(cv, thr)) continue;
+      if (cv < best) {
+        best = cv;
+        bidx = t;
+      }
+    }
+    const double m = wave_min_d(best);
+    int pick = -1;
+    if (m < INFINITY) {
+      const uint64_t hit = __ballot(best == m);
+      // lowest column index t among lanes attaining m
+      int cand = best == m ? bidx : (1 << 30);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
+      (void)hit;
+      pick = vcols[cand];
+    }
+    if (lane == 0 && pick >= 0) {
+      p2g[q] = pick;
+      if (cap[pick] > 0) cap[pick] -= 1;
+    }
+    wave_sync();
+  }
+}
+
+template <int NJ>
+__global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const SmemLayout L = smem_layout(a.Q, a.GT_out, a.cost_in_lds != 0);
+  float* rowS = (float*)(smem + L.rowS);
+  float* rowP = (float*)(smem + L.rowP);
+  float* clsA = (float*)(smem + L.clsA);
+  float* clsPen = (float*)(smem + L.clsPen);
+  float* mPen = (float*)(smem + L.mPen);
+  float* dPen = (float*)(smem + L.dPen);
+  float* contrib = (float*)(smem + L.contrib);
+  int* colok = (int*)(smem + L.colok);
+  int* vcols = (int*)(smem + L.vcols);
+  int* preds = (int*)(smem + L.preds);
+  int* pp = (int*)(smem + L.p);
+  int* way = (int*)(smem + L.way);
+  double* u = (double*)(smem + L.u);
+  int* hrows = (int*)(smem + L.hrows);
+  int* asg = (int*)(smem + L.asg);
+
+  const int64_t lb = blockIdx.x, l = lb / a.B, b = lb % a.B;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t Q = a.Q, GTo = a.GT_out, C = a.C;
+  float* costL = a.cost_in_lds ? (float*)(smem + L.costL) : a.costT + lb * GTo * Q;
+  const int G = a.ncols[b];
+
+  // ---- 1. per-query statistics
+  const int64_t void_idx = a.void_idx;
+  const bool has_void = void_idx >= 0;
+  const bool need_cls_pen = a.force_cls || has_void;
+  const bool softmax_bg = a.use_softmax && a.force_cls && has_void;
+  for (int64_t q = wave; q < Q; q += 4) {
+    // S, P from the ones column (slot G)
+    if (lane == 0) {
+      const int64_t rt = q / a.rows, row = q % a.rows;
+      float P = 0.f, S = 0.f;
+      for (int64_t ks = 0; ks < a.KS; ++ks) {
+        const float* Pp = a.partials +
+                          ((ks * (a.L * a.B) + lb) * a.rtiles + rt) * 3 * a.rows * a.nslot;
+        P += Pp[(1 * a.rows + row) * a.nslot + G];
+        S += Pp[(2 * a.rows + row) * a.nslot + G];
+      }
+      if (!a.normalize) S = (float)(a.Ht * a.Wt);
+      rowS[q] = fmaxf(S, kEps);
+      rowP[q] = P;
+      float mp = 0.f, dp = 0.f;
+      if (a.force_masks) {
+        float ub = 0.f, up = 0.f;
+        for (int64_t ks = 0; ks < a.KS; ++ks) {
+          const float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
+          ub += rs[0];
+          up += rs[1];
+        }
+        const float bce_mean = ub / (float)a.HW;
+        const float psum = up * a.N2;
+        mp = a.sigmoid_scale * bce_mean;
+        dp = a.dice_scale * (psum / (psum + a.smooth));
+      }
+      mPen[q] = mp;
+      dPen[q] = dp;
+    }
+    // label row terms
+    const int64_t zb = (lb * Q + q) * C;
+    if (a.use_softmax) {
+      float m = -INFINITY;
+      for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_elem(a.cls_logits, a.cls_dtype, zb + c));
+      m = wave_max(m);
+      float se = 0.f;
+      for (int64_t c = lane; c < C; c += 64)
+        se += __expf(cls_elem(a.cls_logits, a.cls_dtype, zb + c) - m);
+      se = wave_sum(se);
+      const float lse = __logf(fmaxf(se, 1e-20f)) + m;
+      if (lane == 0) clsA[q] = lse;
+      float pen = 0.f;
+      if (need_cls_pen) {
+        const float zv = cls_elem(a.cls_logits, a.cls_dtype, zb + void_idx);
+        if (softmax_bg) {
+          pen = (lse - zv) * a.cls_scale;
+        } else {
+          // softmax label loss, void channel only: sigmoid BCE towards void
+          // (mask_matching_forward.cu:213-218 with unit focal terms)
+          const Sig s = sig_terms(zv);
+          pen = s.cp * a.cls_scale;
+        }
+      }
+      if (lane == 0) clsPen[q] = pen;
+    } else {
+      float base = 0.f, vpos = 0.f, vneg = 0.f;
+      for (int64_t c = lane; c < C; c += 64) {
+        const ClsTerm t = cls_terms(cls_elem(a.cls_logits, a.cls_dtype, zb + c), a.cls_ep);
+        base += t.neg;
+        if (c == void_idx) {
+          vpos = t.pos;
+          vneg = t.neg;
+        }
+      }
+      base = wave_sum(base);
+      vpos = wave_sum(vpos);
+      vneg = wave_sum(vneg);
+      if (lane == 0) {
+        clsA[q] = base;
+        float pen = 0.f;
+        if (a.force_cls) {
+          const float invC = C > 0 ? 1.f / (float)C : 0.f;
+          pen = base * invC;
+          if (has_void && C > 0) pen += (vpos - vneg) * invC;
+        } else if (has_void) {
+          pen = vpos;
+        }
+        clsPen[q] = pen * a.cls_scale;
+      }
+    }
+  }
+  for (int64_t c = tid; c <= GTo; c += 256) colok[c] = 0;
+  __syncthreads();
+
+  Ctx x;
+  x.a = &a;
+  x.lb = lb;
+  x.l = l;
+  x.b = b;
+  x.G = G;
+  x.rowS = rowS;
+  x.rowP = rowP;
+  x.clsA = clsA;
+
+  // ---- 2. all (q, c) costs
+  const int64_t term = a.L * a.B * Q * GTo;
+  for (int64_t i = tid; i < Q * GTo; i += 256) {
+    const int64_t q = i / GTo, c = i % GTo;
+    float bce, dice, cls;
+    pair_costs(x, q, c, bce, dice, cls);
+    if (a.sep) {
+      const int64_t o = (lb * Q + q) * GTo + c;
+      a.sep[o] = bce;
+      a.sep[term + o] = dice;
+      a.sep[2 * term + o] = cls;
+    }
+    const float tot = (bce + dice) + cls;
+    costL[c * Q + q] = tot;
+    if (cost_ok((double)tot, a.inf_thresh)) colok[c] = 1;  // benign race: all writers store 1
+  }
+  if (a.costs_only) return;
+  __syncthreads();
+  if (!a.cost_in_lds) __threadfence_block();
+
+  // ---- 3. assignment on wave 0
+  if (wave == 0) {
+    int nv = 0;
+    for (int64_t c0 = 0; c0 < GTo; c0 += 64) {
+      const int64_t c = c0 + lane;
+      const bool okc = c < GTo && colok[c];
+      const uint64_t m = __ballot(okc);
+      if (okc) vcols[nv + __popcll(m & ((1ull << lane) - 1ull))] = (int)c;
+      nv += __popcll(m);
+    }
+    int* p2g = asg;  // reuse: per-query result (-1 / column), separate from Hungarian asg below
+    // asg doubles as p2g scratch: Hungarian results go to hasg (preds area reused after)
+    for (int64_t q = lane; q < Q; q += 64) p2g[q] = -1;
+    wave_sync();
+    const double thr = a.inf_thresh, BIG = a.big;
+    const int64_t K = a.topk;
+    bool okh = true;
+    int* hasg = way;  // assignment output of one Hungarian call (length n) lives after way? no:
+    (void)hasg;
+    // scratch for one Hungarian call's output: reuse `contrib` (Q*4 floats >= Q ints)
+    int* hout = (int*)contrib;
+    if (Q > 0 && GTo > 0 && K > 0 && nv > 0) {
+      if (a.strategy == ML_GLOBAL || a.strategy == ML_PSEUDO_GREEDY) {
+        int M = 0;
+        if (a.strategy == ML_GLOBAL) {
+          for (int64_t rep = 0; rep < K && M < Q; ++rep)
+            for (int t = 0; t < nv && M < Q; ++t) {
+              if (lane == 0) hrows[M] = vcols[t];
+              ++M;
+            }
+        } else {
+          for (int t = 0; t < nv && M < Q; ++t) {
+            if (lane == 0) hrows[M] = vcols[t];
+            ++M;
+          }
+        }
+        for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
+        wave_sync();
+        okh = hungarian_wave<NJ>(costL, Q, preds, (int)Q, hrows, M, thr, BIG, pp, way, u, hout);
+        // cap reuses vcols tail? capacities live in colok (GTo ints) from here on
+        int* cap = colok;
+        for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
+        wave_sync();
+        for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
+        wave_sync();
+        if (okh) {
+          for (int64_t q = lane; q < Q; q += 64) {
+            const int r = hout[q];
+            if (r >= 0) {
+              const int c = hrows[r];
+              if (cost_ok((double)costL[c * Q + q], thr)) p2g[q] = c;
+            }
+          }
+          wave_sync();
+          if (a.strategy == ML_PSEUDO_GREEDY) {
+            if (lane == 0)
+              for (int64_t q = 0; q < Q; ++q)
+                if (p2g[q] >= 0 && cap[p2g[q]] > 0) cap[p2g[q]] -= 1;
+            wave_sync();
+            int nr = 0;
+            for (int64_t q0 = 0; q0 < Q; q0 += 64) {
+              const int64_t q = q0 + lane;
+              const bool un = q < Q && p2g[q] < 0;
+              const uint64_t m = __ballot(un);
+              if (un) preds[nr + __popcll(m & ((1ull << lane) - 1ull))] = (int)q;
+              nr += __popcll(m);
+            }
+            wave_sync();
+            if (nr > 0) greedy_wave(costL, Q, preds, nr, vcols, nv, cap, p2g, thr);
+          }
+        }
+      } else if (a.strategy == ML_ROUND) {
+        int* cap = colok;
+        for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
+        wave_sync();
+        for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
+        for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
+        wave_sync();
+        int nrem = (int)Q;
+        for (int64_t rd = 0; rd < K && okh; ++rd) {
+          int M = 0;
+          for (int t = 0; t < nv; ++t)
+            if (cap[vcols[t]] > 0) {
+              if (lane == 0) hrows[M] = vcols[t];
+              ++M;
+            }
+          if (M == 0 || nrem == 0) break;
+          if (M > nrem) M = nrem;
+          wave_sync();
+          okh = hungarian_wave<NJ>(costL, Q, preds, nrem, hrows, M, thr, BIG, pp, way, u, hout);
+          if (!okh) break;
+          // apply in pred order, compact the remaining preds (order preserved)
+          int nn = 0;
+          for (int k0 = 0; k0 < nrem; k0 += 64) {
+            const int k = k0 + lane;
+            bool keep = false;
+            int q = -1;
+            if (k < nrem) {
+              q = preds[k];
+              const int r = hout[k];
+              if (r >= 0) {
+                const int c = hrows[r];
+                if (!cost_ok((double)costL[c * Q + q], thr)) keep = true;
+                else p2g[q] = c;
+              } else {
+                keep = true;
+              }
+            }
+            const uint64_t m = __ballot(keep);
+            // write compacted into hout tail-safe region: use way[] as temp
+            if (keep) way[nn + __popcll(m & ((1ull << lane) - 1ull))] = q;
+            nn += __popcll(m);
+          }
+          wave_sync();
+          if (lane == 0)
+            for (int k = 0; k < nrem; ++k) {
+              const int q = preds[k];
+              const int c = p2g[q];
+              if (c >= 0 && hout[k] >= 0 && hrows[hout[k]] == c && cap[c] > 0) cap[c] -= 1;
+            }
+          wave_sync();
+          for (int k = lane; k < nn; k += 64) preds[k] = way[k];
+          nrem = nn;
+          wave_sync();
+          if (nrem == 0) break;
+        }
+      } else if (a.strategy == ML_GREEDY) {
+        int* cap = colok;
+        for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
+        wave_sync();
+        for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
+        for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
+        wave_sync();
+        greedy_wave(costL, Q, preds, (int)Q, vcols, nv, cap, p2g, thr);
+      }
+    }
+    if (!okh) {
+      if (lane == 0) atomicOr(a.err, 1);
+      for (int64_t q = lane; q < Q; q += 64) p2g[q] = -1;
+    }
+    // drop invalid, rank by (cost, q) within each column (matching.cpp:533-565)
+    for (int64_t q = lane; q < Q; q += 64) {
+      const int c = p2g[q];
+      if (c >= 0 && !cost_ok((double)costL[c * Q + q], thr)) p2g[q] = -1;
+    }
+    wave_sync();
+    for (int64_t q = lane; q < Q; q += 64) {
+      const int c = p2g[q];
+      int64_t rnd = -1;
+      if (c >= 0) {
+        const float cq = costL[c * Q + q];
+        int64_t rank = 0;
+        for (int64_t q2 = 0; q2 < Q; ++q2) {
+          if (q2 == q || p2g[q2] != c) continue;
+          const float c2 = costL[c * Q + q2];
+          if (c2 < cq || (c2 == cq && q2 < q)) ++rank;
+        }
+        rnd = rank < K ? rank : -1;
+      }
+      a.pred_to_gt[lb * Q + q] = c;
+      a.pred_round[lb * Q + q] = rnd;
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. matched-loss partial sums and backward statistics
+  const int* p2g = asg;
+  for (int64_t q = tid; q < Q; q += 256) {
+    const int c = p2g[q];
+    float cm = 0.f, cd = 0.f, cc = 0.f, I = 0.f, T = 0.f;
+    if (c >= 0) {
+      float bce, dice, cls;
+      pair_costs(x, q, c, bce, dice, cls);
+      cm = bce;
+      cd = dice;
+      cc = cls;
+      const int slot = a.slot_of_col[b * GTo + c];
+      if (slot >= 0) {
+        const int64_t rt = q / a.rows, row = q % a.rows;
+        for (int64_t ks = 0; ks < a.KS; ++ks) {
+          const float* Pp = a.partials +
+                            ((ks * (a.L * a.B) + lb) * a.rtiles + rt) * 3 * a.rows * a.nslot;
+          I += Pp[(1 * a.rows + row) * a.nslot + slot];
+          T += Pp[(2 * a.rows + row) * a.nslot + slot];
+        }
+      }
+    } else {
+      if (a.force_masks) {
+        cm = mPen[q];
+        cd = dPen[q];
+      }
+      if (need_cls_pen) cc = clsPen[q];
+    }
+    contrib[q * 4 + 0] = cm;
+    contrib[q * 4 + 1] = cd;
+    contrib[q * 4 + 2] = cc;
+    contrib[q * 4 + 3] = c >= 0 ? 1.f : 0.f;
+    if (a.stats) {
+      float* st = a.stats + (lb * Q + q) * ML_STATS;
+      st[ML_STAT_S] = rowS[q];
+      st[ML_STAT_P] = rowP[q];
+      st[ML_STAT_I] = I;
+      st[ML_STAT_T] = T;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    for (int64_t q = lane; q < Q; q += 64) {
+      s0 += contrib[q * 4 + 0];
+      s1 += contrib[q * 4 + 1];
+      s2 += contrib[q * 4 + 2];
+      s3 += contrib[q * 4 + 3];
+    }
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    s3 = wave_sum(s3);
+    if (lane == 0) {
+      a.img[lb * 4 + 0] = s0;
+      a.img[lb * 4 + 1] = s1;
+      a.img[lb * 4 + 2] = s2;
+      a.img[lb * 4 + 3] = s3;
+    }
+  }
+}
+
+// Per-layer means and denominators (src/cuda/mask_matching_forward.cu:549-583).
+__global__ void layer_kernel(LayerArgs a) {
+  const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (l >= a.L) return;
+  float m = 0.f, d = 0.f, c = 0.f, cnt = 0.f;
+  for (int64_t b = 0; b < a.B; ++b) {
+    const float* s = a.img + (l * a.B + b) * 4;
+    m += s[0];
+    d += s[1];
+    c += s[2];
+    cnt += s[3];
+  }
+  const float total = (float)(a.B * a.Q);
+  const bool has_nm = a.num_masks > 0.0;
+  float md = a.force_masks ? total : (has_nm ? (float)a.num_masks : cnt);
+  float cd = (a.force_cls || a.has_void) ? total : (has_nm ? (float)a.num_masks : cnt);
+  md = fmaxf(md, 1.f);
+  cd = fmaxf(cd, 1.f);
+  a.means[0 * a.L + l] = m / md;
+  a.means[1 * a.L + l] = d / md;
+  a.means[2 * a.L + l] = c / cd;
+  a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN] = 1.f / md;
+  a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / cd;
+}
+
+// Denominators from pred_to_gt alone (backward without saved statistics,
+// src/cuda/mask_matching_backward.cu:480-508).  One wave per layer.
+__global__ void layer_from_p2g_kernel(const int64_t* p2g, float* layer, int64_t L, int64_t B,
+                                      int64_t Q, double num_masks, int force_masks,
+                                      int force_cls, int has_void) {
+  const int64_t l = blockIdx.x;
+  const int lane = threadIdx.x;
+  float cnt = 0.f;
+  for (int64_t i = lane; i < B * Q; i += 64) cnt += p2g[l * B * Q + i] >= 0 ? 1.f : 0.f;
+  cnt = wave_sum(cnt);
+  if (lane == 0) {
+    const float total = (float)(B * Q);
+    const bool has_nm = num_masks > 0.0;
+    float md = force_masks ? total : (has_nm ? (float)num_masks : cnt);
+    float cd = (force_cls || has_void) ? total : (has_nm ? (float)num_masks : cnt);
+    layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN] = 1.f / fmaxf(md, 1.f);
+    layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / fmaxf(cd, 1.f);
+  }
+}
+
+size_t assign_smem_bytes(int64_t Q, int64_t GTo, bool cost_in_lds) {
+  return smem_layout(Q, GTo, cost_in_lds).total;
+}
+
+template <int NJ>
+static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
+  const size_t sm = smem_layout(a.Q, a.GT_out, a.cost_in_lds != 0).total;
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute((const void*)assign_kernel<NJ>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             160 * 1024);
+    if (e != hipSuccess) return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
+    attr_set = true;
+  }
+  {
+    ProfScope ps_("assign", st);
+    hipLaunchKernelGGL(assign_kernel<NJ>, dim3((unsigned)d.LB), dim3(256), sm, st, a);
+  }
+  return check_launch("assign");
+}
+
+int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
+  const int64_t nj = ceil_div(a.Q, 64);
+  if (nj <= 1) return launch_nj<1>(a, d, st);
+  if (nj <= 2) return launch_nj<2>(a, d, st);
+  if (nj <= 4) return launch_nj<4>(a, d, st);
+  if (nj <= 8) return launch_nj<8>(a, d, st);
+  if (nj <= 16) return launch_nj<16>(a, d, st);
+  return fail(ML_EUNSUPPORTED, "more than 1024 queries per image are not supported");
+}
+
+int launch_layer(const LayerArgs& a, hipStream_t st) {
+  {
+    ProfScope ps_("layer", st);
+    hipLaunchKernelGGL(layer_kernel, dim3((unsigned)ceil_div(a.L, 64)), dim3(64), 0, st, a);
+  }
+  return check_launch("layer");
+}
+
+int launch_layer_from_p2g(const int64_t* p2g, float* layer, int64_t L, int64_t B, int64_t Q,
+                          double num_masks, int force_masks, int force_cls, int has_void,
+                          hipStream_t st) {
+  hipLaunchKernelGGL(layer_from_p2g_kernel, dim3((unsigned)L), dim3(64), 0, st, p2g, layer, L, B,
+                     Q, num_masks, force_masks, force_cls, has_void);
+  return check_launch("layer_from_p2g");
+}
+
+}  // namespace ml

@@ -1,0 +1,516 @@
+// C ABI entry points (declared in include/mask_loss_hip.h): argument
+// validation mirroring the reference's checks, workspace layout and the
+// launch sequence of each operator.  Host code only; all work is enqueued on
+// the caller's stream.
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "ml_internal.h"
+
+namespace ml {
+
+static thread_local std::string g_err;
+
+void set_error(const std::string& msg) { g_err = msg; }
+int fail(int code, const std::string& msg) {
+  set_error(msg);
+  return code;
+}
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(ML_ELAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+  return ML_OK;
+}
+
+size_t assign_smem_bytes(int64_t Q, int64_t GTo, bool cost_in_lds);
+
+// ---- instrumentation ----------------------------------------------------------
+namespace {
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<hipEvent_t> g_pool;
+std::vector<ProfRec> g_recs;
+std::vector<std::pair<const char*, hipEvent_t>> g_open;
+
+hipEvent_t take_event() {
+  if (g_pool.empty()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+  hipEvent_t e = g_pool.back();
+  g_pool.pop_back();
+  return e;
+}
+}  // namespace
+
+void prof_begin(const char* name, hipStream_t st) {
+  if (!g_prof_on) return;
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  hipEvent_t e = take_event();
+  if (!e) return;
+  (void)hipEventRecord(e, st);
+  g_open.push_back({name, e});
+}
+
+void prof_end(const char* name, hipStream_t st) {
+  if (!g_prof_on) return;
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  for (size_t i = g_open.size(); i-- > 0;) {
+    if (strcmp(g_open[i].first, name) == 0) {
+      hipEvent_t e = take_event();
+      if (!e) return;
+      (void)hipEventRecord(e, st);
+      g_recs.push_back({name, g_open[i].second, e});
+      g_open.erase(g_open.begin() + (long)i);
+      return;
+    }
+  }
+}
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
+               std::string& err) {
+  d.L = s->L; d.B = s->B; d.Q = s->Q; d.H = s->H; d.W = s->W;
+  d.Ht = s->Ht; d.Wt = s->Wt; d.C = s->C; d.GT_total = s->GT_total;
+  if (d.L < 0 || d.B < 0 || d.Q < 0 || d.C < 0 || d.GT_total < 0) {
+    err = "negative dimension";
+    return false;
+  }
+  if (d.H <= 0 || d.W <= 0) {
+    err = "mask_logits must have positive spatial size";
+    return false;
+  }
+  if (d.Ht % d.H != 0 || d.Wt % d.W != 0 || d.Ht / d.H != d.Wt / d.W || d.Ht == 0) {
+    err = "Target resolution must be the same integer multiple of the mask_logits resolution in both dimensions";
+    return false;
+  }
+  d.s = d.Ht / d.H;
+  if (d.s > 15) {
+    err = "target/logit scale factor above 15 overflows the per-cell uint8 counts";
+    return false;
+  }
+  if (d.GT_total > 65535) {
+    err = "at most 65535 GT slots per image are supported";
+    return false;
+  }
+  d.N2 = d.s * d.s;
+  d.LB = d.L * d.B;
+  d.HW = d.H * d.W;
+  const bool skip = background_index >= 0 && background_index < d.GT_total;
+  d.bg = background_index >= 0 ? background_index : d.GT_total;
+  d.GT_out = d.GT_total - (skip ? 1 : 0);
+  d.HWp = ceil_div(d.HW, kStep) * kStep;
+  const int64_t need = ceil_div(d.GT_out + 1, 16);  // + ones column
+  if (need <= 2) d.NT = 2;
+  else if (need <= 4) d.NT = 4;
+  else if (need <= 7) d.NT = 7;
+  else if (need <= 16) d.NT = 16;
+  else {
+    err = "more than 255 GT columns per image are not supported";
+    return false;
+  }
+  d.RT = cost_rt_for(dtype, d.NT);
+  d.rows = 16 * d.RT;
+  d.nslot = 16 * d.NT;
+  d.rtiles = ceil_div(d.Q, d.rows);
+  const int64_t nsteps = ceil_div(d.HW, kStep);
+  const int64_t per_ks = d.rtiles * d.LB * kWavesCost;
+  int64_t ks = per_ks > 0 ? ceil_div(2048, per_ks) : 1;
+  const int64_t ks_max = nsteps / (kWavesCost * 8) > 1 ? nsteps / (kWavesCost * 8) : 1;
+  if (ks > ks_max) ks = ks_max;
+  if (ks < 1) ks = 1;
+  d.KS = ks;
+  d.counts_mode = d.s > 1;
+  return true;
+}
+
+Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
+  Layout L;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t r = o;
+    o = align256(o + bytes);
+    return r;
+  };
+  L.lab16 = take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2);
+  L.counts8 = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0);
+  L.area = take((size_t)d.B * d.GT_total * 4);
+  L.ncols = take((size_t)d.B * 4);
+  L.colmap = take((size_t)d.B * d.nslot * 4);
+  L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
+  L.partials = take((size_t)d.KS * d.LB * d.rtiles * 3 * d.rows * d.nslot * 4);
+  const int64_t Qp = d.rtiles * d.rows;
+  L.rowsum = take(force_masks ? (size_t)d.KS * d.LB * Qp * 2 * 4 : 0);
+  L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
+  L.img = take((size_t)d.LB * 4 * 4);
+  L.layer = take((size_t)d.L * ML_LAYERS * 4);
+  L.err = take(16);
+  L.total = o;
+  return L;
+}
+
+static bool cost_fits_lds(const Dims& d) {
+  return assign_smem_bytes(d.Q, d.GT_out, true) <= kMaxLds;
+}
+
+static int check_focal(float gamma, float alpha, const char* who) {
+  if (!(gamma >= 0.f)) return fail(ML_EINVAL, std::string(who) + " focal_gamma must be non-negative");
+  if (!(alpha < 0.f || (alpha >= 0.f && alpha <= 1.f)))
+    return fail(ML_EINVAL, std::string(who) + " focal_alpha must be in [0, 1] or negative to disable");
+  return ML_OK;
+}
+
+static int check_params(const ml_params* p, int64_t C, bool matching) {
+  int rc;
+  if ((rc = check_focal(p->mask_gamma, p->mask_alpha, "mask"))) return rc;
+  if ((rc = check_focal(p->cls_gamma, p->cls_alpha, "cls"))) return rc;
+  if (matching) {
+    if (p->topk_matches < 0) return fail(ML_EINVAL, "K must be non-negative");
+    if (p->strategy_id < 0 || p->strategy_id > 3) return fail(ML_EINVAL, "Invalid matching strategy id");
+    if (!(p->uncertainty_gamma >= 0.f))
+      return fail(ML_EINVAL, "uncertainty_gamma must be non-negative");
+    if (!(p->uncertainty_gamma_min >= 0.f && p->uncertainty_gamma_min <= 1.f))
+      return fail(ML_EINVAL, "uncertainty_gamma_min must be in [0,1]");
+    if (p->use_softmax_label_loss && p->force_unmatched_class_to_background &&
+        !(p->void_class_index >= 0 && p->void_class_index < C))
+      return fail(ML_EINVAL,
+                  "void_class_index must be provided when using softmax label loss and forcing "
+                  "unmatched class logits");
+  }
+  return ML_OK;
+}
+
+static bool dtype_ok(int dt) { return dt == ML_F32 || dt == ML_BF16 || dt == ML_F16; }
+
+// Shared forward: prep -> cost -> assign (-> layer).
+static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
+                        const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
+                        const void* cls_logits, const int64_t* cls_targets, int64_t* pred_to_gt,
+                        int64_t* pred_round, float* layer_means, float* sep, float* stats,
+                        void* ws, size_t ws_bytes, hipStream_t st, bool costs_only) {
+  if (!dtype_ok(mask_dtype) || !dtype_ok(cls_dtype)) return fail(ML_EINVAL, "unsupported dtype");
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
+  const bool force_masks = !costs_only && p->force_unmatched_masks_to_empty;
+  const bool in_lds = cost_fits_lds(d);
+  const Layout L = make_layout(d, force_masks, !in_lds);
+  if (ws_bytes < L.total) return fail(ML_EWORKSPACE, "workspace too small");
+  unsigned char* w = (unsigned char*)ws;
+  int rc;
+  if ((rc = launch_fill_i32((int*)(w + L.err), 0, 4, st))) return rc;
+
+  PrepArgs pa;
+  pa.targets = mask_targets;
+  pa.lab16 = (uint16_t*)(w + L.lab16);
+  pa.counts8 = (uint8_t*)(w + L.counts8);
+  pa.area = (int*)(w + L.area);
+  pa.ncols = (int*)(w + L.ncols);
+  pa.colmap = (int*)(w + L.colmap);
+  pa.slot_of_col = (int*)(w + L.slot_of_col);
+  pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
+  pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
+  if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
+
+  const ElemParams mask_ep = make_elem_params(p->mask_gamma, p->mask_alpha,
+                                              p->uncertainty_gamma, p->uncertainty_gamma_min);
+  CostArgs ca;
+  ca.logits = mask_logits;
+  ca.lab16 = pa.lab16;
+  ca.counts8 = d.counts_mode ? pa.counts8 : nullptr;
+  ca.ncols = pa.ncols;
+  ca.colmap = pa.colmap;
+  ca.partials = (float*)(w + L.partials);
+  ca.rowsum = force_masks ? (float*)(w + L.rowsum) : nullptr;
+  ca.L = d.L; ca.B = d.B; ca.Q = d.Q; ca.HW = d.HW; ca.HWp = d.HWp; ca.KS = d.KS;
+  ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.Qp = d.rtiles * d.rows;
+  ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;
+  if (d.LB > 0 && d.rtiles > 0 && (rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
+
+  const bool use_softmax = p->use_softmax_label_loss != 0;
+  int64_t void_idx = (p->void_class_index >= 0 && p->void_class_index < d.C) ? p->void_class_index : -1;
+  AssignArgs aa;
+  aa.cls_logits = cls_logits;
+  aa.cls_dtype = cls_dtype;
+  aa.cls_targets = cls_targets;
+  aa.partials = ca.partials;
+  aa.rowsum = ca.rowsum;
+  aa.area = pa.area;
+  aa.ncols = pa.ncols;
+  aa.slot_of_col = pa.slot_of_col;
+  aa.sep = sep;
+  aa.costT = in_lds ? nullptr : (float*)(w + L.costT);
+  aa.pred_to_gt = pred_to_gt;
+  aa.pred_round = pred_round;
+  aa.stats = stats;
+  aa.img = (float*)(w + L.img);
+  aa.err = (int*)(w + L.err);
+  aa.L = d.L; aa.B = d.B; aa.Q = d.Q; aa.C = d.C; aa.HW = d.HW; aa.Ht = d.Ht; aa.Wt = d.Wt;
+  aa.GT_total = d.GT_total; aa.GT_out = d.GT_out; aa.bg = d.bg; aa.KS = d.KS; aa.rtiles = d.rtiles;
+  aa.Qp = d.rtiles * d.rows; aa.rows = d.rows; aa.nslot = d.nslot; aa.N2 = (float)d.N2;
+  aa.smooth = p->smooth; aa.sigmoid_scale = p->sigmoid_scale; aa.dice_scale = p->dice_scale;
+  aa.cls_scale = p->cls_scale;
+  aa.normalize = p->normalize_uncertainty != 0;
+  aa.use_softmax = use_softmax;
+  aa.force_cls = !costs_only && p->force_unmatched_class_to_background;
+  aa.force_masks = force_masks;
+  aa.void_idx = costs_only ? -1 : void_idx;
+  aa.cls_gamma = p->cls_gamma;
+  aa.cls_alpha = p->cls_alpha;
+  // the label loss uses focal terms only in its sigmoid form
+  aa.cls_ep = use_softmax ? make_elem_params(0.f, -1.f, 0.f, 0.f)
+                          : make_elem_params(p->cls_gamma, p->cls_alpha, 0.f, 0.f);
+  aa.mask_ep = mask_ep;
+  aa.inf_thresh = p->inf_thresh;
+  {
+    const double x = p->inf_thresh;  // big_from, src/cpu/matching.cpp:71-83
+    double big;
+    if (!(x == x) || x == INFINITY || x == -INFINITY || x <= 0.0) big = 1e15;
+    else {
+      big = x * 0.5;
+      if (big == INFINITY || big < 1e6) big = 1e15;
+      if (big > 1e290) big = 1e290;
+    }
+    aa.big = big;
+  }
+  aa.topk = p->topk_matches;
+  aa.strategy = (int)p->strategy_id;
+  aa.costs_only = costs_only;
+  aa.cost_in_lds = in_lds;
+  if (d.LB > 0 && (rc = launch_assign(aa, d, st))) return rc;
+  if (costs_only) return ML_OK;
+
+  LayerArgs la;
+  la.img = aa.img;
+  la.layer = stats ? stats + d.LB * d.Q * ML_STATS : (float*)(w + L.layer);
+  la.means = layer_means;
+  la.L = d.L; la.B = d.B; la.Q = d.Q;
+  la.num_masks = p->num_masks;
+  la.force_masks = force_masks;
+  la.force_cls = p->force_unmatched_class_to_background;
+  la.has_void = void_idx >= 0;
+  if (d.L > 0 && (rc = launch_layer(la, st))) return rc;
+  return ML_OK;
+}
+
+}  // namespace ml
+
+using namespace ml;
+
+extern "C" {
+
+const char* ml_last_error(void) { return g_err.c_str(); }
+
+int ml_profile_enable(int enable) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  if (enable && g_pool.size() < 512) {
+    for (int i = 0; i < 512; ++i) {
+      hipEvent_t e;
+      if (hipEventCreate(&e) != hipSuccess) return fail(ML_ELAUNCH, "hipEventCreate failed");
+      g_pool.push_back(e);
+    }
+  }
+  g_prof_on = enable != 0;
+  return ML_OK;
+}
+
+int ml_profile_reset(void) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  for (auto& r : g_recs) {
+    (void)hipEventSynchronize(r.b);
+    g_pool.push_back(r.a);
+    g_pool.push_back(r.b);
+  }
+  g_recs.clear();
+  return ML_OK;
+}
+
+int ml_profile_read(const char* name, int64_t* launches, double* total_ms) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  int64_t n = 0;
+  double t = 0.0;
+  for (auto& r : g_recs) {
+    if (strcmp(r.name, name) != 0) continue;
+    if (hipEventSynchronize(r.b) != hipSuccess) return fail(ML_ELAUNCH, "event sync failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return fail(ML_ELAUNCH, "elapsed failed");
+    ++n;
+    t += ms;
+  }
+  *launches = n;
+  *total_ms = t;
+  return ML_OK;
+}
+int ml_version(void) { return 1; }
+
+size_t ml_stats_floats(const ml_shape* s) {
+  return (size_t)(s->L * s->B * s->Q * ML_STATS + s->L * ML_LAYERS);
+}
+
+size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p, int mask_dtype) {
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  return make_layout(d, p->force_unmatched_masks_to_empty != 0, !cost_fits_lds(d)).total;
+}
+
+size_t ml_pairwise_mask_loss_workspace_size(const ml_shape* s, const ml_params* p,
+                                            int mask_dtype) {
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  return make_layout(d, false, !cost_fits_lds(d)).total;
+}
+
+int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
+                             const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
+                             const void* cls_logits, const int64_t* cls_targets,
+                             int64_t* pred_to_gt, int64_t* pred_round, float* layer_means,
+                             float* separate_costs, float* stats, void* workspace,
+                             size_t workspace_bytes, ml_stream_t stream) {
+  int rc = check_params(p, s->C, true);
+  if (rc) return rc;
+  return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
+                      cls_targets, pred_to_gt, pred_round, layer_means, separate_costs, stats,
+                      workspace, workspace_bytes, (hipStream_t)stream, false);
+}
+
+int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
+                                  const void* mask_logits, const int64_t* mask_targets,
+                                  int cls_dtype, const void* cls_logits,
+                                  const int64_t* cls_targets, float* separate_costs,
+                                  void* workspace, size_t workspace_bytes, ml_stream_t stream) {
+  int rc = check_params(p, s->C, false);
+  if (rc) return rc;
+  return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
+                      cls_targets, nullptr, nullptr, nullptr, separate_costs, nullptr, workspace,
+                      workspace_bytes, (hipStream_t)stream, true);
+}
+
+size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,
+                                                int mask_dtype) {
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  size_t o = 0;
+  o = align256(o + (d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
+  o = align256(o + (d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
+  o = align256(o + (size_t)d.B * d.GT_total * 4);  // area
+  o = align256(o + (size_t)d.B * 4);                // ncols
+  o = align256(o + (size_t)d.B * d.nslot * 4);      // colmap
+  o = align256(o + (size_t)d.B * d.GT_out * 4);     // slot_of_col
+  o = align256(o + (size_t)d.L * ML_LAYERS * 4);    // layer
+  return o;
+}
+
+int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float* grad_mask,
+                              const float* grad_dice, const float* grad_cls, int mask_dtype,
+                              const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
+                              const void* cls_logits, const int64_t* cls_targets,
+                              const int64_t* pred_to_gt, const float* stats,
+                              void* grad_mask_logits, void* grad_cls_logits, void* workspace,
+                              size_t workspace_bytes, ml_stream_t stream) {
+  int rc = check_params(p, s->C, true);
+  if (rc) return rc;
+  if (!dtype_ok(mask_dtype) || !dtype_ok(cls_dtype)) return fail(ML_EINVAL, "unsupported dtype");
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
+  if (workspace_bytes < ml_mask_matching_backward_workspace_size(s, p, mask_dtype))
+    return fail(ML_EWORKSPACE, "workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  unsigned char* w = (unsigned char*)workspace;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t r = o;
+    o = align256(o + bytes);
+    return r;
+  };
+  PrepArgs pa;
+  pa.lab16 = (uint16_t*)(w + take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
+  pa.counts8 = (uint8_t*)(w + take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
+  pa.area = (int*)(w + take((size_t)d.B * d.GT_total * 4));
+  pa.ncols = (int*)(w + take((size_t)d.B * 4));
+  pa.colmap = (int*)(w + take((size_t)d.B * d.nslot * 4));
+  pa.slot_of_col = (int*)(w + take((size_t)d.B * d.GT_out * 4));
+  float* layer_ws = (float*)(w + take((size_t)d.L * ML_LAYERS * 4));
+  pa.targets = mask_targets;
+  pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
+  pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
+  if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
+
+  const int64_t void_idx =
+      (p->void_class_index >= 0 && p->void_class_index < d.C) ? p->void_class_index : -1;
+  const float* layer;
+  if (stats) {
+    layer = stats + d.LB * d.Q * ML_STATS;
+  } else {
+    if (d.L > 0 &&
+        (rc = launch_layer_from_p2g(pred_to_gt, layer_ws, d.L, d.B, d.Q, p->num_masks,
+                                    p->force_unmatched_masks_to_empty,
+                                    p->force_unmatched_class_to_background, void_idx >= 0, st)))
+      return rc;
+    layer = layer_ws;
+  }
+  BwdArgs ba;
+  ba.logits = mask_logits;
+  ba.dtype = mask_dtype;
+  ba.lab16 = d.counts_mode ? nullptr : pa.lab16;
+  ba.counts8 = d.counts_mode ? pa.counts8 : nullptr;
+  ba.pred_to_gt = pred_to_gt;
+  ba.stats = stats;
+  ba.layer = layer;
+  ba.g_mask = grad_mask;
+  ba.g_dice = grad_dice;
+  ba.g_cls = grad_cls;
+  ba.grad = grad_mask_logits;
+  ba.cls_logits = cls_logits;
+  ba.cls_dtype = cls_dtype;
+  ba.cls_targets = cls_targets;
+  ba.grad_cls = grad_cls_logits;
+  ba.L = d.L; ba.B = d.B; ba.Q = d.Q; ba.HW = d.HW; ba.HWp = d.HWp; ba.C = d.C;
+  ba.GT_total = d.GT_total; ba.bg = d.bg; ba.Ht = d.Ht; ba.Wt = d.Wt; ba.N2 = (float)d.N2;
+  ba.smooth = p->smooth; ba.sigmoid_scale = p->sigmoid_scale; ba.dice_scale = p->dice_scale;
+  ba.cls_scale = p->cls_scale; ba.normalize = p->normalize_uncertainty != 0;
+  ba.force_masks = p->force_unmatched_masks_to_empty != 0;
+  ba.force_cls = p->force_unmatched_class_to_background != 0;
+  ba.use_softmax = p->use_softmax_label_loss != 0;
+  ba.void_idx = void_idx;
+  ba.mask_ep = make_elem_params(p->mask_gamma, p->mask_alpha, p->uncertainty_gamma,
+                                p->uncertainty_gamma_min);
+  ba.cls_ep = ba.use_softmax ? make_elem_params(0.f, -1.f, 0.f, 0.f)
+                             : make_elem_params(p->cls_gamma, p->cls_alpha, 0.f, 0.f);
+  ba.cls_gamma = ba.use_softmax ? 0.f : p->cls_gamma;
+  return launch_bwd(ba, d, st);
+}
+
+int ml_pairwise_label_loss_forward(int64_t L, int64_t B, int64_t Q, int64_t C, int64_t GT_total,
+                                   int cls_dtype, const void* cls_logits,
+                                   const int64_t* cls_targets, int64_t background_index,
+                                   float scale, float gamma, float alpha, int use_softmax,
+                                   float* out, ml_stream_t stream) {
+  if (!dtype_ok(cls_dtype)) return fail(ML_EINVAL, "unsupported dtype");
+  if (!use_softmax) {
+    int rc = check_focal(gamma, alpha, "label");
+    if (rc) return rc;
+  }
+  const bool skip = background_index >= 0 && background_index < GT_total;
+  const int64_t bg = background_index >= 0 ? background_index : GT_total;
+  const int64_t GT_out = GT_total - (skip ? 1 : 0);
+  const ElemParams ep = use_softmax ? make_elem_params(0.f, -1.f, 0.f, 0.f)
+                                    : make_elem_params(gamma, alpha, 0.f, 0.f);
+  return launch_label_cost(cls_logits, cls_dtype, cls_targets, L, B, Q, C, GT_total, GT_out, bg,
+                           scale, ep, use_softmax, out, (hipStream_t)stream);
+}
+
+}  // extern "C"

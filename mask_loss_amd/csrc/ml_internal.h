@@ -1,0 +1,173 @@
+// Host-side launch plumbing shared by the kernels' translation units:
+// workspace layout, kernel argument blocks, launcher declarations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "ml_common.h"
+
+namespace ml {
+
+// Set the thread-local error message returned by ml_last_error().
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+constexpr int kStep = 32;        // cells per MFMA K-step (16x16x32)
+constexpr int kWavesCost = 4;    // waves per cost workgroup
+
+// Derived sizes of one call.
+struct Dims {
+  int64_t L, B, Q, H, W, Ht, Wt, C, GT_total;
+  int64_t LB, HW, s, N2;
+  int64_t GT_out, bg;        // compacted column count, normalised background slot
+  int64_t HWp;               // HW padded to a multiple of kStep
+  int NT;                    // 16-wide column tiles (valid GT columns + ones column)
+  int RT;                    // 16-row tiles per wave
+  int rows;                  // rows per cost workgroup (16 * RT)
+  int64_t rtiles;            // row tiles per image
+  int64_t KS;                // K-splits across workgroups
+  int nslot;                 // 16 * NT
+  bool counts_mode;          // s > 1: per-cell count operands
+};
+
+bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d, std::string& err);
+int cost_rt_for(int dtype, int NT);
+
+// Byte offsets inside the caller's workspace.
+struct Layout {
+  size_t lab16, counts8, area, ncols, colmap, slot_of_col, partials, rowsum,
+      costT, img, layer, err, total;
+};
+Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
+
+// ---- kernel argument blocks ------------------------------------------------
+struct PrepArgs {
+  const int64_t* targets;
+  uint16_t* lab16;
+  uint8_t* counts8;
+  int* area;
+  int* ncols;
+  int* colmap;
+  int* slot_of_col;
+  int64_t B, H, W, Ht, Wt, s, HWp, GT_total, GT_out, bg;
+  int nslot;
+};
+
+struct CostArgs {
+  const void* logits;
+  const uint16_t* lab16;
+  const uint8_t* counts8;
+  const int* ncols;
+  const int* colmap;
+  float* partials;   // [KS][LB][rtiles][3][rows][nslot]
+  float* rowsum;     // [KS][LB][Qp][2] unweighted (force_masks) or null
+  int64_t L, B, Q, HW, HWp, KS, rtiles, GT_total, bg, Qp;
+  int nslot;
+  float N2;
+  ElemParams ep;
+};
+
+struct AssignArgs {
+  // inputs
+  const void* cls_logits;
+  int cls_dtype;
+  const int64_t* cls_targets;
+  const float* partials;
+  const float* rowsum;
+  const int* area;
+  const int* ncols;
+  const int* slot_of_col;
+  // outputs
+  float* sep;            // (3, L, B, Q, GT_out) or null
+  float* costT;          // [LB][GT_out][Q] transposed total cost (global fallback)
+  int64_t* pred_to_gt;   // (L,B,Q) or null (costs-only mode)
+  int64_t* pred_round;
+  float* stats;          // (L,B,Q,ML_STATS) or null
+  float* img;            // [LB][4]: mask, dice, cls sums, matched count
+  int* err;
+  // dims / params
+  int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, KS, rtiles, Qp;
+  int rows, nslot;
+  float N2;
+  float smooth, sigmoid_scale, dice_scale, cls_scale;
+  int normalize, use_softmax, force_cls, force_masks;
+  int64_t void_idx;
+  float cls_gamma, cls_alpha;
+  ElemParams cls_ep;
+  ElemParams mask_ep;
+  double inf_thresh, big;
+  int64_t topk;
+  int strategy;
+  int costs_only;
+  int cost_in_lds;
+};
+
+struct LayerArgs {
+  const float* img;
+  float* layer;        // [L][ML_LAYERS]
+  float* means;        // (3, L)
+  int64_t L, B, Q;
+  double num_masks;
+  int force_masks, force_cls, has_void;
+};
+
+struct BwdArgs {
+  const void* logits;
+  int dtype;
+  const uint16_t* lab16;
+  const uint8_t* counts8;
+  const int64_t* pred_to_gt;
+  const float* stats;     // per-query stats or null
+  const float* layer;     // [L][ML_LAYERS]
+  const float* g_mask;
+  const float* g_dice;
+  const float* g_cls;
+  void* grad;             // (L,B,Q,HW) in dtype
+  const void* cls_logits;
+  int cls_dtype;
+  const int64_t* cls_targets;
+  void* grad_cls;
+  int64_t L, B, Q, HW, HWp, C, GT_total, bg, Ht, Wt;
+  float N2;
+  float smooth, sigmoid_scale, dice_scale, cls_scale;
+  int normalize, force_masks, force_cls, use_softmax;
+  int64_t void_idx;
+  ElemParams mask_ep;
+  ElemParams cls_ep;
+  float cls_gamma;
+};
+
+// ---- instrumentation: bracket a launch with events when profiling is on ------
+void prof_begin(const char* name, hipStream_t st);
+void prof_end(const char* name, hipStream_t st);
+struct ProfScope {
+  const char* n;
+  hipStream_t s;
+  ProfScope(const char* name, hipStream_t st) : n(name), s(st) { prof_begin(n, s); }
+  ~ProfScope() { prof_end(n, s); }
+};
+
+// ---- launchers (defined in the kernels' translation units) ---------------------
+int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st);
+int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool force_masks, hipStream_t st);
+int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st);
+int launch_layer(const LayerArgs& a, hipStream_t st);
+int launch_layer_from_p2g(const int64_t* p2g, float* layer, int64_t L, int64_t B, int64_t Q,
+                          double num_masks, int force_masks, int force_cls, int has_void,
+                          hipStream_t st);
+int launch_bwd(const BwdArgs& a, const Dims& d, hipStream_t st);
+int launch_label_cost(const void* cls_logits, int cls_dtype, const int64_t* cls_targets,
+                      int64_t L, int64_t B, int64_t Q, int64_t C, int64_t GT_total,
+                      int64_t GT_out, int64_t bg, float scale, const ElemParams& ep,
+                      int use_softmax, float* out, hipStream_t st);
+int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st);
+
+}  // namespace ml

@@ -1,0 +1,131 @@
+// Target preparation: int64 label map -> compact per-image target operands.
+//
+//   s == 1 : u16 label per cell (labels outside [0, GT_total) -> 0xFFFF)
+//   s  > 1 : u8 count of each label inside the s x s block of every cell
+//            (B, GT_total, HWp), the reference's count tensor
+//            (src/cuda/utils.cuh:6-36)
+// plus the per-GT areas (pixel counts, src/cuda/pw_mask.cu:391) and, per
+// image, the compacted list of output columns whose GT has non-zero area.
+#include "ml_internal.h"
+
+namespace ml {
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t v, int64_t n) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st) {
+  if (n <= 0) return ML_OK;
+  int64_t blocks = ceil_div(n, 256);
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint32_t*)p,
+                     (uint32_t)v, n);
+  return check_launch("fill");
+}
+
+constexpr int kHistMax = 4096;  // GT slots histogrammed in LDS; larger -> global atomics
+
+// s == 1: one thread per cell.  grid (ceil(HWp/256), B)
+__global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
+  __shared__ int hist[kHistMax];
+  const int64_t b = blockIdx.y;
+  const int64_t HW = a.H * a.W;
+  const bool lds_hist = a.GT_total <= kHistMax;
+  if (lds_hist)
+    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) hist[i] = 0;
+  __syncthreads();
+  const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (cell < a.HWp) {
+    uint16_t v = kNoLabel;
+    if (cell < HW) {
+      const int64_t lab = a.targets[b * HW + cell];
+      if ((uint64_t)lab < (uint64_t)a.GT_total) {
+        v = (uint16_t)lab;
+        if (lds_hist) atomicAdd(&hist[lab], 1);
+        else atomicAdd(&a.area[b * a.GT_total + lab], 1);
+      }
+    }
+    a.lab16[b * a.HWp + cell] = v;
+  }
+  __syncthreads();
+  if (lds_hist)
+    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x)
+      if (hist[i]) atomicAdd(&a.area[b * a.GT_total + i], hist[i]);
+}
+
+// s > 1: one thread per low-res cell, counts[b][lab][cell] (single writer).
+__global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
+  __shared__ int hist[kHistMax];
+  const int64_t b = blockIdx.y;
+  const int64_t HW = a.H * a.W;
+  const bool lds_hist = a.GT_total <= kHistMax;
+  if (lds_hist)
+    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) hist[i] = 0;
+  __syncthreads();
+  const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (cell < HW) {
+    const int64_t i = cell / a.W, j = cell % a.W;
+    for (int64_t dy = 0; dy < a.s; ++dy) {
+      const int64_t* row = a.targets + (b * a.Ht + i * a.s + dy) * a.Wt + j * a.s;
+      for (int64_t dx = 0; dx < a.s; ++dx) {
+        const int64_t lab = row[dx];
+        if ((uint64_t)lab < (uint64_t)a.GT_total) {
+          uint8_t* c = a.counts8 + (b * a.GT_total + lab) * a.HWp + cell;
+          *c = (uint8_t)(*c + 1);
+          if (lds_hist) atomicAdd(&hist[lab], 1);
+          else atomicAdd(&a.area[b * a.GT_total + lab], 1);
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (lds_hist)
+    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x)
+      if (hist[i]) atomicAdd(&a.area[b * a.GT_total + i], hist[i]);
+}
+
+// One wave per image: compacted list of columns with non-empty GT.
+__global__ __launch_bounds__(64) void prep_columns_kernel(PrepArgs a) {
+  const int64_t b = blockIdx.x;
+  const int lane = threadIdx.x;
+  int base = 0;
+  for (int64_t c0 = 0; c0 < a.GT_out; c0 += 64) {
+    const int64_t c = c0 + lane;
+    bool ok = false;
+    if (c < a.GT_out) {
+      const int64_t act = c + (c >= a.bg ? 1 : 0);
+      ok = a.area[b * a.GT_total + act] > 0;
+    }
+    const uint64_t m = __ballot(ok);
+    const int slot = base + __popcll(m & ((1ull << lane) - 1ull));
+    if (c < a.GT_out) {
+      a.slot_of_col[b * a.GT_out + c] = ok ? slot : -1;
+      if (ok) a.colmap[b * a.nslot + slot] = (int)c;
+    }
+    base += __popcll(m);
+  }
+  for (int s = base + lane; s < a.nslot; s += 64) a.colmap[b * a.nslot + s] = -1;
+  if (lane == 0) a.ncols[b] = base;
+}
+
+int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
+  ProfScope ps_("prep", st);
+  int rc = launch_fill_i32(a.area, 0, d.B * d.GT_total, st);
+  if (rc) return rc;
+  const dim3 grid((unsigned)ceil_div(d.HWp, 256), (unsigned)d.B);
+  if (!d.counts_mode) {
+    hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);
+  } else {
+    rc = launch_fill_i32((int*)a.counts8, 0, d.B * d.GT_total * d.HWp / 4, st);
+    if (rc) return rc;
+    hipLaunchKernelGGL(prep_counts_kernel, grid, dim3(256), 0, st, a);
+  }
+  if ((rc = check_launch("prep"))) return rc;
+  hipLaunchKernelGGL(prep_columns_kernel, dim3((unsigned)d.B), dim3(64), 0, st, a);
+  if ((rc = check_launch("prep_columns"))) return rc;
+  return ML_OK;
+}
+
+}  // namespace ml

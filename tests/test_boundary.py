@@ -1,0 +1,125 @@
+"""CPU checks of the drop-in boundary: the C-ABI library exports every symbol
+declared in include/mask_loss_hip.h, the `mask_loss` module exposes the
+reference's operator names, and host tensors are rejected (there is no CPU
+implementation behind the boundary)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mask_loss_hip.h")
+LIB = os.path.join(ROOT, "mask_loss_amd", "libmask_loss_hip.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ml_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for n in ["ml_mask_matching_forward", "ml_mask_matching_backward",
+              "ml_pairwise_mask_loss_forward", "ml_pairwise_label_loss_forward",
+              "ml_last_error", "ml_mask_matching_workspace_size"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import torch  # noqa: F401  (shares one HIP runtime with the library)
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(LIB)
+    for n in declared_functions():
+        assert hasattr(lib, n), f"{n} not exported"
+    lib.ml_version.restype = ctypes.c_int
+    assert lib.ml_version() >= 1
+
+
+def test_workspace_query_rejects_bad_shapes():
+    import torch  # noqa: F401
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(LIB)
+
+    class Shape(ctypes.Structure):
+        _fields_ = [(k, ctypes.c_int64) for k in ["L", "B", "Q", "H", "W", "Ht", "Wt", "C", "GT_total"]]
+
+    class Params(ctypes.Structure):
+        _fields_ = [("smooth", ctypes.c_float), ("sigmoid_scale", ctypes.c_float),
+                    ("dice_scale", ctypes.c_float), ("cls_scale", ctypes.c_float),
+                    ("background_index", ctypes.c_int64), ("uncertainty_gamma", ctypes.c_float),
+                    ("uncertainty_gamma_min", ctypes.c_float), ("inf_thresh", ctypes.c_double),
+                    ("num_masks", ctypes.c_double), ("force_cls", ctypes.c_int32),
+                    ("force_masks", ctypes.c_int32), ("topk", ctypes.c_int64),
+                    ("strategy", ctypes.c_int64), ("mask_gamma", ctypes.c_float),
+                    ("mask_alpha", ctypes.c_float), ("cls_gamma", ctypes.c_float),
+                    ("cls_alpha", ctypes.c_float), ("void", ctypes.c_int64),
+                    ("softmax", ctypes.c_int32), ("normalize", ctypes.c_int32)]
+
+    lib.ml_mask_matching_workspace_size.restype = ctypes.c_size_t
+    p = Params(1, 1, 1, 1, 0, 1, 0.05, 1e30, -1, 1, 0, 1, 0, 0, -1, 0, -1, 133, 1, 1)
+    good = Shape(1, 16, 200, 256, 256, 256, 256, 134, 101)
+    assert lib.ml_mask_matching_workspace_size(ctypes.byref(good), ctypes.byref(p), 1) > 0
+    bad = Shape(1, 16, 200, 256, 256, 300, 256, 134, 101)  # not an integer multiple
+    assert lib.ml_mask_matching_workspace_size(ctypes.byref(bad), ctypes.byref(p), 1) == 0
+
+
+def test_extension_surface_and_host_tensors_rejected():
+    import torch
+    import mask_loss_amd
+    ml = mask_loss_amd.mask_loss
+    for n in ["mask_matching", "mask_matching_backward", "pairwise_mask_loss_forward",
+              "forward_pw_sigmoid_label_loss", "forward_pw_softmax_label_loss"]:
+        assert hasattr(ml, n)
+    z = torch.zeros(1, 1, 2, 4, 4)
+    t = torch.zeros(1, 4, 4, dtype=torch.long)
+    zc = torch.zeros(1, 1, 2, 3)
+    ct = torch.zeros(1, 2, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.mask_matching(z, t, zc, ct, 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, 1e30, -1.0, False,
+                         False, 1, 0, 0.0, -1.0, 0.0, -1.0, -1, False, True)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.pairwise_mask_loss_forward(z, t, zc, ct, 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, 0.0, -1.0,
+                                      0.0, -1.0, False, True)
+
+
+def test_function_validation_errors():
+    import torch
+    from mask_loss_amd.functions import MaskMatchingFunction
+    z = torch.zeros(1, 1, 2, 4, 4)
+    t = torch.zeros(1, 4, 4, dtype=torch.long)
+    zc = torch.zeros(1, 1, 2, 3)
+    ct = torch.zeros(1, 2, dtype=torch.long)
+    base = [z, t, zc, ct, 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, True, 1e30, -1.0, False, False, 1,
+            "global", 0.0, None, 0.0, None, None, "sigmoid"]
+
+    def call(**over):
+        names = ["mask_logits", "mask_targets", "cls_logits", "cls_targets", "smooth",
+                 "sigmoid_scale", "dice_scale", "cls_scale", "background_index",
+                 "uncertainty_gamma", "uncertainty_gamma_min", "normalize_uncertainty",
+                 "inf_thresh", "num_masks", "force_bg", "force_empty", "K", "strategy",
+                 "mask_gamma", "mask_alpha", "cls_gamma", "cls_alpha", "void", "label_loss"]
+        args = list(base)
+        for k, v in over.items():
+            args[names.index(k)] = v
+        return MaskMatchingFunction.apply(*args)
+
+    with pytest.raises(ValueError, match="assignment_strategy"):
+        call(strategy="hungarian")
+    with pytest.raises(ValueError, match="K must be"):
+        call(K=-1)
+    with pytest.raises(ValueError, match="uncertainty_gamma_min"):
+        call(uncertainty_gamma_min=1.5)
+    with pytest.raises(ValueError, match="void index"):
+        call(void=7)
+    with pytest.raises(ValueError, match="void_class_index must be provided"):
+        call(label_loss="softmax", force_bg=True)
+    with pytest.raises(ValueError, match="label_loss"):
+        call(label_loss="hinge")
+    with pytest.raises(ValueError, match="focal_alpha"):
+        call(mask_alpha=2.0)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        call()

@@ -1,0 +1,300 @@
+"""GPU parity: the HIP path (through the `mask_loss` extension and its C ABI)
+against the float64 oracle on the same seeded inputs.
+
+Tolerances (north star): float32 logits rel 1e-5, bfloat16 logits rel 2e-2.
+A value r is matched by g when |g - r| <= rtol * (|r| + floor), with floor =
+1e-2 for costs and losses (dice costs approach 0 for good matches, where a
+purely relative bound is ill-posed) and floor = 1e-2 * max|r| for gradients.
+Assignment indices are compared bit for bit against the C restatement of the
+reference solver run on the GPU's own float32 cost matrix (the reference
+solver's input), and against the oracle's float64 costs where the optimal
+assignment's cost gap exceeds the tolerance.
+"""
+import math
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import assign as OA  # noqa: E402
+from oracle import mask_oracle as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+RTOL = {"float32": 1e-5, "bfloat16": 2e-2, "float16": 2e-3}
+TDT = {"float32": torch.float32, "bfloat16": torch.bfloat16, "float16": torch.float16}
+
+
+@pytest.fixture(scope="module")
+def ml():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import mask_loss_amd
+    return mask_loss_amd.mask_loss
+
+
+def close(g, r, rtol, floor):
+    g = np.asarray(g, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    assert g.shape == r.shape, (g.shape, r.shape)
+    assert np.array_equal(np.isinf(g), np.isinf(r)), "inf pattern differs"
+    f = np.isfinite(r)
+    err = np.abs(g[f] - r[f])
+    bound = rtol * (np.abs(r[f]) + floor)
+    bad = err > bound
+    assert not bad.any(), f"max err {err.max():.3e}, worst ratio {(err / bound).max():.3f}"
+
+
+def rounded(z, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(z, dtype=np.float32)).to(TDT[dtype])
+    return t, t.float().numpy().astype(np.float64)
+
+
+def make_case(seed, L=1, B=2, Q=20, H=16, W=16, s=1, G=6, C=9, dtype="float32", sigma=2.0,
+              empty_image=False):
+    rng = np.random.default_rng(seed)
+    z = rng.normal(0, sigma, size=(L, B, Q, H, W)).astype(np.float32)
+    tgt = np.zeros((B, H * s, W * s), dtype=np.int64)
+    for b in range(B):
+        if empty_image and b == 0:
+            continue
+        for g in range(1, G + 1):
+            cy, cx = rng.uniform(0, H * s), rng.uniform(0, W * s)
+            ry, rx = rng.uniform(1, H * s / 3), rng.uniform(1, W * s / 3)
+            yy, xx = np.mgrid[0:H * s, 0:W * s]
+            tgt[b][((yy - cy) / ry) ** 2 + ((xx - cx) / rx) ** 2 <= 1] = g
+    cls_t = np.full((B, G + 2), -1, dtype=np.int64)  # slot 0 = background, last = padding
+    cls_t[:, 1:G + 1] = rng.integers(0, C - 1, size=(B, G))
+    zc = rng.normal(0, 1, size=(L, B, Q, C)).astype(np.float32)
+    zt, z64 = rounded(z, dtype)
+    return dict(z=zt.cuda(), z64=z64, tgt=torch.from_numpy(tgt).cuda(), tgt_np=tgt,
+                zc=torch.from_numpy(zc).cuda(), zc64=zc.astype(np.float64),
+                ct=torch.from_numpy(cls_t).cuda(), ct_np=cls_t, C=C, dtype=dtype)
+
+
+COST_CASES = [
+    dict(name="f32_default", kw={}, p={}),
+    dict(name="bf16_default", kw=dict(dtype="bfloat16", sigma=3.0), p={}),
+    dict(name="f16_default", kw=dict(dtype="float16"), p={}),
+    dict(name="f32_counts_s2", kw=dict(s=2, H=12, W=12), p={}),
+    dict(name="f32_counts_s4", kw=dict(s=4, H=8, W=8), p={}),
+    dict(name="f32_focal", kw={}, p=dict(mask_gamma=2.0, mask_alpha=0.25, cls_gamma=2.0, cls_alpha=0.25)),
+    dict(name="f32_focal_g1", kw={}, p=dict(mask_gamma=1.0, mask_alpha=0.6, cls_gamma=1.5)),
+    dict(name="f32_ug0_nonorm", kw={}, p=dict(ug=0.0, normalize=False)),
+    dict(name="f32_ug2", kw={}, p=dict(ug=2.0, ug_min=0.1)),
+    dict(name="f32_nobg", kw={}, p=dict(bg=-1)),
+    dict(name="f32_bg_mid", kw={}, p=dict(bg=3)),
+    dict(name="f32_softmax", kw={}, p=dict(use_softmax=True)),
+    dict(name="f32_odd_shapes", kw=dict(Q=37, H=7, W=5, B=3), p={}),
+    dict(name="f32_tail32", kw=dict(Q=17, H=10, W=10), p={}),
+    dict(name="f32_many_gt", kw=dict(G=40, Q=50, H=32, W=32), p={}),
+    dict(name="bf16_many_gt", kw=dict(G=120, Q=64, H=32, W=32, dtype="bfloat16"), p={}),
+    dict(name="f32_empty_image", kw=dict(empty_image=True), p={}),
+    dict(name="f32_L2", kw=dict(L=2), p=dict(scales=(1.3, 0.7, 2.0), smooth=0.5)),
+]
+
+
+def params(p):
+    d = dict(smooth=1.0, scales=(1.0, 1.0, 1.0), bg=0, ug=1.0, ug_min=0.05, mask_gamma=0.0,
+             mask_alpha=-1.0, cls_gamma=0.0, cls_alpha=-1.0, use_softmax=False, normalize=True)
+    d.update(p)
+    return d
+
+
+def gpu_costs(ml, x, P):
+    ss, ds, cs = P["scales"]
+    return ml.pairwise_mask_loss_forward(
+        x["z"], x["tgt"], x["zc"], x["ct"], P["smooth"], ss, ds, cs, P["bg"], P["ug"],
+        P["ug_min"], P["mask_gamma"], P["mask_alpha"], P["cls_gamma"], P["cls_alpha"],
+        P["use_softmax"], P["normalize"])
+
+
+def oracle_costs(x, P):
+    ss, ds, cs = P["scales"]
+    return O.pairwise_mask_loss_forward(
+        x["z64"], x["tgt_np"], x["zc64"], x["ct_np"], P["smooth"], ss, ds, cs, P["bg"], P["ug"],
+        P["ug_min"], P["mask_gamma"], P["mask_alpha"], P["cls_gamma"], P["cls_alpha"],
+        P["use_softmax"], P["normalize"])
+
+
+@pytest.mark.parametrize("case", COST_CASES, ids=lambda c: c["name"])
+def test_pairwise_costs(ml, case):
+    x = make_case(5, **case["kw"])
+    P = params(case["p"])
+    got = gpu_costs(ml, x, P).cpu().numpy()
+    ref = oracle_costs(x, P)
+    rt = RTOL[x["dtype"]]
+    close(got[0], ref[0], rt, 1e-2)
+    close(got[1], ref[1], rt, 1e-2)
+    close(got[2], ref[2], 1e-5, 1e-2)  # label costs are float32 in every case
+
+
+@pytest.mark.parametrize("softmax", [False, True])
+def test_label_cost_ops(ml, softmax):
+    x = make_case(9)
+    if softmax:
+        got = ml.forward_pw_softmax_label_loss(x["zc"], x["ct"], 0, 1.7).cpu().numpy()
+        ref = O.pairwise_softmax_label_cost(x["zc64"], x["ct_np"], 0, 1.7)
+    else:
+        got = ml.forward_pw_sigmoid_label_loss(x["zc"], x["ct"], -1, 1.7, 2.0, 0.25).cpu().numpy()
+        ref = O.pairwise_sigmoid_label_cost(x["zc64"], x["ct_np"], -1, 1.7, 2.0, 0.25)
+    close(got, ref, 1e-5, 1e-2)
+
+
+def matching_call(ml, x, P, M):
+    ss, ds, cs = P["scales"]
+    return ml.mask_matching_fused(
+        x["z"], x["tgt"], x["zc"], x["ct"], P["smooth"], ss, ds, cs, P["bg"], P["ug"], P["ug_min"],
+        M["inf_thresh"], M["num_masks"], M["force_cls"], M["force_masks"], M["K"], M["strategy"],
+        P["mask_gamma"], P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["void"],
+        P["use_softmax"], P["normalize"])
+
+
+MATCH_CASES = [
+    dict(name="global_softmax_forcebg", kw={}, p=dict(use_softmax=True),
+         m=dict(force_cls=True, void=8)),
+    dict(name="global_sigmoid", kw={}, p={}, m={}),
+    dict(name="global_sigmoid_void_forcemasks", kw={}, p={}, m=dict(void=8, force_masks=True)),
+    dict(name="global_K2", kw=dict(Q=30), p={}, m=dict(K=2)),
+    dict(name="round_K2", kw=dict(Q=30), p={}, m=dict(K=2, strategy=1)),
+    dict(name="greedy_K2", kw=dict(Q=30), p={}, m=dict(K=2, strategy=2)),
+    dict(name="pseudo_greedy_K3", kw=dict(Q=30), p={}, m=dict(K=3, strategy=3)),
+    dict(name="more_gts_than_queries", kw=dict(Q=5, G=9), p={}, m={}),
+    dict(name="bf16_headline_like", kw=dict(dtype="bfloat16", sigma=3.0, Q=70, G=30, H=32, W=32),
+         p=dict(use_softmax=True), m=dict(force_cls=True, void=8)),
+    dict(name="num_masks", kw={}, p={}, m=dict(num_masks=7.0)),
+    dict(name="inf_thresh_low", kw={}, p={}, m=dict(inf_thresh=2.0)),
+    dict(name="counts_s2_force", kw=dict(s=2, H=12, W=12), p=dict(mask_gamma=2.0, mask_alpha=0.25),
+         m=dict(force_masks=True, force_cls=True)),
+    dict(name="empty_image", kw=dict(empty_image=True), p={}, m=dict(force_cls=True, void=8)),
+    dict(name="q_tail_1024", kw=dict(Q=130, H=8, W=8, G=20), p={}, m={}),
+]
+
+
+def mparams(m):
+    d = dict(inf_thresh=1e30, num_masks=-1.0, force_cls=False, force_masks=False, K=1,
+             strategy=0, void=-1)
+    d.update(m)
+    return d
+
+
+@pytest.mark.parametrize("case", MATCH_CASES, ids=lambda c: c["name"])
+def test_matching_forward(ml, case):
+    x = make_case(21, **case["kw"])
+    P, M = params(case["p"]), mparams(case["m"])
+    p2g, pr, m, d, c, stats = [t.cpu() for t in matching_call(ml, x, P, M)]
+    # 1. solver bit-exactness on the GPU's own float32 cost matrix
+    sep = gpu_costs(ml, x, P)
+    total = ((sep[0] + sep[1]) + sep[2]).double().cpu().numpy()
+    L, B, Q, G = total.shape
+    rp2g, rpr = OA.assign_batch(total.reshape(L * B, Q, G), M["inf_thresh"], M["K"], M["strategy"])
+    assert np.array_equal(p2g.numpy().reshape(L * B, Q), rp2g), "assignment differs from reference solver"
+    assert np.array_equal(pr.numpy().reshape(L * B, Q), rpr), "pred_round differs"
+    # 2. losses against the oracle evaluated at the same assignment
+    ss, ds, cs = P["scales"]
+    ref_sep = oracle_costs(x, P)
+    rm, rd, rc = O.matching_forward_losses(
+        ref_sep, p2g.numpy(), x["z64"], x["zc64"], x["tgt_np"].shape, P["smooth"], ss, ds, cs,
+        P["mask_gamma"], P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["num_masks"],
+        M["force_masks"], M["force_cls"], M["void"], P["use_softmax"])
+    rt = RTOL[x["dtype"]]
+    close(m.numpy(), rm, rt, 1e-2)
+    close(d.numpy(), rd, rt, 1e-2)
+    close(c.numpy(), rc, 1e-5, 1e-2)
+    # 3. oracle's own float64 assignment agrees wherever it is not a near-tie
+    rt64 = ref_sep.sum(0)
+    op2g, _ = OA.assign_batch(rt64.reshape(L * B, Q, G), M["inf_thresh"], M["K"], M["strategy"])
+    for s_ in range(L * B):
+        if np.array_equal(op2g[s_], p2g.numpy().reshape(L * B, Q)[s_]):
+            continue
+        cost_of = lambda a: sum(rt64.reshape(L * B, Q, G)[s_, q, g] for q, g in enumerate(a) if g >= 0)
+        gap = abs(cost_of(p2g.numpy().reshape(L * B, Q)[s_]) - cost_of(op2g[s_]))
+        assert gap <= 10 * rt * max(1.0, abs(cost_of(op2g[s_]))), f"slice {s_}: gap {gap}"
+
+
+BWD_CASES = [
+    dict(name="f32_softmax_forcebg", kw={}, p=dict(use_softmax=True), m=dict(force_cls=True, void=8)),
+    dict(name="f32_sigmoid_focal_forcemasks", kw={}, p=dict(mask_gamma=2.0, mask_alpha=0.25,
+         cls_gamma=2.0, cls_alpha=0.25), m=dict(force_masks=True, void=8)),
+    dict(name="f32_counts_s2", kw=dict(s=2, H=12, W=12), p={}, m=dict(force_cls=True)),
+    dict(name="f32_nonorm_ug0", kw={}, p=dict(ug=0.0, normalize=False), m={}),
+    dict(name="bf16_softmax", kw=dict(dtype="bfloat16", sigma=3.0), p=dict(use_softmax=True),
+         m=dict(force_cls=True, void=8)),
+    dict(name="f32_odd", kw=dict(Q=37, H=7, W=5, B=3), p={}, m=dict(void=8)),
+]
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: c["name"])
+def test_matching_backward(ml, case, fused):
+    x = make_case(33, **case["kw"])
+    P, M = params(case["p"]), mparams(case["m"])
+    outs = matching_call(ml, x, P, M)
+    p2g, stats = outs[0], outs[5]
+    L = x["z"].shape[0]
+    gm = torch.tensor([0.7] * L, device="cuda")
+    gd = torch.tensor([1.3] * L, device="cuda")
+    gc = torch.tensor([0.9] * L, device="cuda")
+    ss, ds, cs = P["scales"]
+    args = (gm, gd, gc, x["z"], x["tgt"], x["zc"], x["ct"], p2g, P["smooth"], ss, ds, cs, P["bg"],
+            P["ug"], P["ug_min"], M["num_masks"], M["force_cls"], M["force_masks"], P["mask_gamma"],
+            P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["void"], P["use_softmax"],
+            P["normalize"])
+    if fused:
+        gz, gzc = ml.mask_matching_backward_fused(*args, stats)
+    else:
+        gz, gzc = ml.mask_matching_backward(*args)
+    assert gz.dtype == x["z"].dtype and gzc.dtype == x["zc"].dtype
+    rz, rzc = O.matching_backward(
+        gm.cpu().numpy(), gd.cpu().numpy(), gc.cpu().numpy(), x["z64"], x["tgt_np"], x["zc64"],
+        x["ct_np"], p2g.cpu().numpy(), P["smooth"], ss, ds, cs, P["bg"], P["ug"], P["ug_min"],
+        M["num_masks"], M["force_cls"], M["force_masks"], P["mask_gamma"], P["mask_alpha"],
+        P["cls_gamma"], P["cls_alpha"], M["void"], P["use_softmax"], P["normalize"])
+    rt = RTOL[x["dtype"]]
+    gzn = gz.float().cpu().numpy()
+    close(gzn, rz, rt, 1e-2 * np.abs(rz).max())
+    close(gzc.cpu().numpy(), rzc, 1e-5, 1e-2 * np.abs(rzc).max())
+    unmatched = p2g.cpu().numpy() < 0
+    if not M["force_masks"]:
+        assert (gzn[unmatched] == 0).all()
+
+
+def test_function_autograd_bf16(ml):
+    from mask_loss_amd.functions import MaskMatchingFunction
+    x = make_case(44, dtype="bfloat16", sigma=3.0, Q=40, G=12)
+    z = x["z"].clone().requires_grad_(True)
+    zc = x["zc"].clone().requires_grad_(True)
+    p2g, pr, m, d, c = MaskMatchingFunction.apply(
+        z, x["tgt"], zc, x["ct"], 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, True, 1e30, -1.0, True, False,
+        1, "global", 0.0, None, 0.0, None, 8, "softmax")
+    (m.sum() + d.sum() + c.sum()).backward()
+    assert z.grad.dtype == torch.bfloat16 and z.grad.shape == z.shape
+    rz, rzc = O.matching_backward(
+        np.ones(1), np.ones(1), np.ones(1), x["z64"], x["tgt_np"], x["zc64"], x["ct_np"],
+        p2g.cpu().numpy(), 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, -1.0, True, False, 0.0, -1.0, 0.0,
+        -1.0, 8, True, True)
+    close(z.grad.float().cpu().numpy(), rz, 2e-2, 1e-2 * np.abs(rz).max())
+    close(zc.grad.cpu().numpy(), rzc, 1e-5, 1e-2 * np.abs(rzc).max())
+
+
+def test_reference_wrapper_argument_order(ml):
+    """The reference's MaskMatchingFunction calls mask_matching with 25
+    positional arguments (normalize_uncertainty twice); both orders work."""
+    x = make_case(3)
+    a24 = ml.mask_matching(x["z"], x["tgt"], x["zc"], x["ct"], 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05,
+                           1e30, -1.0, False, False, 1, 0, 0.0, -1.0, 0.0, -1.0, -1, False, True)
+    a25 = ml.mask_matching(x["z"], x["tgt"], x["zc"], x["ct"], 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05,
+                           True, 1e30, -1.0, False, False, 1, 0, 0.0, -1.0, 0.0, -1.0, -1, False,
+                           True)
+    for u, v in zip(a24, a25):
+        assert torch.equal(u, v)
+
+
+def test_deterministic(ml):
+    x = make_case(8, dtype="bfloat16", Q=64, G=20, H=32, W=32)
+    P, M = params(dict(use_softmax=True)), mparams(dict(force_cls=True, void=8))
+    a = [t.clone() for t in matching_call(ml, x, P, M)]
+    b = [t.clone() for t in matching_call(ml, x, P, M)]
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)

@@ -139,7 +139,7 @@ def main():
     ms = e0.elapsed_time(e1) / a.steps
 
     kernels = {}
-    for name in ["prep", "pair_cost", "assign", "layer", "bwd_mask", "bwd_cls"]:
+    for name in ["prep", "pair_cost", "finalize", "assign", "layer", "bwd_mask", "bwd_cls"]:
         n, t = read_prof(lib, name)
         if n:
             kernels[name] = {"launches": n, "avg_us": round(1e3 * t / n, 2)}

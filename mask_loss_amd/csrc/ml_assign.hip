@@ -54,8 +54,7 @@ __device__ __forceinline__ ClsTerm cls_terms(float z, const ElemParams& ep) {
 }
 
 struct SmemLayout {
-  size_t rowS, rowP, clsA, clsPen, mPen, dPen, contrib, colok, vcols, preds, p, way, u, hrows,
-      asg, costL, total;
+  size_t contrib, colok, vcols, preds, p, way, u, hrows, asg, costL, total;
 };
 
 __host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, bool cost_in_lds) {
@@ -66,12 +65,6 @@ __host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, bool c
     o += (bytes + 15) & ~size_t(15);
     return r;
   };
-  s.rowS = take(Q * 4);
-  s.rowP = take(Q * 4);
-  s.clsA = take(Q * 4);
-  s.clsPen = take(Q * 4);
-  s.mPen = take(Q * 4);
-  s.dPen = take(Q * 4);
   s.contrib = take(Q * 4 * 4);
   s.colok = take((GTo + 1) * 4);
   s.vcols = take((GTo + 1) * 4);
@@ -87,53 +80,139 @@ __host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, bool c
   return s;
 }
 
-struct Ctx {
-  const AssignArgs* a;
-  int64_t lb, l, b;
-  int G;
-  const float* rowS;
-  const float* rowP;
-  const float* clsA;
-};
-
-// bce, dice, cls of (q, column c) from the K-split partials.
-__device__ void pair_costs(const Ctx& x, int64_t q, int64_t c, float& bce, float& dice,
-                           float& cls) {
-  const AssignArgs& a = *x.a;
-  const int slot = a.slot_of_col[x.b * a.GT_out + c];
-  if (slot < 0) {
-    bce = INFINITY;
-    dice = INFINITY;
-  } else {
-    const int64_t rt = q / a.rows, row = q % a.rows;
-    float num = 0.f, I = 0.f, T = 0.f;
-    for (int64_t ks = 0; ks < a.KS; ++ks) {
-      const float* P = a.partials +
-                       ((ks * (a.L * a.B) + x.lb) * a.rtiles + rt) * 3 * a.rows * a.nslot;
-      num += P[(0 * a.rows + row) * a.nslot + slot];
-      I += P[(1 * a.rows + row) * a.nslot + slot];
-      T += P[(2 * a.rows + row) * a.nslot + slot];
-    }
-    bce = num / x.rowS[q] * a.sigmoid_scale;
-    dice = (1.f - (2.f * I + a.smooth) / (x.rowP[q] + T + a.smooth)) * a.dice_scale;
-  }
-  const int64_t act = c + (c >= a.bg ? 1 : 0);
-  const int64_t y = a.cls_targets[x.b * a.GT_total + act];
-  if (y < 0 || y >= a.C) {
-    cls = INFINITY;
-  } else {
-    const float zy = cls_elem(a.cls_logits, a.cls_dtype, (x.lb * a.Q + q) * a.C + y);
-    if (a.use_softmax) {
-      cls = (x.clsA[q] - zy) * a.cls_scale;
-    } else {
-      const ClsTerm t = cls_terms(zy, a.cls_ep);
-      cls = (x.clsA[q] + (t.pos - t.neg)) * (1.f / (float)a.C) * a.cls_scale;
-    }
-  }
-}
-
 __device__ __forceinline__ bool cost_ok(double c, double thr) { return isfinite(c) && c < thr; }
 
+// ---------------------------------------------------------------------------
+// Finalize: one wave per (l, b, q) row.  Sums the K-split partials of every
+// used column slot, forms bce and dice (src/cuda/pw_mask.cu:299-305), the
+// label cost (src/cuda/pw_sigmoid_label_loss.cu:76-105,
+// src/cuda/pw_softmax_label_loss.cu:84-102), +inf for empty GTs or invalid
+// classes, and the row terms used later: normaliser S, mass P, and the
+// unmatched-query penalties (src/cuda/mask_matching_forward.cu:125-277).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
+  __shared__ float sl[4][3][256 + 16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= a.L * a.B * a.Q) return;
+  const int64_t lb = row / a.Q, q = row % a.Q, b = lb % a.B;
+  const int64_t GTo = a.GT_out, C = a.C;
+  const int G = a.ncols[b];
+  const int64_t rt = q / a.rows, rr = q % a.rows;
+  const int64_t pstride = (a.L * a.B) * a.rtiles * 3 * a.rows * a.nslot;
+  const float* P0 = a.partials + (lb * a.rtiles + rt) * 3 * a.rows * a.nslot + rr * a.nslot;
+  for (int s = lane; s <= G; s += 64) {
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+    for (int64_t ks = 0; ks < a.KS; ++ks) {
+      const float* P = P0 + ks * pstride;
+      v0 += P[s];
+      v1 += P[a.rows * a.nslot + s];
+      v2 += P[2 * a.rows * a.nslot + s];
+    }
+    sl[wave][0][s] = v0;
+    sl[wave][1][s] = v1;
+    sl[wave][2][s] = v2;
+  }
+  wave_sync();
+  float S = sl[wave][2][G];
+  const float P = sl[wave][1][G];
+  if (!a.normalize) S = (float)(a.Ht * a.Wt);
+  S = fmaxf(S, kEps);
+
+  // label row term and unmatched class penalty
+  const int64_t zb = row * C;
+  const int64_t void_idx = a.void_idx;
+  const bool has_void = void_idx >= 0;
+  const bool softmax_bg = a.use_softmax && a.force_cls && has_void;
+  float rowv, pen = 0.f;
+  if (a.use_softmax) {
+    float m = -INFINITY;
+    for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_elem(a.cls_logits, a.cls_dtype, zb + c));
+    m = wave_max(m);
+    float se = 0.f;
+    for (int64_t c = lane; c < C; c += 64)
+      se += __expf(cls_elem(a.cls_logits, a.cls_dtype, zb + c) - m);
+    se = wave_sum(se);
+    rowv = __logf(fmaxf(se, 1e-20f)) + m;
+    if (a.force_cls || has_void) {
+      const float zv = cls_elem(a.cls_logits, a.cls_dtype, zb + void_idx);
+      // softmax CE towards void when forcing background; otherwise the
+      // sigmoid BCE of the void channel (mask_matching_forward.cu:146-218)
+      pen = softmax_bg ? (rowv - zv) * a.cls_scale : sig_terms(zv).cp * a.cls_scale;
+    }
+  } else {
+    float base = 0.f, vpos = 0.f, vneg = 0.f;
+    for (int64_t c = lane; c < C; c += 64) {
+      const ClsTerm t = cls_terms(cls_elem(a.cls_logits, a.cls_dtype, zb + c), a.cls_ep);
+      base += t.neg;
+      if (c == void_idx) {
+        vpos = t.pos;
+        vneg = t.neg;
+      }
+    }
+    base = wave_sum(base);
+    vpos = wave_sum(vpos);
+    vneg = wave_sum(vneg);
+    rowv = base;
+    if (a.force_cls) {
+      const float invC = C > 0 ? 1.f / (float)C : 0.f;
+      pen = base * invC;
+      if (has_void && C > 0) pen += (vpos - vneg) * invC;
+    } else if (has_void) {
+      pen = vpos;
+    }
+    pen *= a.cls_scale;
+  }
+
+  // all output columns of this row
+  const int64_t term = a.L * a.B * a.Q * GTo;
+  for (int64_t c = lane; c < GTo; c += 64) {
+    const int slot = a.slot_of_col[b * GTo + c];
+    float bce = INFINITY, dice = INFINITY, cls;
+    if (slot >= 0) {
+      bce = sl[wave][0][slot] / S * a.sigmoid_scale;
+      dice = (1.f - (2.f * sl[wave][1][slot] + a.smooth) / (P + sl[wave][2][slot] + a.smooth)) *
+             a.dice_scale;
+    }
+    const int64_t act = c + (c >= a.bg ? 1 : 0);
+    const int64_t y = a.cls_targets[b * a.GT_total + act];
+    if (y < 0 || y >= C) {
+      cls = INFINITY;
+    } else {
+      const float zy = cls_elem(a.cls_logits, a.cls_dtype, zb + y);
+      if (a.use_softmax) {
+        cls = (rowv - zy) * a.cls_scale;
+      } else {
+        const ClsTerm t = cls_terms(zy, a.cls_ep);
+        cls = (rowv + (t.pos - t.neg)) * (1.f / (float)C) * a.cls_scale;
+      }
+    }
+    const int64_t o = row * GTo + c;
+    a.sep[o] = bce;
+    a.sep[term + o] = dice;
+    a.sep[2 * term + o] = cls;
+  }
+  if (lane == 0 && a.rowstat) {
+    float mp = 0.f, dp = 0.f;
+    if (a.force_masks) {
+      float ub = 0.f, up = 0.f;
+      for (int64_t ks = 0; ks < a.KS; ++ks) {
+        const float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
+        ub += rs[0];
+        up += rs[1];
+      }
+      const float psum = up * a.N2;
+      mp = a.sigmoid_scale * (ub / (float)a.HW);
+      dp = a.dice_scale * (psum / (psum + a.smooth));
+    }
+    float* rs = a.rowstat + row * 8;
+    rs[0] = S;
+    rs[1] = P;
+    rs[2] = mp;
+    rs[3] = dp;
+    rs[4] = pen;
+  }
+}
 // ---------------------------------------------------------------------------
 // e-maxx Hungarian on one wave.  Rows = hrows[0..M) (GT columns), columns =
 // preds[0..n) (queries).  asg[k] = row index assigned to column k, or -1.
@@ -310,12 +389,6 @@ template <int NJ>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const SmemLayout L = smem_layout(a.Q, a.GT_out, a.cost_in_lds != 0);
-  float* rowS = (float*)(smem + L.rowS);
-  float* rowP = (float*)(smem + L.rowP);
-  float* clsA = (float*)(smem + L.clsA);
-  float* clsPen = (float*)(smem + L.clsPen);
-  float* mPen = (float*)(smem + L.mPen);
-  float* dPen = (float*)(smem + L.dPen);
   float* contrib = (float*)(smem + L.contrib);
   int* colok = (int*)(smem + L.colok);
   int* vcols = (int*)(smem + L.vcols);
@@ -326,133 +399,46 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   int* hrows = (int*)(smem + L.hrows);
   int* asg = (int*)(smem + L.asg);
 
-  const int64_t lb = blockIdx.x, l = lb / a.B, b = lb % a.B;
+  const int64_t lb = blockIdx.x, b = lb % a.B;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int64_t Q = a.Q, GTo = a.GT_out, C = a.C;
+  const int64_t Q = a.Q, GTo = a.GT_out;
   float* costL = a.cost_in_lds ? (float*)(smem + L.costL) : a.costT + lb * GTo * Q;
-  const int G = a.ncols[b];
+  const int64_t term = a.L * a.B * Q * GTo;
+  const float* sep = a.sep + lb * Q * GTo;
 
-  // ---- 1. per-query statistics
-  const int64_t void_idx = a.void_idx;
-  const bool has_void = void_idx >= 0;
-  const bool need_cls_pen = a.force_cls || has_void;
-  const bool softmax_bg = a.use_softmax && a.force_cls && has_void;
-  for (int64_t q = wave; q < Q; q += 4) {
-    // S, P from the ones column (slot G)
-    if (lane == 0) {
-      const int64_t rt = q / a.rows, row = q % a.rows;
-      float P = 0.f, S = 0.f;
-      for (int64_t ks = 0; ks < a.KS; ++ks) {
-        const float* Pp = a.partials +
-                          ((ks * (a.L * a.B) + lb) * a.rtiles + rt) * 3 * a.rows * a.nslot;
-        P += Pp[(1 * a.rows + row) * a.nslot + G];
-        S += Pp[(2 * a.rows + row) * a.nslot + G];
-      }
-      if (!a.normalize) S = (float)(a.Ht * a.Wt);
-      rowS[q] = fmaxf(S, kEps);
-      rowP[q] = P;
-      float mp = 0.f, dp = 0.f;
-      if (a.force_masks) {
-        float ub = 0.f, up = 0.f;
-        for (int64_t ks = 0; ks < a.KS; ++ks) {
-          const float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
-          ub += rs[0];
-          up += rs[1];
-        }
-        const float bce_mean = ub / (float)a.HW;
-        const float psum = up * a.N2;
-        mp = a.sigmoid_scale * bce_mean;
-        dp = a.dice_scale * (psum / (psum + a.smooth));
-      }
-      mPen[q] = mp;
-      dPen[q] = dp;
-    }
-    // label row terms
-    const int64_t zb = (lb * Q + q) * C;
-    if (a.use_softmax) {
-      float m = -INFINITY;
-      for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_elem(a.cls_logits, a.cls_dtype, zb + c));
-      m = wave_max(m);
-      float se = 0.f;
-      for (int64_t c = lane; c < C; c += 64)
-        se += __expf(cls_elem(a.cls_logits, a.cls_dtype, zb + c) - m);
-      se = wave_sum(se);
-      const float lse = __logf(fmaxf(se, 1e-20f)) + m;
-      if (lane == 0) clsA[q] = lse;
-      float pen = 0.f;
-      if (need_cls_pen) {
-        const float zv = cls_elem(a.cls_logits, a.cls_dtype, zb + void_idx);
-        if (softmax_bg) {
-          pen = (lse - zv) * a.cls_scale;
-        } else {
-          // softmax label loss, void channel only: sigmoid BCE towards void
-          // (mask_matching_forward.cu:213-218 with unit focal terms)
-          const Sig s = sig_terms(zv);
-          pen = s.cp * a.cls_scale;
-        }
-      }
-      if (lane == 0) clsPen[q] = pen;
-    } else {
-      float base = 0.f, vpos = 0.f, vneg = 0.f;
-      for (int64_t c = lane; c < C; c += 64) {
-        const ClsTerm t = cls_terms(cls_elem(a.cls_logits, a.cls_dtype, zb + c), a.cls_ep);
-        base += t.neg;
-        if (c == void_idx) {
-          vpos = t.pos;
-          vneg = t.neg;
-        }
-      }
-      base = wave_sum(base);
-      vpos = wave_sum(vpos);
-      vneg = wave_sum(vneg);
-      if (lane == 0) {
-        clsA[q] = base;
-        float pen = 0.f;
-        if (a.force_cls) {
-          const float invC = C > 0 ? 1.f / (float)C : 0.f;
-          pen = base * invC;
-          if (has_void && C > 0) pen += (vpos - vneg) * invC;
-        } else if (has_void) {
-          pen = vpos;
-        }
-        clsPen[q] = pen * a.cls_scale;
-      }
-    }
-  }
+  // ---- 1. total cost (bce + dice) + cls as float (src/cpu/matching.cpp:665),
+  //         transposed to [column][query]; column validity (matching.cpp:497-511)
   for (int64_t c = tid; c <= GTo; c += 256) colok[c] = 0;
   __syncthreads();
-
-  Ctx x;
-  x.a = &a;
-  x.lb = lb;
-  x.l = l;
-  x.b = b;
-  x.G = G;
-  x.rowS = rowS;
-  x.rowP = rowP;
-  x.clsA = clsA;
-
-  // ---- 2. all (q, c) costs
-  const int64_t term = a.L * a.B * Q * GTo;
-  for (int64_t i = tid; i < Q * GTo; i += 256) {
-    const int64_t q = i / GTo, c = i % GTo;
-    float bce, dice, cls;
-    pair_costs(x, q, c, bce, dice, cls);
-    if (a.sep) {
-      const int64_t o = (lb * Q + q) * GTo + c;
-      a.sep[o] = bce;
-      a.sep[term + o] = dice;
-      a.sep[2 * term + o] = cls;
+  {
+    const int64_t n = Q * GTo;
+    constexpr int U = 8;  // independent loads in flight per thread
+    for (int64_t i0 = tid; i0 < n; i0 += 256 * U) {
+      float v0[U], v1[U], v2[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int64_t i = i0 + k * 256;
+        if (i < n) {
+          v0[k] = sep[i];
+          v1[k] = sep[term + i];
+          v2[k] = sep[2 * term + i];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int64_t i = i0 + k * 256;
+        if (i < n) {
+          const int64_t q = i / GTo, c = i % GTo;
+          const float tot = (v0[k] + v1[k]) + v2[k];
+          costL[c * Q + q] = tot;
+          if (cost_ok((double)tot, a.inf_thresh)) colok[c] = 1;  // benign race: all store 1
+        }
+      }
     }
-    const float tot = (bce + dice) + cls;
-    costL[c * Q + q] = tot;
-    if (cost_ok((double)tot, a.inf_thresh)) colok[c] = 1;  // benign race: all writers store 1
   }
-  if (a.costs_only) return;
   __syncthreads();
-  if (!a.cost_in_lds) __threadfence_block();
 
-  // ---- 3. assignment on wave 0
+  // ---- 2. assignment on wave 0
   if (wave == 0) {
     int nv = 0;
     for (int64_t c0 = 0; c0 < GTo; c0 += 64) {
@@ -462,41 +448,30 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       if (okc) vcols[nv + __popcll(m & ((1ull << lane) - 1ull))] = (int)c;
       nv += __popcll(m);
     }
-    int* p2g = asg;  // reuse: per-query result (-1 / column), separate from Hungarian asg below
-    // asg doubles as p2g scratch: Hungarian results go to hasg (preds area reused after)
+    int* p2g = asg;         // per-query result (-1 or column)
+    int* hout = (int*)contrib;  // output of one Hungarian call
     for (int64_t q = lane; q < Q; q += 64) p2g[q] = -1;
     wave_sync();
     const double thr = a.inf_thresh, BIG = a.big;
     const int64_t K = a.topk;
     bool okh = true;
-    int* hasg = way;  // assignment output of one Hungarian call (length n) lives after way? no:
-    (void)hasg;
-    // scratch for one Hungarian call's output: reuse `contrib` (Q*4 floats >= Q ints)
-    int* hout = (int*)contrib;
     if (Q > 0 && GTo > 0 && K > 0 && nv > 0) {
+      int* cap = colok;  // capacities (column validity no longer needed)
+      for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
+      wave_sync();
+      for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
+      for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
+      wave_sync();
       if (a.strategy == ML_GLOBAL || a.strategy == ML_PSEUDO_GREEDY) {
         int M = 0;
-        if (a.strategy == ML_GLOBAL) {
-          for (int64_t rep = 0; rep < K && M < Q; ++rep)
-            for (int t = 0; t < nv && M < Q; ++t) {
-              if (lane == 0) hrows[M] = vcols[t];
-              ++M;
-            }
-        } else {
+        const int64_t reps = a.strategy == ML_GLOBAL ? K : 1;
+        for (int64_t rep = 0; rep < reps && M < Q; ++rep)
           for (int t = 0; t < nv && M < Q; ++t) {
             if (lane == 0) hrows[M] = vcols[t];
             ++M;
           }
-        }
-        for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
         wave_sync();
         okh = hungarian_wave<NJ>(costL, Q, preds, (int)Q, hrows, M, thr, BIG, pp, way, u, hout);
-        // cap reuses vcols tail? capacities live in colok (GTo ints) from here on
-        int* cap = colok;
-        for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
-        wave_sync();
-        for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
-        wave_sync();
         if (okh) {
           for (int64_t q = lane; q < Q; q += 64) {
             const int r = hout[q];
@@ -524,12 +499,6 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
           }
         }
       } else if (a.strategy == ML_ROUND) {
-        int* cap = colok;
-        for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
-        wave_sync();
-        for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
-        for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
-        wave_sync();
         int nrem = (int)Q;
         for (int64_t rd = 0; rd < K && okh; ++rd) {
           int M = 0;
@@ -543,7 +512,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
           wave_sync();
           okh = hungarian_wave<NJ>(costL, Q, preds, nrem, hrows, M, thr, BIG, pp, way, u, hout);
           if (!okh) break;
-          // apply in pred order, compact the remaining preds (order preserved)
+          // apply in query order and compact the remaining queries (order kept)
           int nn = 0;
           for (int k0 = 0; k0 < nrem; k0 += 64) {
             const int k = k0 + lane;
@@ -561,7 +530,6 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
               }
             }
             const uint64_t m = __ballot(keep);
-            // write compacted into hout tail-safe region: use way[] as temp
             if (keep) way[nn + __popcll(m & ((1ull << lane) - 1ull))] = q;
             nn += __popcll(m);
           }
@@ -579,12 +547,6 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
           if (nrem == 0) break;
         }
       } else if (a.strategy == ML_GREEDY) {
-        int* cap = colok;
-        for (int64_t c = lane; c < GTo; c += 64) cap[c] = 0;
-        wave_sync();
-        for (int t = lane; t < nv; t += 64) cap[vcols[t]] = (int)K;
-        for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
-        wave_sync();
         greedy_wave(costL, Q, preds, (int)Q, vcols, nv, cap, p2g, thr);
       }
     }
@@ -598,16 +560,30 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       if (c >= 0 && !cost_ok((double)costL[c * Q + q], thr)) p2g[q] = -1;
     }
     wave_sync();
+    // compact the matched queries; rank each among those of its column
+    int nm = 0;
+    int* mq = preds;  // matched query list (preds no longer needed)
+    for (int64_t q0 = 0; q0 < Q; q0 += 64) {
+      const int64_t q = q0 + lane;
+      const bool mt = q < Q && p2g[q] >= 0;
+      const uint64_t m = __ballot(mt);
+      if (mt) mq[nm + __popcll(m & ((1ull << lane) - 1ull))] = (int)q;
+      nm += __popcll(m);
+    }
+    wave_sync();
     for (int64_t q = lane; q < Q; q += 64) {
       const int c = p2g[q];
       int64_t rnd = -1;
       if (c >= 0) {
-        const float cq = costL[c * Q + q];
         int64_t rank = 0;
-        for (int64_t q2 = 0; q2 < Q; ++q2) {
-          if (q2 == q || p2g[q2] != c) continue;
-          const float c2 = costL[c * Q + q2];
-          if (c2 < cq || (c2 == cq && q2 < q)) ++rank;
+        if (K > 1) {
+          const float cq = costL[c * Q + q];
+          for (int k = 0; k < nm; ++k) {
+            const int q2 = mq[k];
+            if (q2 == q || p2g[q2] != c) continue;
+            const float c2 = costL[c * Q + q2];
+            if (c2 < cq || (c2 == cq && q2 < q)) ++rank;
+          }
         }
         rnd = rank < K ? rank : -1;
       }
@@ -617,33 +593,34 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   }
   __syncthreads();
 
-  // ---- 4. matched-loss partial sums and backward statistics
+  // ---- 3. matched-loss partial sums and backward statistics
   const int* p2g = asg;
+  const bool need_cls_pen = a.force_cls || a.void_idx >= 0;
+  const int64_t rt_rows = a.rows;
+  const int64_t pstride = (a.L * a.B) * a.rtiles * 3 * a.rows * a.nslot;
   for (int64_t q = tid; q < Q; q += 256) {
     const int c = p2g[q];
+    const float* rs = a.rowstat + (lb * Q + q) * 8;
     float cm = 0.f, cd = 0.f, cc = 0.f, I = 0.f, T = 0.f;
     if (c >= 0) {
-      float bce, dice, cls;
-      pair_costs(x, q, c, bce, dice, cls);
-      cm = bce;
-      cd = dice;
-      cc = cls;
+      cm = sep[q * GTo + c];
+      cd = sep[term + q * GTo + c];
+      cc = sep[2 * term + q * GTo + c];
       const int slot = a.slot_of_col[b * GTo + c];
-      if (slot >= 0) {
-        const int64_t rt = q / a.rows, row = q % a.rows;
+      if (slot >= 0 && a.stats) {
+        const int64_t rt = q / rt_rows, rr = q % rt_rows;
+        const float* P0 = a.partials + (lb * a.rtiles + rt) * 3 * a.rows * a.nslot + rr * a.nslot + slot;
         for (int64_t ks = 0; ks < a.KS; ++ks) {
-          const float* Pp = a.partials +
-                            ((ks * (a.L * a.B) + lb) * a.rtiles + rt) * 3 * a.rows * a.nslot;
-          I += Pp[(1 * a.rows + row) * a.nslot + slot];
-          T += Pp[(2 * a.rows + row) * a.nslot + slot];
+          I += P0[ks * pstride + a.rows * a.nslot];
+          T += P0[ks * pstride + 2 * a.rows * a.nslot];
         }
       }
     } else {
       if (a.force_masks) {
-        cm = mPen[q];
-        cd = dPen[q];
+        cm = rs[2];
+        cd = rs[3];
       }
-      if (need_cls_pen) cc = clsPen[q];
+      if (need_cls_pen) cc = rs[4];
     }
     contrib[q * 4 + 0] = cm;
     contrib[q * 4 + 1] = cd;
@@ -651,8 +628,8 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
     contrib[q * 4 + 3] = c >= 0 ? 1.f : 0.f;
     if (a.stats) {
       float* st = a.stats + (lb * Q + q) * ML_STATS;
-      st[ML_STAT_S] = rowS[q];
-      st[ML_STAT_P] = rowP[q];
+      st[ML_STAT_S] = rs[0];
+      st[ML_STAT_P] = rs[1];
       st[ML_STAT_I] = I;
       st[ML_STAT_T] = T;
     }
@@ -678,6 +655,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
     }
   }
 }
+
 
 // Per-layer means and denominators (src/cuda/mask_matching_forward.cu:549-583).
 __global__ void layer_kernel(LayerArgs a) {
@@ -746,7 +724,17 @@ static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
   return check_launch("assign");
 }
 
+int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
+  const int64_t rows = d.LB * d.Q;
+  if (rows == 0) return ML_OK;
+  ProfScope ps_("finalize", st);
+  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, a);
+  return check_launch("finalize");
+}
+
 int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
+  int rc = launch_finalize(a, d, st);
+  if (rc || a.costs_only) return rc;
   const int64_t nj = ceil_div(a.Q, 64);
   if (nj <= 1) return launch_nj<1>(a, d, st);
   if (nj <= 2) return launch_nj<2>(a, d, st);

@@ -14,6 +14,7 @@
 namespace ml {
 
 static thread_local std::string g_err;
+int g_use_lut = 1;  // bf16 per-cell planes from the LDS table (0: formulas, for tests)
 
 void set_error(const std::string& msg) { g_err = msg; }
 int fail(int code, const std::string& msg) {
@@ -123,10 +124,12 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
   d.rows = 16 * d.RT;
   d.nslot = 16 * d.NT;
   d.rtiles = ceil_div(d.Q, d.rows);
+  // one wave per (image, row tile, K-split); aim for ~8 waves per CU and at
+  // least 8 K-steps per wave
   const int64_t nsteps = ceil_div(d.HW, kStep);
-  const int64_t per_ks = d.rtiles * d.LB * kWavesCost;
+  const int64_t per_ks = d.rtiles * d.LB;
   int64_t ks = per_ks > 0 ? ceil_div(2048, per_ks) : 1;
-  const int64_t ks_max = nsteps / (kWavesCost * 8) > 1 ? nsteps / (kWavesCost * 8) : 1;
+  const int64_t ks_max = nsteps / 8 > 1 ? nsteps / 8 : 1;
   if (ks > ks_max) ks = ks_max;
   if (ks < 1) ks = 1;
   d.KS = ks;
@@ -152,6 +155,8 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   const int64_t Qp = d.rtiles * d.rows;
   L.rowsum = take(force_masks ? (size_t)d.KS * d.LB * Qp * 2 * 4 : 0);
   L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
+  L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
+  L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
   L.img = take((size_t)d.LB * 4 * 4);
   L.layer = take((size_t)d.L * ML_LAYERS * 4);
   L.err = take(16);
@@ -235,6 +240,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   ca.L = d.L; ca.B = d.B; ca.Q = d.Q; ca.HW = d.HW; ca.HWp = d.HWp; ca.KS = d.KS;
   ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.Qp = d.rtiles * d.rows;
   ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;
+  ca.use_lut = g_use_lut;
   if (d.LB > 0 && d.rtiles > 0 && (rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
 
   const bool use_softmax = p->use_softmax_label_loss != 0;
@@ -248,7 +254,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.area = pa.area;
   aa.ncols = pa.ncols;
   aa.slot_of_col = pa.slot_of_col;
-  aa.sep = sep;
+  aa.sep = sep ? sep : (float*)(w + L.sep);
+  aa.rowstat = (float*)(w + L.rowstat);
   aa.costT = in_lds ? nullptr : (float*)(w + L.costT);
   aa.pred_to_gt = pred_to_gt;
   aa.pred_round = pred_round;

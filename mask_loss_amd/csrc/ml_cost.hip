@@ -9,14 +9,23 @@
 //   P = sum N2 w p (from the I plane) and S = sum N2 w (from the T plane).
 // This is the reference's fused BCE+dice reduction (src/cuda/pw_mask.cu:52-308)
 // rewritten as (Q x K)(K x G) products: bce*S = base + Delta of pw_mask.cu:300
-// regrouped as sum_{cells} w cn (N2-n) + w cp n (no cancellation between the
-// two terms), I and T as pw_mask.cu:270-271, P and S as pw_mask.cu:140-141.
+// regrouped as sum_{cells} w cn (N2-n) + w cp n (both terms non-negative, so no
+// cancellation), I and T as pw_mask.cu:270-271, P and S as pw_mask.cu:140-141.
 //
-// Layout: one workgroup = 4 waves sharing (image, row tile, K-split); each wave
-// owns every 4th 32-cell K-step, so the workgroup reads full cache lines of
-// every logit row.  Each wave keeps all column tiles of its rows in
-// accumulators; the four waves are reduced through LDS in a fixed order and
-// one partial per workgroup is written: partials[ks][lb][rtile][3][rows][nslot].
+// Work decomposition: one wave = 16*RT query rows of one image over a
+// contiguous range of 32-cell K-steps (K-split index = blockIdx.x); the four
+// waves of a workgroup take four consecutive (image, row-tile) tasks.  Each
+// image is handled by the kernel instance whose column-tile count NT matches
+// its number of non-empty GTs (+1 ones column), so accumulator registers are
+// sized to the image, not to the padded GT width.  Every wave writes its own
+// partial sums: partials[ks][lb][rtile][3][rows][nslot].
+//
+// Per-cell planes: bf16 logits take only 65536 values, so for them the four
+// planes are read from a per-workgroup LDS table built with the same float32
+// formulas (|z| in [2^-16, 64): one entry per bf16 value; |z| < 2^-16: the
+// z = 0 entry; a step holding any |z| >= 64, inf or nan falls back to the
+// formulas).  Other dtypes evaluate the formulas directly and split each
+// plane into NS bf16 terms so products keep float32 accuracy.
 #include "ml_internal.h"
 
 namespace ml {
@@ -25,57 +34,126 @@ template <int DT>
 struct InTraits;
 template <>
 struct InTraits<ML_F32> {
-  typedef float T;
   static constexpr int kSplit = 3;  // hi/mid/lo bf16 terms: fp32-equivalent products
 };
 template <>
 struct InTraits<ML_BF16> {
-  typedef uint16_t T;
   static constexpr int kSplit = 1;
 };
 template <>
 struct InTraits<ML_F16> {
-  typedef uint16_t T;
   static constexpr int kSplit = 2;
 };
 
-// Load 8 consecutive logits starting at element index i (row-major), zero the
-// ones at or beyond `lim` (end of the row).  `vec` = vector load allowed.
+// ---- LUT geometry (bytes): positive block at 0, negative block at 32768 ----
+constexpr uint32_t kLutBase = 111u << 7;         // bf16 magnitude bits of 2^-16
+constexpr uint32_t kLutOver = 0x4280u;           // bf16 magnitude bits of 64.0
+constexpr uint32_t kLutN = kLutOver - kLutBase;  // 2816 regular entries
+constexpr uint32_t kLutSub = kLutBase - 1;       // idx = sat(m - kLutSub): 0 = tiny
+constexpr uint32_t kLutBlock = kLutN + 2;        // tiny + regular + overflow slot
+constexpr uint32_t kLutNegOff = 32768;
+constexpr uint32_t kLutBytes = kLutNegOff + kLutBlock * 8;
+
+__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_pk_max_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ uint32_t pk_lshl3_u16(uint32_t a) {
+  uint32_t r;
+  asm("v_pk_lshlrev_b16 %0, %1, %2" : "=v"(r) : "v"(0x00030003u), "v"(a));
+  return r;
+}
+
+// The four planes of one logit from the float32 formulas (+ the unweighted
+// terms of the unmatched-mask penalty).
+__device__ __forceinline__ void planes_formula(float z, const ElemParams& ep, float& neg,
+                                               float& pos, float& wp, float& w, float& negu,
+                                               float& pu) {
+  const Sig s = sig_terms(z);
+  w = unc_weight(s, ep);
+  float mn, mp;
+  focal_mods(s, ep, mn, mp);
+  negu = ep.an * mn * s.cn;
+  pu = s.p;
+  neg = w * negu;
+  pos = w * (ep.ap * mp * s.cp);
+  wp = w * s.p;
+}
+
+// Build the LUT in LDS (all threads of the workgroup).
+__device__ void build_lut(unsigned char* lut, const ElemParams& ep) {
+  for (uint32_t e = threadIdx.x; e < 2 * kLutBlock; e += blockDim.x) {
+    const uint32_t sgn = e >= kLutBlock ? 1u : 0u;
+    const uint32_t j = e - sgn * kLutBlock;
+    uint32_t mag;
+    if (j == 0) mag = 0;                          // |z| < 2^-16 -> z = 0
+    else if (j <= kLutN) mag = kLutSub + j;       // exact bf16 value
+    else mag = kLutOver;                          // unused overflow slot
+    const float z = __uint_as_float(((sgn << 15) | mag) << 16);
+    float neg, pos, wp, w, nu, pu;
+    planes_formula(z, ep, neg, pos, wp, w, nu, pu);
+    uint2 v;
+    v.x = pack_bf16x2(neg, pos);
+    v.y = pack_bf16x2(wp, w);
+    *(uint2*)(lut + sgn * kLutNegOff + j * 8) = v;
+  }
+}
+
+// 8 consecutive logits of one row as raw words.
 template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t i, int64_t nvalid, bool vec,
-                                      float z[8]) {
-  if (DT == ML_F32) {
-    const float* p = (const float*)base + i;
-    if (vec && nvalid >= 8) {
-      const float4 v0 = *(const float4*)p;
-      const float4 v1 = *(const float4*)(p + 4);
-      z[0] = v0.x; z[1] = v0.y; z[2] = v0.z; z[3] = v0.w;
-      z[4] = v1.x; z[5] = v1.y; z[6] = v1.z; z[7] = v1.w;
+struct Raw8 {
+  uint4 w[DT == ML_F32 ? 2 : 1];
+};
+
+// `vec`: rows start 16-byte aligned (HW % 4 == 0 for float32, HW % 8 == 0
+// otherwise); else the 8 values are read one by one.
+template <int DT>
+__device__ __forceinline__ void load_raw8(const void* base, int64_t i, Raw8<DT>& r, bool vec) {
+  if constexpr (DT == ML_F32) {
+    const float* f = (const float*)base + i;
+    if (vec) {
+      r.w[0] = ((const uint4*)f)[0];
+      r.w[1] = ((const uint4*)f)[1];
     } else {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) z[k] = k < nvalid ? p[k] : 0.f;
+      r.w[0] = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                          __float_as_uint(f[3]));
+      r.w[1] = make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]),
+                          __float_as_uint(f[7]));
     }
   } else {
-    const uint16_t* p = (const uint16_t*)base + i;
-    if (vec && nvalid >= 8) {
-      const uint4 v = *(const uint4*)p;
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (DT == ML_BF16) {
-          z[2 * k] = bf16_lo(w4[k]);
-          z[2 * k + 1] = bf16_hi(w4[k]);
-        } else {
-          z[2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[k] & 0xFFFF));
-          z[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w4[k] >> 16));
-        }
-      }
+    const uint16_t* h = (const uint16_t*)base + i;
+    if (vec) {
+      r.w[0] = *(const uint4*)h;
     } else {
+      r.w[0] = make_uint4((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
+                          (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16));
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void raw_to_f32(const Raw8<DT>& r, float z[8]) {
+  if constexpr (DT == ML_F32) {
+    const uint32_t u[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w,
+                           r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint16_t h = k < nvalid ? p[k] : (uint16_t)0;
-        z[k] = DT == ML_BF16 ? __uint_as_float(((uint32_t)h) << 16)
-                             : (float)__builtin_bit_cast(_Float16, h);
+    for (int k = 0; k < 8; ++k) z[k] = __uint_as_float(u[k]);
+  } else {
+    const uint32_t u[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (DT == ML_BF16) {
+        z[2 * k] = bf16_lo(u[k]);
+        z[2 * k + 1] = bf16_hi(u[k]);
+      } else {
+        z[2 * k] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[k] & 0xFFFF));
+        z[2 * k + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u[k] >> 16));
       }
     }
   }
@@ -103,26 +181,92 @@ __device__ __forceinline__ void split_pack(const float v[8], bf16x8_t out[NS]) {
   }
 }
 
-template <int NT, int RT>
-struct CostShape {
-  static constexpr int kAcc = 3 * RT * NT;  // f32x4 accumulators per lane
-};
+// A planes of one row's 8 cells by formula; with MASK, cells >= nvalid are zero.
+template <int DT, int NS, bool MASK>
+__device__ __forceinline__ void planes8_formula(const Raw8<DT>& r, const ElemParams& ep,
+                                                int64_t nvalid, bool unw, bf16x8_t A[4][NS],
+                                                float& ub, float& up) {
+  float z[8];
+  raw_to_f32<DT>(r, z);
+  float v[4][8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    float neg, pos, wp, w, nu, pu;
+    planes_formula(z[k], ep, neg, pos, wp, w, nu, pu);
+    const bool ok = !MASK || k < nvalid;
+    v[0][k] = ok ? neg : 0.f;
+    v[1][k] = ok ? pos : 0.f;
+    v[2][k] = ok ? wp : 0.f;
+    v[3][k] = ok ? w : 0.f;
+    if (unw) {
+      ub += ok ? nu : 0.f;
+      up += ok ? pu : 0.f;
+    }
+  }
+#pragma unroll
+  for (int pl = 0; pl < 4; ++pl) split_pack<NS>(v[pl], A[pl]);
+}
+
+// A planes of one row's 8 bf16 cells from the LDS table.
+__device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char* lut,
+                                            bf16x8_t A[4]) {
+  const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+  u32x4_t a0, a1, a2, a3;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t m = u[i] & 0x7FFF7FFFu;
+    const uint32_t idx =
+        pk_min_u16(pk_sub_sat_u16(m, kLutSub * 0x10001u), (kLutN + 1) * 0x10001u);
+    const uint32_t addr = (u[i] & 0x80008000u) | pk_lshl3_u16(idx);
+    const uint2 e0 = *(const uint2*)(lut + (addr & 0xFFFFu));
+    const uint2 e1 = *(const uint2*)(lut + (addr >> 16));
+    a0[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x05040100u);
+    a1[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x07060302u);
+    a2[i] = __builtin_amdgcn_perm(e1.y, e0.y, 0x05040100u);
+    a3[i] = __builtin_amdgcn_perm(e1.y, e0.y, 0x07060302u);
+  }
+  A[0] = __builtin_bit_cast(bf16x8_t, a0);
+  A[1] = __builtin_bit_cast(bf16x8_t, a1);
+  A[2] = __builtin_bit_cast(bf16x8_t, a2);
+  A[3] = __builtin_bit_cast(bf16x8_t, a3);
+}
+
+// true if any of the 8 bf16 values needs the formulas (|z| >= 64, inf, nan)
+__device__ __forceinline__ bool lut_overflow(const uint4& x) {
+  const uint32_t m = pk_max_u16(pk_max_u16(x.x & 0x7FFF7FFFu, x.y & 0x7FFF7FFFu),
+                                pk_max_u16(x.z & 0x7FFF7FFFu, x.w & 0x7FFF7FFFu));
+  return max(m & 0xFFFFu, m >> 16) >= kLutOver;
+}
+
+// Column-tile count class of an image: smallest instantiated NT >= need.
+__host__ __device__ inline int nt_class(int ncols_plus_one) {
+  const int need = (ncols_plus_one + 15) >> 4;
+  return need <= 2 ? 2 : need <= 4 ? 4 : need <= 7 ? 7 : 16;
+}
 
 template <int DT, int RT, int NT, bool CNT>
 __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
   constexpr int NS = InTraits<DT>::kSplit;
-  constexpr int NACC = CostShape<NT, RT>::kAcc;
-  __shared__ float red[NACC * 4 * 64];
-  __shared__ float red_unw[2 * RT * 16 * 4];
+  constexpr bool LUT = DT == ML_BF16;
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 15, g4 = lane >> 4;
-  const int64_t lb = blockIdx.z, b = lb % a.B;
-  const int64_t q0 = (int64_t)blockIdx.y * (16 * RT);
-  const int64_t ks = blockIdx.x;
-  const int G = a.ncols[b];
-  const int nt_used = (G + 1 + 15) >> 4;
+  const ElemParams ep = a.ep;
   const bool unw = a.rowsum != nullptr;
+  const bool use_lut = LUT && a.use_lut && !unw;
+  if (use_lut) {
+    build_lut(smem, ep);
+    __syncthreads();
+  }
+
+  const int64_t task = (int64_t)blockIdx.y * kWavesCost + wave;
+  if (task >= a.L * a.B * a.rtiles) return;
+  const int64_t lb = task / a.rtiles, rtile = task % a.rtiles, b = lb % a.B;
+  const int G = a.ncols[b];
+  if (nt_class(G + 1) != NT) return;
+  const int nt_used = (G + 1 + 15) >> 4;
+  const int64_t q0 = rtile * (16 * RT);
 
   // per-lane column operands.  Tiles below the boundary tile hold real GT
   // columns only (constant operand coefficients); the boundary tile mixes
@@ -153,60 +297,35 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
       for (int nt = 0; nt < NT; ++nt) acc[i][rt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float ub[RT], up[RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) { ub[rt] = 0.f; up[rt] = 0.f; }
+  for (int rt = 0; rt < RT; ++rt) {
+    ub[rt] = 0.f;
+    up[rt] = 0.f;
+  }
 
-  const ElemParams ep = a.ep;
-  const bool vec_ok = DT == ML_F32 ? (a.HW % 4 == 0) : (a.HW % 8 == 0);
-  const int64_t nsteps = ceil_div(a.HW, kStep);
-  const int64_t stride = a.KS * kWavesCost;
+  // this wave's K-steps: [s0, s1) of the full steps, plus the tail step
+  const int64_t full = a.HW / kStep;
+  const int64_t per = ceil_div(full, a.KS);
+  const int64_t s0 = min(full, (int64_t)blockIdx.x * per);
+  const int64_t s1 = min(full, s0 + per);
+  const bool has_tail = (a.HW % kStep) != 0 && (int64_t)blockIdx.x == a.KS - 1;
 
-  for (int64_t st = ks * kWavesCost + wave; st < nsteps; st += stride) {
-    const int64_t cell0 = st * kStep + g4 * 8;
-    const int64_t nvalid = a.HW - cell0;  // may be <= 0 in the tail
-
-    // ---- A planes for RT row tiles
-    bf16x8_t A[4][RT][NS];
+  int64_t rowoff[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const int64_t q = q0 + rt * 16 + r;
-      const bool row_ok = q < a.Q;
-      const int64_t qc = row_ok ? q : a.Q - 1;
-      float z[8];
-      load8<DT>(a.logits, (lb * a.Q + qc) * a.HW + cell0, row_ok ? nvalid : 0, vec_ok, z);
-      float v[4][8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const bool ok = row_ok && k < nvalid;
-        const Sig s = sig_terms(z[k]);
-        const float w = unc_weight(s, ep);
-        float mn, mp;
-        focal_mods(s, ep, mn, mp);
-        const float neg = ep.an * mn * s.cn;
-        v[0][k] = ok ? w * neg : 0.f;
-        v[1][k] = ok ? w * (ep.ap * mp * s.cp) : 0.f;
-        v[2][k] = ok ? w * s.p : 0.f;
-        v[3][k] = ok ? w : 0.f;
-        if (unw) {
-          ub[rt] += ok ? neg : 0.f;
-          up[rt] += ok ? s.p : 0.f;
-        }
-      }
-#pragma unroll
-      for (int pl = 0; pl < 4; ++pl) split_pack<NS>(v[pl], A[pl][rt]);
-    }
+  for (int rt = 0; rt < RT; ++rt) {
+    const int64_t q = min(q0 + rt * 16 + r, a.Q - 1);  // rows >= Q compute unused outputs
+    rowoff[rt] = (lb * a.Q + q) * a.HW + g4 * 8;
+  }
+  const uint16_t* labp = a.lab16 + b * a.HWp + g4 * 8;
+  const bool vec = DT == ML_F32 ? (a.HW % 4 == 0) : (a.HW % 8 == 0);
 
-    // ---- target operands per column tile, then MFMA
-    uint32_t L2[4];
-    if (!CNT) {
-      const uint4 lv = *(const uint4*)(a.lab16 + b * a.HWp + cell0);
-      L2[0] = lv.x; L2[1] = lv.y; L2[2] = lv.z; L2[3] = lv.w;
-    }
+  auto mma_step = [&](bf16x8_t (&A)[4][RT][NS], const uint4& lv, int64_t cell0) {
+    const uint32_t L2[4] = {lv.x, lv.y, lv.z, lv.w};
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if (nt >= nt_used) continue;
       u32x4_t bp, bv;
       const bool last = nt == nt_last;
-      if (!CNT) {
+      if constexpr (!CNT) {
         const uint32_t coef = last ? coef_last : 0x3F803F80u;
         const uint32_t base = last ? base_last : 0x3F803F80u;
 #pragma unroll
@@ -245,64 +364,111 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
         }
       }
     }
-  }
+  };
 
-  // ---- deterministic cross-wave reduction: wave 3 -> 2 -> 1 -> 0
-  for (int w = kWavesCost - 1; w >= 1; --w) {
-    if (wave == w) {
-      int idx = 0;
+  if (s0 < s1) {
+    Raw8<DT> cur[RT], nxt[RT];
+    uint4 lcur, lnxt;
 #pragma unroll
-      for (int i = 0; i < 3; ++i)
+    for (int rt = 0; rt < RT; ++rt) load_raw8<DT>(a.logits, rowoff[rt] + s0 * kStep, cur[rt], vec);
+    lcur = *(const uint4*)(labp + s0 * kStep);
+    for (int64_t st = s0; st < s1; ++st) {
+      if (st + 1 < s1) {  // prefetch the next step
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
+          load_raw8<DT>(a.logits, rowoff[rt] + (st + 1) * kStep, nxt[rt], vec);
+        lnxt = *(const uint4*)(labp + (st + 1) * kStep);
+      }
+      bf16x8_t A[4][RT][NS];
+      bool slow = true;
+      if (use_lut) {
+        bool ov = false;
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt)
+        for (int rt = 0; rt < RT; ++rt) ov |= lut_overflow(cur[rt].w[0]);
+        slow = __ballot(ov) != 0;
+      }
+      if (!slow) {
+        if constexpr (LUT) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e, ++idx) {
-              float v = acc[i][rt][nt][e];
-              if (w < kWavesCost - 1) v += red[idx * 64 + lane];
-              red[idx * 64 + lane] = v;
-            }
-      if (unw) {
+          for (int rt = 0; rt < RT; ++rt) {
+            bf16x8_t T[4];
+            planes8_lut(cur[rt].w[0], smem, T);
+#pragma unroll
+            for (int pl = 0; pl < 4; ++pl) A[pl][rt][0] = T[pl];
+          }
+        }
+      } else {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-          float vb = ub[rt], vp = up[rt];
-          if (w < kWavesCost - 1) {
-            vb += red_unw[(rt * 2 + 0) * 64 + lane];
-            vp += red_unw[(rt * 2 + 1) * 64 + lane];
-          }
-          red_unw[(rt * 2 + 0) * 64 + lane] = vb;
-          red_unw[(rt * 2 + 1) * 64 + lane] = vp;
+          bf16x8_t T[4][NS];
+          planes8_formula<DT, NS, false>(cur[rt], ep, 8, unw, T, ub[rt], up[rt]);
+#pragma unroll
+          for (int pl = 0; pl < 4; ++pl)
+#pragma unroll
+            for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
         }
       }
+      mma_step(A, lcur, st * kStep + g4 * 8);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) cur[rt] = nxt[rt];
+      lcur = lnxt;
     }
-    __syncthreads();
   }
-  if (wave != 0) return;
+  if (has_tail) {  // last partial step: guarded loads, masked planes
+    const int64_t st = full;
+    const int64_t cell0 = st * kStep + g4 * 8;
+    const int64_t nvalid = a.HW - cell0;
+    bf16x8_t A[4][RT][NS];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      Raw8<DT> raw;
+      uint32_t u[DT == ML_F32 ? 8 : 4];
+      const int64_t i0 = rowoff[rt] + st * kStep;
+#pragma unroll
+      for (int k = 0; k < (DT == ML_F32 ? 8 : 4); ++k) u[k] = 0;
+      if constexpr (DT == ML_F32) {
+        for (int k = 0; k < 8; ++k)
+          if (k < nvalid) u[k] = __float_as_uint(((const float*)a.logits)[i0 + k]);
+        raw.w[0] = make_uint4(u[0], u[1], u[2], u[3]);
+        raw.w[1] = make_uint4(u[4], u[5], u[6], u[7]);
+      } else {
+        for (int k = 0; k < 8; ++k)
+          if (k < nvalid)
+            u[k >> 1] |= (uint32_t)((const uint16_t*)a.logits)[i0 + k] << ((k & 1) * 16);
+        raw.w[0] = make_uint4(u[0], u[1], u[2], u[3]);
+      }
+      bf16x8_t T[4][NS];
+      planes8_formula<DT, NS, true>(raw, ep, nvalid, unw, T, ub[rt], up[rt]);
+#pragma unroll
+      for (int pl = 0; pl < 4; ++pl)
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
+    }
+    const uint4 lv = *(const uint4*)(labp + st * kStep);
+    mma_step(A, lv, cell0);
+  }
 
-  const int64_t rows = 16 * RT;
-  float* out = a.partials + ((ks * (a.L * a.B) + lb) * a.rtiles + blockIdx.y) * 3 * rows * a.nslot;
-  {
-    int idx = 0;
+  // ---- write this wave's partial sums (only the tiles in use)
+  const int rows = 16 * RT;
+  float* out = a.partials +
+               (((int64_t)blockIdx.x * (a.L * a.B) + lb) * a.rtiles + rtile) * 3 * rows * a.nslot;
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
+  for (int i = 0; i < 3; ++i)
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+      for (int nt = 0; nt < NT; ++nt) {
+        if (nt >= nt_used) continue;
 #pragma unroll
-          for (int e = 0; e < 4; ++e, ++idx) {
-            const float v = acc[i][rt][nt][e] + red[idx * 64 + lane];
-            const int row = rt * 16 + g4 * 4 + e;
-            const int slot = nt * 16 + r;
-            out[(i * rows + row) * a.nslot + slot] = v;
-          }
-  }
+        for (int e = 0; e < 4; ++e) {
+          const int row = rt * 16 + g4 * 4 + e;
+          out[(i * rows + row) * a.nslot + nt * 16 + r] = acc[i][rt][nt][e];
+        }
+      }
   if (unw) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      float vb = ub[rt] + red_unw[(rt * 2 + 0) * 64 + lane];
-      float vp = up[rt] + red_unw[(rt * 2 + 1) * 64 + lane];
+      float vb = ub[rt], vp = up[rt];
       // lanes r, r+16, r+32, r+48 hold the same row: fixed-order pair sums
       vb += __shfl_xor(vb, 16, 64);
       vp += __shfl_xor(vp, 16, 64);
@@ -310,7 +476,7 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
       vp += __shfl_xor(vp, 32, 64);
       const int64_t q = q0 + rt * 16 + r;
       if (g4 == 0 && q < a.Q) {
-        float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
+        float* rs = a.rowsum + (((int64_t)blockIdx.x * (a.L * a.B) + lb) * a.Qp + q) * 2;
         rs[0] = vb;
         rs[1] = vp;
       }
@@ -319,32 +485,40 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
 }
 
 template <int DT, int RT, int NT>
-static void launch_one(const CostArgs& a, const Dims& d, hipStream_t st) {
-  const dim3 grid((unsigned)d.KS, (unsigned)d.rtiles, (unsigned)d.LB);
-  ProfScope ps_("pair_cost", st);
+static int launch_one(const CostArgs& a, const Dims& d, hipStream_t st) {
+  const int64_t tasks = d.LB * d.rtiles;
+  const dim3 grid((unsigned)d.KS, (unsigned)ceil_div(tasks, kWavesCost));
+  const bool lut = DT == ML_BF16 && a.use_lut && a.rowsum == nullptr;
+  const size_t lds = lut ? kLutBytes : 0;
   if (d.counts_mode)
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true>), grid, dim3(256), lds, st, a);
   else
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false>), grid, dim3(256), 0, st, a);
-}
-
-template <int DT>
-static int launch_dt(const CostArgs& a, const Dims& d, hipStream_t st) {
-  if (d.NT <= 2) launch_one<DT, 1, 2>(a, d, st);
-  else if (d.NT <= 4) launch_one<DT, 1, 4>(a, d, st);
-  else if (d.NT <= 7) launch_one<DT, 1, 7>(a, d, st);
-  else if (d.NT <= 16) launch_one<DT, 1, 16>(a, d, st);
-  else return fail(ML_EUNSUPPORTED, "more than 255 GT columns per image are not supported");
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false>), grid, dim3(256), lds, st, a);
   return check_launch("pair_cost");
 }
 
-int cost_rt_for(int, int) { return 1; }
+// One launch per column-tile class up to the padded width; each image is
+// processed by exactly one of them.
+template <int DT, int RT>
+static int launch_classes(const CostArgs& a, const Dims& d, hipStream_t st) {
+  int rc = launch_one<DT, RT, 2>(a, d, st);
+  if (!rc && d.NT >= 4) rc = launch_one<DT, RT, 4>(a, d, st);
+  if (!rc && d.NT >= 7) rc = launch_one<DT, RT, 7>(a, d, st);
+  if constexpr (RT == 1) {
+    if (!rc && d.NT >= 16) rc = launch_one<DT, 1, 16>(a, d, st);
+  }
+  return rc;
+}
+
+int cost_rt_for(int dtype, int NT) { return (dtype == ML_BF16 && NT < 16) ? 2 : 1; }
 
 int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool, hipStream_t st) {
+  ProfScope ps_("pair_cost", st);
   switch (dtype) {
-    case ML_F32: return launch_dt<ML_F32>(a, d, st);
-    case ML_BF16: return launch_dt<ML_BF16>(a, d, st);
-    case ML_F16: return launch_dt<ML_F16>(a, d, st);
+    case ML_F32: return launch_classes<ML_F32, 1>(a, d, st);
+    case ML_BF16:
+      return d.RT == 2 ? launch_classes<ML_BF16, 2>(a, d, st) : launch_classes<ML_BF16, 1>(a, d, st);
+    case ML_F16: return launch_classes<ML_F16, 1>(a, d, st);
   }
   return fail(ML_EINVAL, "unsupported mask logits dtype");
 }

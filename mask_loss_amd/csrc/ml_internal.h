@@ -44,7 +44,7 @@ int cost_rt_for(int dtype, int NT);
 // Byte offsets inside the caller's workspace.
 struct Layout {
   size_t lab16, counts8, area, ncols, colmap, slot_of_col, partials, rowsum,
-      costT, img, layer, err, total;
+      costT, sep, rowstat, img, layer, err, total;
 };
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
 
@@ -73,6 +73,7 @@ struct CostArgs {
   int nslot;
   float N2;
   ElemParams ep;
+  int use_lut;       // bf16 logits: per-cell planes from the LDS table
 };
 
 struct AssignArgs {
@@ -91,6 +92,7 @@ struct AssignArgs {
   int64_t* pred_to_gt;   // (L,B,Q) or null (costs-only mode)
   int64_t* pred_round;
   float* stats;          // (L,B,Q,ML_STATS) or null
+  float* rowstat;        // [LB*Q][8]: S, P, mask pen, dice pen, cls pen
   float* img;            // [LB][4]: mask, dice, cls sums, matched count
   int* err;
   // dims / params

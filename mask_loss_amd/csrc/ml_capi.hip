@@ -154,6 +154,7 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   L.partials = take((size_t)d.KS * d.LB * d.rtiles * 3 * d.rows * d.nslot * 4);
   const int64_t Qp = d.rtiles * d.rows;
   L.rowsum = take(force_masks ? (size_t)d.KS * d.LB * Qp * 2 * 4 : 0);
+  L.flags = take((size_t)d.KS * d.LB * d.rtiles * 4);
   L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
@@ -237,6 +238,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   ca.colmap = pa.colmap;
   ca.partials = (float*)(w + L.partials);
   ca.rowsum = force_masks ? (float*)(w + L.rowsum) : nullptr;
+  ca.flags = (int*)(w + L.flags);
   ca.L = d.L; ca.B = d.B; ca.Q = d.Q; ca.HW = d.HW; ca.HWp = d.HWp; ca.KS = d.KS;
   ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.Qp = d.rtiles * d.rows;
   ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;

@@ -23,9 +23,11 @@
 // Per-cell planes: bf16 logits take only 65536 values, so for them the four
 // planes are read from a per-workgroup LDS table built with the same float32
 // formulas (|z| in [2^-16, 64): one entry per bf16 value; |z| < 2^-16: the
-// z = 0 entry; a step holding any |z| >= 64, inf or nan falls back to the
-// formulas).  Other dtypes evaluate the formulas directly and split each
+// z = 0 entry; |z| >= 64, inf and nan read a NaN marker, and a wave whose
+// sums come out NaN is redone with the formulas by a fix-up launch).  Other dtypes evaluate the formulas directly and split each
 // plane into NS bf16 terms so products keep float32 accuracy.
+#include <algorithm>
+
 #include "ml_internal.h"
 
 namespace ml {
@@ -53,15 +55,11 @@ constexpr uint32_t kLutSub = kLutBase - 1;       // idx = sat(m - kLutSub): 0 = 
 constexpr uint32_t kLutBlock = kLutN + 2;        // tiny + regular + overflow slot
 constexpr uint32_t kLutNegOff = 32768;
 constexpr uint32_t kLutBytes = kLutNegOff + kLutBlock * 8;
+constexpr int kDepth = 4;  // K-steps of logits in flight per wave
 
 __device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
   uint32_t r;
   asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_max_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   return r;
 }
 __device__ __forceinline__ uint32_t pk_lshl3_u16(uint32_t a) {
@@ -86,21 +84,26 @@ __device__ __forceinline__ void planes_formula(float z, const ElemParams& ep, fl
   wp = w * s.p;
 }
 
-// Build the LUT in LDS (all threads of the workgroup).
+// Build the LUT in LDS (all threads of the workgroup).  The overflow slot
+// holds NaN so that a wave whose sums come out NaN knows it met |z| >= 64,
+// inf or nan (finite table entries cannot produce NaN) and redoes its K-range
+// with the formulas.
 __device__ void build_lut(unsigned char* lut, const ElemParams& ep) {
   for (uint32_t e = threadIdx.x; e < 2 * kLutBlock; e += blockDim.x) {
     const uint32_t sgn = e >= kLutBlock ? 1u : 0u;
     const uint32_t j = e - sgn * kLutBlock;
-    uint32_t mag;
-    if (j == 0) mag = 0;                          // |z| < 2^-16 -> z = 0
-    else if (j <= kLutN) mag = kLutSub + j;       // exact bf16 value
-    else mag = kLutOver;                          // unused overflow slot
-    const float z = __uint_as_float(((sgn << 15) | mag) << 16);
-    float neg, pos, wp, w, nu, pu;
-    planes_formula(z, ep, neg, pos, wp, w, nu, pu);
     uint2 v;
-    v.x = pack_bf16x2(neg, pos);
-    v.y = pack_bf16x2(wp, w);
+    if (j <= kLutN) {
+      const uint32_t mag = j == 0 ? 0u : kLutSub + j;  // j == 0: |z| < 2^-16 -> z = 0
+      const float z = __uint_as_float(((sgn << 15) | mag) << 16);
+      float neg, pos, wp, w, nu, pu;
+      planes_formula(z, ep, neg, pos, wp, w, nu, pu);
+      v.x = pack_bf16x2(neg, pos);
+      v.y = pack_bf16x2(wp, w);
+    } else {
+      v.x = 0x7FC07FC0u;  // NaN marker
+      v.y = 0x7FC07FC0u;
+    }
     *(uint2*)(lut + sgn * kLutNegOff + j * 8) = v;
   }
 }
@@ -231,56 +234,43 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
   A[3] = __builtin_bit_cast(bf16x8_t, a3);
 }
 
-// true if any of the 8 bf16 values needs the formulas (|z| >= 64, inf, nan)
-__device__ __forceinline__ bool lut_overflow(const uint4& x) {
-  const uint32_t m = pk_max_u16(pk_max_u16(x.x & 0x7FFF7FFFu, x.y & 0x7FFF7FFFu),
-                                pk_max_u16(x.z & 0x7FFF7FFFu, x.w & 0x7FFF7FFFu));
-  return max(m & 0xFFFFu, m >> 16) >= kLutOver;
-}
-
 // Column-tile count class of an image: smallest instantiated NT >= need.
 __host__ __device__ inline int nt_class(int ncols_plus_one) {
   const int need = (ncols_plus_one + 15) >> 4;
   return need <= 2 ? 2 : need <= 4 ? 4 : need <= 7 ? 7 : 16;
 }
 
-template <int DT, int RT, int NT, bool CNT>
-__global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
+// One wave's work: 16*RT query rows of task (lb, rtile) over the K-steps of
+// split `ks`.  TAB: per-cell planes from the LDS table (bf16 only); returns
+// true if the sums came out NaN, i.e. some cell hit the table's overflow
+// marker, in which case the partial sums written are unusable and the
+// caller redoes the wave with TAB = false.
+template <int DT, int RT, int NT, bool CNT, bool TAB>
+__device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
+                                          int64_t ks, const unsigned char* lut) {
   constexpr int NS = InTraits<DT>::kSplit;
-  constexpr bool LUT = DT == ML_BF16;
-  extern __shared__ __align__(16) unsigned char smem[];
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int D = TAB ? kDepth : 2;  // K-steps of logits and labels in flight
+  const int lane = threadIdx.x & 63;
   const int r = lane & 15, g4 = lane >> 4;
   const ElemParams ep = a.ep;
-  const bool unw = a.rowsum != nullptr;
-  const bool use_lut = LUT && a.use_lut && !unw;
-  if (use_lut) {
-    build_lut(smem, ep);
-    __syncthreads();
-  }
-
-  const int64_t task = (int64_t)blockIdx.y * kWavesCost + wave;
-  if (task >= a.L * a.B * a.rtiles) return;
-  const int64_t lb = task / a.rtiles, rtile = task % a.rtiles, b = lb % a.B;
+  const bool unw = !TAB && a.rowsum != nullptr;
+  const int64_t b = lb % a.B;
   const int G = a.ncols[b];
-  if (nt_class(G + 1) != NT) return;
   const int nt_used = (G + 1 + 15) >> 4;
   const int64_t q0 = rtile * (16 * RT);
 
-  // per-lane column operands.  Tiles below the boundary tile hold real GT
-  // columns only (constant operand coefficients); the boundary tile mixes
-  // real columns, the ones column (slot G) and padding.
-  uint32_t colL[NT];
-  const int nt_last = nt_used - 1;
-  const int slot_b = nt_last * 16 + r;
+  // per-lane column operands: label pair, and the coefficients that turn the
+  // match bit into the one-hot (B) and complement (B') bf16 operands.  Real
+  // columns: B = 1 on match, B' = 1 elsewhere; ones column (slot G): B = N2,
+  // B' = 0; padding: both 0.
+  uint32_t colL[NT], coefB[NT], baseB[NT];
   const uint32_t n2pair = pack_bf16x2(a.N2, a.N2);
-  const uint32_t base_last = slot_b < G ? 0x3F803F80u : (slot_b == G ? n2pair : 0u);
-  const uint32_t coef_last = slot_b < G ? 0x3F803F80u : 0u;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int slot = nt * 16 + r;
     colL[nt] = 0;
+    coefB[nt] = slot < G ? 0x3F803F80u : 0u;
+    baseB[nt] = slot < G ? 0x3F803F80u : (slot == G ? n2pair : 0u);
     if (slot < G) {
       const int c = a.colmap[b * a.nslot + slot];
       const int act = c + (c >= a.bg ? 1 : 0);
@@ -305,9 +295,9 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
   // this wave's K-steps: [s0, s1) of the full steps, plus the tail step
   const int64_t full = a.HW / kStep;
   const int64_t per = ceil_div(full, a.KS);
-  const int64_t s0 = min(full, (int64_t)blockIdx.x * per);
+  const int64_t s0 = min(full, ks * per);
   const int64_t s1 = min(full, s0 + per);
-  const bool has_tail = (a.HW % kStep) != 0 && (int64_t)blockIdx.x == a.KS - 1;
+  const bool has_tail = (a.HW % kStep) != 0 && ks == a.KS - 1;
 
   int64_t rowoff[RT];
 #pragma unroll
@@ -324,15 +314,12 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
     for (int nt = 0; nt < NT; ++nt) {
       if (nt >= nt_used) continue;
       u32x4_t bp, bv;
-      const bool last = nt == nt_last;
       if constexpr (!CNT) {
-        const uint32_t coef = last ? coef_last : 0x3F803F80u;
-        const uint32_t base = last ? base_last : 0x3F803F80u;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t m = pk_min_u16(L2[i] ^ colL[nt], 0x00010001u);
-          bp[i] = pk_mul_lo_u16(m, coef);
-          bv[i] = pk_sub_u16(base, bp[i]);
+          bp[i] = pk_mul_lo_u16(m, coefB[nt]);
+          bv[i] = pk_sub_u16(baseB[nt], bp[i]);
         }
       } else {
         const int slot = nt * 16 + r;
@@ -367,53 +354,68 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
   };
 
   if (s0 < s1) {
-    Raw8<DT> cur[RT], nxt[RT];
-    uint4 lcur, lnxt;
+    Raw8<DT> buf[D][RT];
+    uint4 lbuf[D];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) load_raw8<DT>(a.logits, rowoff[rt] + s0 * kStep, cur[rt], vec);
-    lcur = *(const uint4*)(labp + s0 * kStep);
-    for (int64_t st = s0; st < s1; ++st) {
-      if (st + 1 < s1) {  // prefetch the next step
+    for (int j = 0; j < D; ++j) {
+      if (s0 + j < s1) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
-          load_raw8<DT>(a.logits, rowoff[rt] + (st + 1) * kStep, nxt[rt], vec);
-        lnxt = *(const uint4*)(labp + (st + 1) * kStep);
+          load_raw8<DT>(a.logits, rowoff[rt] + (s0 + j) * kStep, buf[j][rt], vec);
+        lbuf[j] = *(const uint4*)(labp + (s0 + j) * kStep);
       }
-      bf16x8_t A[4][RT][NS];
-      bool slow = true;
-      if (use_lut) {
-        bool ov = false;
+    }
+    for (int64_t sb = s0; sb < s1; sb += D) {
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) ov |= lut_overflow(cur[rt].w[0]);
-        slow = __ballot(ov) != 0;
-      }
-      if (!slow) {
-        if constexpr (LUT) {
+      for (int j = 0; j < D; ++j) {
+        const int64_t st = sb + j;
+        if (st < s1) {
+          Raw8<DT> cur[RT];
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) cur[rt] = buf[j][rt];
+          const uint4 lcur = lbuf[j];
+          if (st + D < s1) {  // refill this slot with step st + D
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+              load_raw8<DT>(a.logits, rowoff[rt] + (st + D) * kStep, buf[j][rt], vec);
+            lbuf[j] = *(const uint4*)(labp + (st + D) * kStep);
+          }
+          bf16x8_t A[4][RT][NS];
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt) {
-            bf16x8_t T[4];
-            planes8_lut(cur[rt].w[0], smem, T);
+            bf16x8_t T[4][NS];
+            if constexpr (TAB) {
+              bf16x8_t T1[4];
+              planes8_lut(cur[rt].w[0], lut, T1);
 #pragma unroll
-            for (int pl = 0; pl < 4; ++pl) A[pl][rt][0] = T[pl];
+              for (int pl = 0; pl < 4; ++pl) T[pl][0] = T1[pl];
+            } else {
+              planes8_formula<DT, NS, false>(cur[rt], ep, 8, unw, T, ub[rt], up[rt]);
+            }
+#pragma unroll
+            for (int pl = 0; pl < 4; ++pl)
+#pragma unroll
+              for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
           }
-        }
-      } else {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          bf16x8_t T[4][NS];
-          planes8_formula<DT, NS, false>(cur[rt], ep, 8, unw, T, ub[rt], up[rt]);
-#pragma unroll
-          for (int pl = 0; pl < 4; ++pl)
-#pragma unroll
-            for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
+          mma_step(A, lcur, st * kStep + g4 * 8);
         }
       }
-      mma_step(A, lcur, st * kStep + g4 * 8);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) cur[rt] = nxt[rt];
-      lcur = lnxt;
     }
   }
+
+  bool bad = false;
+  if constexpr (TAB) {
+    // the ones column sees every cell of the row through the w plane, so a
+    // NaN marker anywhere in the K-range shows up in acc[2]
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bad |= __builtin_isnan(acc[2][rt][nt][e]);
+    bad = __ballot(bad) != 0;
+  }
+
   if (has_tail) {  // last partial step: guarded loads, masked planes
     const int64_t st = full;
     const int64_t cell0 = st * kStep + g4 * 8;
@@ -450,8 +452,7 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
 
   // ---- write this wave's partial sums (only the tiles in use)
   const int rows = 16 * RT;
-  float* out = a.partials +
-               (((int64_t)blockIdx.x * (a.L * a.B) + lb) * a.rtiles + rtile) * 3 * rows * a.nslot;
+  float* out = a.partials + ((ks * (a.L * a.B) + lb) * a.rtiles + rtile) * 3 * rows * a.nslot;
 #pragma unroll
   for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -476,36 +477,104 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
       vp += __shfl_xor(vp, 32, 64);
       const int64_t q = q0 + rt * 16 + r;
       if (g4 == 0 && q < a.Q) {
-        float* rs = a.rowsum + (((int64_t)blockIdx.x * (a.L * a.B) + lb) * a.Qp + q) * 2;
+        float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
         rs[0] = vb;
         rs[1] = vp;
       }
     }
   }
+  return bad;
+}
+
+// Grid: (KS, ceil(LB*rtiles / 4)); wave w of workgroup y takes task 4y + w,
+// and only tasks whose image falls in column-tile class NT do work.
+template <int DT, int RT, int NT, bool CNT, bool TAB>
+__global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
+  __shared__ __align__(16) unsigned char lut_s[TAB ? kLutBytes : 16];
+  const int wave = threadIdx.x >> 6;
+  const int64_t ntasks = a.L * a.B * a.rtiles;
+
+  // does any wave of this workgroup have an image of this column class?
+  bool wg_work = false;
+  for (int w = 0; w < kWavesCost; ++w) {
+    const int64_t t = (int64_t)blockIdx.y * kWavesCost + w;
+    if (t < ntasks) wg_work |= nt_class(a.ncols[(t / a.rtiles) % a.B] + 1) == NT;
+  }
+  if (!wg_work) return;
+  if constexpr (TAB) {
+    build_lut(lut_s, a.ep);
+    __syncthreads();
+  }
+  const int64_t task = (int64_t)blockIdx.y * kWavesCost + wave;
+  if (task >= ntasks) return;
+  const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
+  if (nt_class(a.ncols[lb % a.B] + 1) != NT) return;
+  const bool bad = cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, blockIdx.x, lut_s);
+  if constexpr (TAB) {
+    if ((threadIdx.x & 63) == 0) a.flags[(int64_t)blockIdx.x * ntasks + task] = bad ? 1 : 0;
+  }
+}
+
+// Formula-path wave as a real call, so that the fix-up kernel's register
+// allocation is one instantiation's, not the sum of all of them.
+template <int RT, int NT>
+__device__ __noinline__ void cost_wave_formula(const CostArgs& a, int64_t lb, int64_t rtile,
+                                               int64_t ks) {
+  cost_wave<ML_BF16, RT, NT, false, false>(a, lb, rtile, ks, nullptr);
+}
+
+// Redo, with the formulas, every wave of the bf16 table path whose flag is
+// set (a cell with |z| >= 64, inf or nan in its K-range).  Grid-stride over
+// all (split, task) pairs; a flag read is the only work for clean waves.
+template <int RT>
+__global__ __launch_bounds__(256) void cost_fix_kernel(CostArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int64_t ntasks = a.L * a.B * a.rtiles;
+  const int64_t nw = a.KS * ntasks;
+  for (int64_t w = (int64_t)blockIdx.x * kWavesCost + wave; w < nw;
+       w += (int64_t)gridDim.x * kWavesCost) {
+    if (!a.flags[w]) continue;
+    const int64_t ks = w / ntasks, task = w % ntasks;
+    const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
+    switch (nt_class(a.ncols[lb % a.B] + 1)) {
+      case 2: cost_wave_formula<RT, 2>(a, lb, rtile, ks); break;
+      case 4: cost_wave_formula<RT, 4>(a, lb, rtile, ks); break;
+      case 7: cost_wave_formula<RT, 7>(a, lb, rtile, ks); break;
+      default:
+        if constexpr (RT == 1) cost_wave_formula<1, 16>(a, lb, rtile, ks);
+        break;
+    }
+  }
 }
 
 template <int DT, int RT, int NT>
-static int launch_one(const CostArgs& a, const Dims& d, hipStream_t st) {
+static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   const int64_t tasks = d.LB * d.rtiles;
   const dim3 grid((unsigned)d.KS, (unsigned)ceil_div(tasks, kWavesCost));
-  const bool lut = DT == ML_BF16 && a.use_lut && a.rowsum == nullptr;
-  const size_t lds = lut ? kLutBytes : 0;
   if (d.counts_mode)
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true>), grid, dim3(256), lds, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true, false>), grid, dim3(256), 0, st, a);
+  else if (DT == ML_BF16 && tab)
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, DT == ML_BF16>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false>), grid, dim3(256), lds, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, false>), grid, dim3(256), 0, st, a);
   return check_launch("pair_cost");
 }
 
 // One launch per column-tile class up to the padded width; each image is
 // processed by exactly one of them.
 template <int DT, int RT>
-static int launch_classes(const CostArgs& a, const Dims& d, hipStream_t st) {
-  int rc = launch_one<DT, RT, 2>(a, d, st);
-  if (!rc && d.NT >= 4) rc = launch_one<DT, RT, 4>(a, d, st);
-  if (!rc && d.NT >= 7) rc = launch_one<DT, RT, 7>(a, d, st);
+static int launch_classes(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
+  int rc = launch_one<DT, RT, 2>(a, d, tab, st);
+  if (!rc && d.NT >= 4) rc = launch_one<DT, RT, 4>(a, d, tab, st);
+  if (!rc && d.NT >= 7) rc = launch_one<DT, RT, 7>(a, d, tab, st);
   if constexpr (RT == 1) {
-    if (!rc && d.NT >= 16) rc = launch_one<DT, 1, 16>(a, d, st);
+    if (!rc && d.NT >= 16) rc = launch_one<DT, 1, 16>(a, d, tab, st);
+  }
+  if (!rc && tab) {
+    const int64_t nw = d.KS * d.LB * d.rtiles;
+    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(nw, kWavesCost), 256);
+    hipLaunchKernelGGL((cost_fix_kernel<RT>), dim3(grid), dim3(256), 0, st, a);
+    rc = check_launch("pair_cost_fix");
   }
   return rc;
 }
@@ -514,11 +583,14 @@ int cost_rt_for(int dtype, int NT) { return (dtype == ML_BF16 && NT < 16) ? 2 : 
 
 int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool, hipStream_t st) {
   ProfScope ps_("pair_cost", st);
+  // bf16 with label maps and no unweighted row sums: table path
+  const bool tab = dtype == ML_BF16 && !d.counts_mode && a.use_lut && a.rowsum == nullptr;
   switch (dtype) {
-    case ML_F32: return launch_classes<ML_F32, 1>(a, d, st);
+    case ML_F32: return launch_classes<ML_F32, 1>(a, d, false, st);
     case ML_BF16:
-      return d.RT == 2 ? launch_classes<ML_BF16, 2>(a, d, st) : launch_classes<ML_BF16, 1>(a, d, st);
-    case ML_F16: return launch_classes<ML_F16, 1>(a, d, st);
+      return d.RT == 2 ? launch_classes<ML_BF16, 2>(a, d, tab, st)
+                       : launch_classes<ML_BF16, 1>(a, d, tab, st);
+    case ML_F16: return launch_classes<ML_F16, 1>(a, d, false, st);
   }
   return fail(ML_EINVAL, "unsupported mask logits dtype");
 }

@@ -43,7 +43,7 @@ int cost_rt_for(int dtype, int NT);
 
 // Byte offsets inside the caller's workspace.
 struct Layout {
-  size_t lab16, counts8, area, ncols, colmap, slot_of_col, partials, rowsum,
+  size_t lab16, counts8, area, ncols, colmap, slot_of_col, partials, rowsum, flags,
       costT, sep, rowstat, img, layer, err, total;
 };
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
@@ -69,6 +69,7 @@ struct CostArgs {
   const int* colmap;
   float* partials;   // [KS][LB][rtiles][3][rows][nslot]
   float* rowsum;     // [KS][LB][Qp][2] unweighted (force_masks) or null
+  int* flags;        // [KS][LB*rtiles] table-overflow flag per wave (bf16 table path)
   int64_t L, B, Q, HW, HWp, KS, rtiles, GT_total, bg, Qp;
   int nslot;
   float N2;

@@ -52,9 +52,15 @@ def rounded(z, dtype):
 
 
 def make_case(seed, L=1, B=2, Q=20, H=16, W=16, s=1, G=6, C=9, dtype="float32", sigma=2.0,
-              empty_image=False):
+              empty_image=False, extreme=False):
     rng = np.random.default_rng(seed)
     z = rng.normal(0, sigma, size=(L, B, Q, H, W)).astype(np.float32)
+    if extreme:  # |z| >= 64 in a few rows: outside the bf16 table, formulas redo those waves
+        vals = np.array([64.0, -64.0, 80.0, -100.0, 300.0, -1000.0, 65.5, -8192.0], np.float32)
+        for l, b, q in [(0, 0, 1), (0, 0, 2), (0, 1, Q - 1)]:
+            cells = rng.choice(H * W, size=12, replace=False)
+            z[l, b, q].reshape(-1)[cells] = rng.choice(vals, size=12)
+        z[0, 1, 0] = 70.0  # a whole row beyond the table
     tgt = np.zeros((B, H * s, W * s), dtype=np.int64)
     for b in range(B):
         if empty_image and b == 0:
@@ -90,6 +96,9 @@ COST_CASES = [
     dict(name="f32_tail32", kw=dict(Q=17, H=10, W=10), p={}),
     dict(name="f32_many_gt", kw=dict(G=40, Q=50, H=32, W=32), p={}),
     dict(name="bf16_many_gt", kw=dict(G=120, Q=64, H=32, W=32, dtype="bfloat16"), p={}),
+    dict(name="bf16_extreme", kw=dict(Q=40, H=32, W=32, dtype="bfloat16", sigma=3.0, extreme=True), p={}),
+    dict(name="bf16_extreme_many_gt",
+         kw=dict(G=70, Q=40, H=32, W=32, dtype="bfloat16", sigma=3.0, extreme=True), p={}),
     dict(name="f32_empty_image", kw=dict(empty_image=True), p={}),
     dict(name="f32_L2", kw=dict(L=2), p=dict(scales=(1.3, 0.7, 2.0), smooth=0.5)),
 ]

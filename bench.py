@@ -34,7 +34,37 @@ def parse():
     ap.add_argument("--config", default="cfg3_dense_headline")
     ap.add_argument("--cpu-sample-queries", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of 512 MiB (3 launches), the reference "
+                         "point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return ap.parse_args()
+
+
+COPY_BYTES = 512 << 20
+
+
+def copy_calibration():
+    import torch
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 3}), flush=True)
+
+
+def load_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` on `workload` from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel
+    factor), or None if that profile is absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)[workload][kernel]
+        return int(rec["fetch_bytes"] + rec["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def prof_lib():
@@ -95,6 +125,9 @@ def cpu_baseline(cfg, x_cpu, p2g_gpu, total_gpu, q_sample):
 
 def main():
     a = parse()
+    if a.copy_calibration:
+        copy_calibration()
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
                                    "(multi-GPU sharding is described in DESIGN.md, not built)"}))
@@ -168,7 +201,7 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-        "traffic": None,
+        "traffic": load_traffic(cfg.name, dom),
         "algorithmic_bytes": dom_bytes,
         "avg_launch_us": kernels[dom]["avg_us"],
     }

@@ -98,16 +98,14 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
   const int64_t lb = row / a.Q, q = row % a.Q, b = lb % a.B;
   const int64_t GTo = a.GT_out, C = a.C;
   const int G = a.ncols[b];
-  const int64_t rt = q / a.rows, rr = q % a.rows;
-  const int64_t pstride = (a.L * a.B) * a.rtiles * 3 * a.rows * a.nslot;
-  const float* P0 = a.partials + (lb * a.rtiles + rt) * 3 * a.rows * a.nslot + rr * a.nslot;
+  const RowPartials rp = row_partials(a.partials, a.sched, a.plan, lb, q, a.rows, a.rtiles, G);
   for (int s = lane; s <= G; s += 64) {
     float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-    for (int64_t ks = 0; ks < a.KS; ++ks) {
-      const float* P = P0 + ks * pstride;
+    for (int ks = 0; ks < rp.KS; ++ks) {
+      const float* P = rp.p0 + ks * rp.ks_stride;
       v0 += P[s];
-      v1 += P[a.rows * a.nslot + s];
-      v2 += P[2 * a.rows * a.nslot + s];
+      v1 += P[rp.plane + s];
+      v2 += P[2 * rp.plane + s];
     }
     sl[wave][0][s] = v0;
     sl[wave][1][s] = v1;
@@ -196,8 +194,8 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
     float mp = 0.f, dp = 0.f;
     if (a.force_masks) {
       float ub = 0.f, up = 0.f;
-      for (int64_t ks = 0; ks < a.KS; ++ks) {
-        const float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
+      for (int ks = 0; ks < rp.KS; ++ks) {
+        const float* rs = a.rowsum + ((rp.slot0 + ks) * a.rows + q % a.rows) * 2;
         ub += rs[0];
         up += rs[1];
       }
@@ -596,8 +594,6 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   // ---- 3. matched-loss partial sums and backward statistics
   const int* p2g = asg;
   const bool need_cls_pen = a.force_cls || a.void_idx >= 0;
-  const int64_t rt_rows = a.rows;
-  const int64_t pstride = (a.L * a.B) * a.rtiles * 3 * a.rows * a.nslot;
   for (int64_t q = tid; q < Q; q += 256) {
     const int c = p2g[q];
     const float* rs = a.rowstat + (lb * Q + q) * 8;
@@ -608,11 +604,11 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       cc = sep[2 * term + q * GTo + c];
       const int slot = a.slot_of_col[b * GTo + c];
       if (slot >= 0 && a.stats) {
-        const int64_t rt = q / rt_rows, rr = q % rt_rows;
-        const float* P0 = a.partials + (lb * a.rtiles + rt) * 3 * a.rows * a.nslot + rr * a.nslot + slot;
-        for (int64_t ks = 0; ks < a.KS; ++ks) {
-          I += P0[ks * pstride + a.rows * a.nslot];
-          T += P0[ks * pstride + 2 * a.rows * a.nslot];
+        const RowPartials rp =
+            row_partials(a.partials, a.sched, a.plan, lb, q, a.rows, a.rtiles, a.ncols[b]);
+        for (int ks = 0; ks < rp.KS; ++ks) {
+          I += rp.p0[ks * rp.ks_stride + rp.plane + slot];
+          T += rp.p0[ks * rp.ks_stride + 2 * rp.plane + slot];
         }
       }
     } else {

@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -124,17 +125,31 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
   d.rows = 16 * d.RT;
   d.nslot = 16 * d.NT;
   d.rtiles = ceil_div(d.Q, d.rows);
-  // one wave per (image, row tile, K-split); aim for ~8 waves per CU and at
-  // least 8 K-steps per wave
+  // a wave covers at least 8 K-steps of its task
   const int64_t nsteps = ceil_div(d.HW, kStep);
-  const int64_t per_ks = d.rtiles * d.LB;
-  int64_t ks = per_ks > 0 ? ceil_div(2048, per_ks) : 1;
-  const int64_t ks_max = nsteps / 8 > 1 ? nsteps / 8 : 1;
-  if (ks > ks_max) ks = ks_max;
-  if (ks < 1) ks = 1;
-  d.KS = ks;
+  d.ks_max = nsteps / 8 > 1 ? nsteps / 8 : 1;
   d.counts_mode = d.s > 1;
   return true;
+}
+
+// Class regions sized for max(kCostSlots, tasks) work items each; slots are
+// the workspace bound (kCostSlots).
+CostPlan bound_cost_plan(const Dims& d) {
+  CostPlan p{};
+  p.ntasks = d.LB * d.rtiles;
+  p.ks_max = d.ks_max;
+  p.nclass = 0;
+  while (p.nclass < kClasses && class_nt(p.nclass) <= d.NT) ++p.nclass;
+  const int64_t cap = std::max<int64_t>(kCostSlots, p.ntasks);
+  int64_t f = 0;
+  for (int c = 0; c < kClasses; ++c) {
+    p.slots[c] = (int)kCostSlots;
+    p.slot_base[c] = (int64_t)c * cap;
+    p.float_base[c] = f;
+    if (c < p.nclass) f += cap * 3 * d.rows * 16 * class_nt(c);
+  }
+  p.float_total = f;
+  return p;
 }
 
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
@@ -151,10 +166,12 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   L.ncols = take((size_t)d.B * 4);
   L.colmap = take((size_t)d.B * d.nslot * 4);
   L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
-  L.partials = take((size_t)d.KS * d.LB * d.rtiles * 3 * d.rows * d.nslot * 4);
-  const int64_t Qp = d.rtiles * d.rows;
-  L.rowsum = take(force_masks ? (size_t)d.KS * d.LB * Qp * 2 * 4 : 0);
-  L.flags = take((size_t)d.KS * d.LB * d.rtiles * 4);
+  const CostPlan pl = bound_cost_plan(d);
+  const int64_t cap = std::max<int64_t>(kCostSlots, pl.ntasks);
+  L.sched = take((size_t)sched_ints(pl.ntasks) * 4);
+  L.partials = take((size_t)pl.float_total * 4);
+  L.rowsum = take(force_masks ? (size_t)pl.nclass * cap * d.rows * 2 * 4 : 0);
+  L.flags = take((size_t)pl.nclass * cap * 4);
   L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
@@ -216,6 +233,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   int rc;
   if ((rc = launch_fill_i32((int*)(w + L.err), 0, 4, st))) return rc;
 
+  const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
+  const CostPlan plan = make_cost_plan(d, mask_dtype, tab);
   PrepArgs pa;
   pa.targets = mask_targets;
   pa.lab16 = (uint16_t*)(w + L.lab16);
@@ -226,6 +245,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.slot_of_col = (int*)(w + L.slot_of_col);
   pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
   pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
+  pa.sched = (int*)(w + L.sched);
+  pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = plan;
   if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
 
   const ElemParams mask_ep = make_elem_params(p->mask_gamma, p->mask_alpha,
@@ -236,11 +257,13 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   ca.counts8 = d.counts_mode ? pa.counts8 : nullptr;
   ca.ncols = pa.ncols;
   ca.colmap = pa.colmap;
+  ca.sched = pa.sched;
+  ca.plan = plan;
   ca.partials = (float*)(w + L.partials);
   ca.rowsum = force_masks ? (float*)(w + L.rowsum) : nullptr;
   ca.flags = (int*)(w + L.flags);
-  ca.L = d.L; ca.B = d.B; ca.Q = d.Q; ca.HW = d.HW; ca.HWp = d.HWp; ca.KS = d.KS;
-  ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.Qp = d.rtiles * d.rows;
+  ca.L = d.L; ca.B = d.B; ca.Q = d.Q; ca.HW = d.HW; ca.HWp = d.HWp;
+  ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.rows = d.rows;
   ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;
   ca.use_lut = g_use_lut;
   if (d.LB > 0 && d.rtiles > 0 && (rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
@@ -253,6 +276,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.cls_targets = cls_targets;
   aa.partials = ca.partials;
   aa.rowsum = ca.rowsum;
+  aa.sched = ca.sched;
+  aa.plan = plan;
   aa.area = pa.area;
   aa.ncols = pa.ncols;
   aa.slot_of_col = pa.slot_of_col;
@@ -265,8 +290,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.img = (float*)(w + L.img);
   aa.err = (int*)(w + L.err);
   aa.L = d.L; aa.B = d.B; aa.Q = d.Q; aa.C = d.C; aa.HW = d.HW; aa.Ht = d.Ht; aa.Wt = d.Wt;
-  aa.GT_total = d.GT_total; aa.GT_out = d.GT_out; aa.bg = d.bg; aa.KS = d.KS; aa.rtiles = d.rtiles;
-  aa.Qp = d.rtiles * d.rows; aa.rows = d.rows; aa.nslot = d.nslot; aa.N2 = (float)d.N2;
+  aa.GT_total = d.GT_total; aa.GT_out = d.GT_out; aa.bg = d.bg; aa.rtiles = d.rtiles;
+  aa.rows = d.rows; aa.nslot = d.nslot; aa.N2 = (float)d.N2;
   aa.smooth = p->smooth; aa.sigmoid_scale = p->sigmoid_scale; aa.dice_scale = p->dice_scale;
   aa.cls_scale = p->cls_scale;
   aa.normalize = p->normalize_uncertainty != 0;
@@ -456,6 +481,8 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   pa.targets = mask_targets;
   pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
   pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
+  pa.sched = nullptr;
+  pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = CostPlan{};
   if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
 
   const int64_t void_idx =

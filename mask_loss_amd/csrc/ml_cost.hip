@@ -27,6 +27,7 @@
 // sums come out NaN is redone with the formulas by a fix-up launch).  Other dtypes evaluate the formulas directly and split each
 // plane into NS bf16 terms so products keep float32 accuracy.
 #include <algorithm>
+#include <atomic>
 
 #include "ml_internal.h"
 
@@ -234,26 +235,23 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
   A[3] = __builtin_bit_cast(bf16x8_t, a3);
 }
 
-// Column-tile count class of an image: smallest instantiated NT >= need.
-__host__ __device__ inline int nt_class(int ncols_plus_one) {
-  const int need = (ncols_plus_one + 15) >> 4;
-  return need <= 2 ? 2 : need <= 4 ? 4 : need <= 7 ? 7 : 16;
-}
-
 // One wave's work: 16*RT query rows of task (lb, rtile) over the K-steps of
-// split `ks`.  TAB: per-cell planes from the LDS table (bf16 only); returns
-// true if the sums came out NaN, i.e. some cell hit the table's overflow
-// marker, in which case the partial sums written are unusable and the
-// caller redoes the wave with TAB = false.
+// split ks of KS; writes the partial sums to `out` ([3][16*RT][16*NT]) and,
+// for unweighted penalties, the row sums to `rs` ([16*RT][2]).  TAB:
+// per-cell planes from the LDS table (bf16 only); returns true if the sums
+// came out NaN, i.e. some cell hit the table's overflow marker, in which case
+// the partial sums written are unusable and the wave is redone with
+// TAB = false.
 template <int DT, int RT, int NT, bool CNT, bool TAB>
 __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
-                                          int64_t ks, const unsigned char* lut) {
+                                          int64_t ks, int64_t KS, const unsigned char* lut,
+                                          float* out, float* rs_out) {
   constexpr int NS = InTraits<DT>::kSplit;
   constexpr int D = TAB ? kDepth : 2;  // K-steps of logits and labels in flight
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g4 = lane >> 4;
   const ElemParams ep = a.ep;
-  const bool unw = !TAB && a.rowsum != nullptr;
+  const bool unw = !TAB && rs_out != nullptr;
   const int64_t b = lb % a.B;
   const int G = a.ncols[b];
   const int nt_used = (G + 1 + 15) >> 4;
@@ -294,10 +292,10 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
 
   // this wave's K-steps: [s0, s1) of the full steps, plus the tail step
   const int64_t full = a.HW / kStep;
-  const int64_t per = ceil_div(full, a.KS);
+  const int64_t per = ceil_div(full, KS);
   const int64_t s0 = min(full, ks * per);
   const int64_t s1 = min(full, s0 + per);
-  const bool has_tail = (a.HW % kStep) != 0 && ks == a.KS - 1;
+  const bool has_tail = (a.HW % kStep) != 0 && ks == KS - 1;
 
   int64_t rowoff[RT];
 #pragma unroll
@@ -451,8 +449,7 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
   }
 
   // ---- write this wave's partial sums (only the tiles in use)
-  const int rows = 16 * RT;
-  float* out = a.partials + ((ks * (a.L * a.B) + lb) * a.rtiles + rtile) * 3 * rows * a.nslot;
+  constexpr int rows = 16 * RT, nslot = 16 * NT;
 #pragma unroll
   for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -463,7 +460,7 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = rt * 16 + g4 * 4 + e;
-          out[(i * rows + row) * a.nslot + nt * 16 + r] = acc[i][rt][nt][e];
+          out[(i * rows + row) * nslot + nt * 16 + r] = acc[i][rt][nt][e];
         }
       }
   if (unw) {
@@ -475,82 +472,148 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
       vp += __shfl_xor(vp, 16, 64);
       vb += __shfl_xor(vb, 32, 64);
       vp += __shfl_xor(vp, 32, 64);
-      const int64_t q = q0 + rt * 16 + r;
-      if (g4 == 0 && q < a.Q) {
-        float* rs = a.rowsum + ((ks * (a.L * a.B) + lb) * a.Qp + q) * 2;
-        rs[0] = vb;
-        rs[1] = vp;
+      if (g4 == 0) {
+        rs_out[(rt * 16 + r) * 2] = vb;
+        rs_out[(rt * 16 + r) * 2 + 1] = vp;
       }
     }
   }
   return bad;
 }
 
-// Grid: (KS, ceil(LB*rtiles / 4)); wave w of workgroup y takes task 4y + w,
-// and only tasks whose image falls in column-tile class NT do work.
+template <int NT>
+constexpr int kClassOf = NT == 2 ? 0 : NT == 4 ? 1 : NT == 7 ? 2 : 3;
+
+// One launch per column-tile class: wave w of the grid takes work item w of
+// the class (item = task index * KS + split), with the class's tasks, count
+// and K-split read from the device schedule.  The grid has
+// max(slots, tasks) waves, so every item has a wave.
 template <int DT, int RT, int NT, bool CNT, bool TAB>
 __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
+  constexpr int CI = kClassOf<NT>;
   __shared__ __align__(16) unsigned char lut_s[TAB ? kLutBytes : 16];
   const int wave = threadIdx.x >> 6;
-  const int64_t ntasks = a.L * a.B * a.rtiles;
-
-  // does any wave of this workgroup have an image of this column class?
-  bool wg_work = false;
-  for (int w = 0; w < kWavesCost; ++w) {
-    const int64_t t = (int64_t)blockIdx.y * kWavesCost + w;
-    if (t < ntasks) wg_work |= nt_class(a.ncols[(t / a.rtiles) % a.B] + 1) == NT;
-  }
-  if (!wg_work) return;
+  const int64_t n = a.sched[CI], KS = a.sched[kClasses + CI];
+  const int64_t total = n * KS;
+  const int64_t w0 = (int64_t)blockIdx.x * kWavesCost;
+  if (w0 >= total) return;  // the whole workgroup is idle
   if constexpr (TAB) {
     build_lut(lut_s, a.ep);
     __syncthreads();
   }
-  const int64_t task = (int64_t)blockIdx.y * kWavesCost + wave;
-  if (task >= ntasks) return;
+  const int64_t w = w0 + wave;
+  if (w >= total) return;
+  const int64_t i = w / KS, ks = w % KS;
+  const int64_t task = a.sched[2 * kClasses + CI * a.plan.ntasks + i];
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
-  if (nt_class(a.ncols[lb % a.B] + 1) != NT) return;
-  const bool bad = cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, blockIdx.x, lut_s);
+  constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
+  float* out = a.partials + a.plan.float_base[CI] + w * tile;
+  float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + w) * (16 * RT) * 2 : nullptr;
+  const bool bad = cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs);
   if constexpr (TAB) {
-    if ((threadIdx.x & 63) == 0) a.flags[(int64_t)blockIdx.x * ntasks + task] = bad ? 1 : 0;
+    if ((threadIdx.x & 63) == 0) a.flags[a.plan.slot_base[CI] + w] = bad ? 1 : 0;
   }
 }
 
 // Formula-path wave as a real call, so that the fix-up kernel's register
 // allocation is one instantiation's, not the sum of all of them.
 template <int RT, int NT>
-__device__ __noinline__ void cost_wave_formula(const CostArgs& a, int64_t lb, int64_t rtile,
-                                               int64_t ks) {
-  cost_wave<ML_BF16, RT, NT, false, false>(a, lb, rtile, ks, nullptr);
+__device__ __noinline__ void cost_wave_formula(const CostArgs& a, int64_t w) {
+  constexpr int CI = kClassOf<NT>;
+  const int64_t KS = a.sched[kClasses + CI];
+  const int64_t i = w / KS, ks = w % KS;
+  const int64_t task = a.sched[2 * kClasses + CI * a.plan.ntasks + i];
+  const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
+  constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
+  cost_wave<ML_BF16, RT, NT, false, false>(a, lb, rtile, ks, KS, nullptr,
+                                           a.partials + a.plan.float_base[CI] + w * tile, nullptr);
 }
 
-// Redo, with the formulas, every wave of the bf16 table path whose flag is
-// set (a cell with |z| >= 64, inf or nan in its K-range).  Grid-stride over
-// all (split, task) pairs; a flag read is the only work for clean waves.
+// Redo, with the formulas, every work item of the bf16 table path whose flag
+// is set (a cell with |z| >= 64, inf or nan in its K-range).  Grid-stride
+// over the items of every class; a flag read is the only work for clean ones.
 template <int RT>
 __global__ __launch_bounds__(256) void cost_fix_kernel(CostArgs a) {
   const int wave = threadIdx.x >> 6;
-  const int64_t ntasks = a.L * a.B * a.rtiles;
-  const int64_t nw = a.KS * ntasks;
-  for (int64_t w = (int64_t)blockIdx.x * kWavesCost + wave; w < nw;
-       w += (int64_t)gridDim.x * kWavesCost) {
-    if (!a.flags[w]) continue;
-    const int64_t ks = w / ntasks, task = w % ntasks;
-    const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
-    switch (nt_class(a.ncols[lb % a.B] + 1)) {
-      case 2: cost_wave_formula<RT, 2>(a, lb, rtile, ks); break;
-      case 4: cost_wave_formula<RT, 4>(a, lb, rtile, ks); break;
-      case 7: cost_wave_formula<RT, 7>(a, lb, rtile, ks); break;
-      default:
-        if constexpr (RT == 1) cost_wave_formula<1, 16>(a, lb, rtile, ks);
-        break;
+  const int64_t step = (int64_t)gridDim.x * kWavesCost;
+#pragma unroll
+  for (int ci = 0; ci < kClasses; ++ci) {
+    if (ci >= a.plan.nclass) break;
+    const int64_t total = (int64_t)a.sched[ci] * a.sched[kClasses + ci];
+    const int64_t sb = ci == 0 ? a.plan.slot_base[0] : ci == 1 ? a.plan.slot_base[1]
+                     : ci == 2 ? a.plan.slot_base[2] : a.plan.slot_base[3];
+    for (int64_t w = (int64_t)blockIdx.x * kWavesCost + wave; w < total; w += step) {
+      if (!a.flags[sb + w]) continue;
+      if (ci == 0) cost_wave_formula<RT, 2>(a, w);
+      else if (ci == 1) cost_wave_formula<RT, 4>(a, w);
+      else if (ci == 2) cost_wave_formula<RT, 7>(a, w);
+      else if constexpr (RT == 1) cost_wave_formula<1, 16>(a, w);
     }
   }
 }
 
+// ---- launch plan ---------------------------------------------------------------
+// Resident waves of one cost kernel instance on the current device (cached).
+template <int DT, int RT, int NT, bool CNT, bool TAB>
+static int occ_slots() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int nb = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_kernel<DT, RT, NT, CNT, TAB>, 256, 0) !=
+            hipSuccess || nb < 1)
+      nb = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+    v = nb * cus * kWavesCost;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+template <int DT, int RT, int NT>
+static int occ_slots_for(bool cnt, bool tab) {
+  if (cnt) return occ_slots<DT, RT, NT, true, false>();
+  if (DT == ML_BF16 && tab) return occ_slots<DT, RT, NT, false, DT == ML_BF16>();
+  return occ_slots<DT, RT, NT, false, false>();
+}
+
+template <int DT, int RT>
+static void plan_slots(CostPlan& p, bool cnt, bool tab) {
+  for (int ci = 0; ci < p.nclass; ++ci) {
+    int v = 0;
+    switch (ci) {
+      case 0: v = occ_slots_for<DT, RT, 2>(cnt, tab); break;
+      case 1: v = occ_slots_for<DT, RT, 4>(cnt, tab); break;
+      case 2: v = occ_slots_for<DT, RT, 7>(cnt, tab); break;
+      default:
+        if constexpr (RT == 1) v = occ_slots_for<DT, 1, 16>(cnt, tab);
+        break;
+    }
+    p.slots[ci] = (int)std::min<int64_t>(std::max(v, kWavesCost), kCostSlots);
+  }
+}
+
+CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
+  CostPlan p = bound_cost_plan(d);
+  const bool cnt = d.counts_mode;
+  switch (dtype) {
+    case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false); break;
+    case ML_BF16:
+      if (d.RT == 2) plan_slots<ML_BF16, 2>(p, cnt, tab);
+      else plan_slots<ML_BF16, 1>(p, cnt, tab);
+      break;
+    case ML_F16: plan_slots<ML_F16, 1>(p, cnt, false); break;
+  }
+  return p;
+}
+
 template <int DT, int RT, int NT>
 static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
-  const int64_t tasks = d.LB * d.rtiles;
-  const dim3 grid((unsigned)d.KS, (unsigned)ceil_div(tasks, kWavesCost));
+  constexpr int CI = kClassOf<NT>;
+  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), kWavesCost));
   if (d.counts_mode)
     hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true, false>), grid, dim3(256), 0, st, a);
   else if (DT == ML_BF16 && tab)
@@ -565,15 +628,13 @@ static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st
 template <int DT, int RT>
 static int launch_classes(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   int rc = launch_one<DT, RT, 2>(a, d, tab, st);
-  if (!rc && d.NT >= 4) rc = launch_one<DT, RT, 4>(a, d, tab, st);
-  if (!rc && d.NT >= 7) rc = launch_one<DT, RT, 7>(a, d, tab, st);
+  if (!rc && a.plan.nclass > 1) rc = launch_one<DT, RT, 4>(a, d, tab, st);
+  if (!rc && a.plan.nclass > 2) rc = launch_one<DT, RT, 7>(a, d, tab, st);
   if constexpr (RT == 1) {
-    if (!rc && d.NT >= 16) rc = launch_one<DT, 1, 16>(a, d, tab, st);
+    if (!rc && a.plan.nclass > 3) rc = launch_one<DT, 1, 16>(a, d, tab, st);
   }
   if (!rc && tab) {
-    const int64_t nw = d.KS * d.LB * d.rtiles;
-    const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(nw, kWavesCost), 256);
-    hipLaunchKernelGGL((cost_fix_kernel<RT>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((cost_fix_kernel<RT>), dim3(256), dim3(256), 0, st, a);
     rc = check_launch("pair_cost_fix");
   }
   return rc;

@@ -23,6 +23,65 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 constexpr int kStep = 32;        // cells per MFMA K-step (16x16x32)
 constexpr int kWavesCost = 4;    // waves per cost workgroup
 
+// Column-tile classes of the cost contraction: an image with G non-empty GT
+// columns (+ the ones column) is handled by the kernel instance whose tile
+// count NT is the smallest of {2, 4, 7, 16} that holds G + 1 columns.
+constexpr int kClasses = 4;
+__host__ __device__ inline int class_nt(int ci) { return ci == 0 ? 2 : ci == 1 ? 4 : ci == 2 ? 7 : 16; }
+__host__ __device__ inline int class_of(int ncols_plus_one) {
+  const int need = (ncols_plus_one + 15) >> 4;
+  return need <= 2 ? 0 : need <= 4 ? 1 : need <= 7 ? 2 : 3;
+}
+// Upper bound of resident cost waves the workspace is sized for (256 CUs x 8).
+constexpr int64_t kCostSlots = 2048;
+
+// Host-side plan of the cost launches.  Each class launch has `slots[c]`
+// waves (what the GPU holds resident at that kernel's occupancy, at most
+// kCostSlots); on the device the schedule picks the class's K-split KS_c =
+// clamp(slots / n_c, 1, ks_max) for its n_c (image, row-tile) tasks, and wave
+// w of the class takes task w / KS_c, split w % KS_c (grid-stride beyond).
+// Work item w of class c owns partial tile float_base[c] + w * tile(c) and
+// global slot slot_base[c] + w (flags, unweighted row sums).
+struct CostPlan {
+  int nclass;                    // classes with class_nt(c) <= padded NT
+  int slots[kClasses];
+  int64_t slot_base[kClasses];
+  int64_t float_base[kClasses];
+  int64_t ks_max;
+  int64_t ntasks;                // L * B * rtiles
+  int64_t float_total;           // partials size (floats)
+};
+// Device schedule (ints in the workspace): n[kClasses], ks[kClasses],
+// list[kClasses][ntasks] (task ids per class, ascending), idx[ntasks]
+// (position of each task in its class list).
+__host__ __device__ inline int64_t sched_ints(int64_t ntasks) { return 2 * kClasses + (kClasses + 1) * ntasks; }
+
+// Where the K-split partial sums of query row (lb, q) live: split 0's value
+// of plane 0 at column slot 0, the stride between splits and between planes,
+// the split count, and the global slot of split 0.
+struct RowPartials {
+  const float* p0;
+  int64_t ks_stride, plane, slot0;
+  int KS;
+};
+__device__ inline RowPartials row_partials(const float* partials, const int* sched,
+                                           const CostPlan& plan, int64_t lb, int64_t q,
+                                           int64_t rows, int64_t rtiles, int G) {
+  const int ci = class_of(G + 1);
+  const int64_t nslot_c = 16 * class_nt(ci);
+  const int64_t task = lb * rtiles + q / rows;
+  const int64_t i = sched[2 * kClasses + kClasses * plan.ntasks + task];
+  const int KS = sched[kClasses + ci];
+  const int64_t tile = 3 * rows * nslot_c;
+  RowPartials r;
+  r.KS = KS;
+  r.ks_stride = tile;
+  r.plane = rows * nslot_c;
+  r.p0 = partials + plan.float_base[ci] + i * KS * tile + (q % rows) * nslot_c;
+  r.slot0 = plan.slot_base[ci] + i * KS;
+  return r;
+}
+
 // Derived sizes of one call.
 struct Dims {
   int64_t L, B, Q, H, W, Ht, Wt, C, GT_total;
@@ -33,7 +92,7 @@ struct Dims {
   int RT;                    // 16-row tiles per wave
   int rows;                  // rows per cost workgroup (16 * RT)
   int64_t rtiles;            // row tiles per image
-  int64_t KS;                // K-splits across workgroups
+  int64_t ks_max;            // most K-splits per task (>= 8 K-steps per wave)
   int nslot;                 // 16 * NT
   bool counts_mode;          // s > 1: per-cell count operands
 };
@@ -43,10 +102,14 @@ int cost_rt_for(int dtype, int NT);
 
 // Byte offsets inside the caller's workspace.
 struct Layout {
-  size_t lab16, counts8, area, ncols, colmap, slot_of_col, partials, rowsum, flags,
+  size_t lab16, counts8, area, ncols, colmap, slot_of_col, sched, partials, rowsum, flags,
       costT, sep, rowstat, img, layer, err, total;
 };
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
+// Plan slots / offsets of the cost launches (queries kernel occupancy on the
+// current device; the workspace bound uses kCostSlots only).
+CostPlan make_cost_plan(const Dims& d, int dtype, bool tab);
+CostPlan bound_cost_plan(const Dims& d);
 
 // ---- kernel argument blocks ------------------------------------------------
 struct PrepArgs {
@@ -57,8 +120,11 @@ struct PrepArgs {
   int* ncols;
   int* colmap;
   int* slot_of_col;
+  int* sched;            // cost schedule (see CostPlan), or null
   int64_t B, H, W, Ht, Wt, s, HWp, GT_total, GT_out, bg;
   int nslot;
+  int64_t L, rtiles;
+  CostPlan plan;
 };
 
 struct CostArgs {
@@ -67,10 +133,12 @@ struct CostArgs {
   const uint8_t* counts8;
   const int* ncols;
   const int* colmap;
-  float* partials;   // [KS][LB][rtiles][3][rows][nslot]
-  float* rowsum;     // [KS][LB][Qp][2] unweighted (force_masks) or null
-  int* flags;        // [KS][LB*rtiles] table-overflow flag per wave (bf16 table path)
-  int64_t L, B, Q, HW, HWp, KS, rtiles, GT_total, bg, Qp;
+  const int* sched;  // device schedule (see CostPlan)
+  float* partials;   // per work item: [3][rows][16 * NT_class]
+  float* rowsum;     // per work item: [rows][2] unweighted (force_masks) or null
+  int* flags;        // per work item: table-overflow flag (bf16 table path)
+  CostPlan plan;
+  int64_t L, B, Q, HW, HWp, rtiles, GT_total, bg, rows;
   int nslot;
   float N2;
   ElemParams ep;
@@ -84,6 +152,8 @@ struct AssignArgs {
   const int64_t* cls_targets;
   const float* partials;
   const float* rowsum;
+  const int* sched;
+  CostPlan plan;
   const int* area;
   const int* ncols;
   const int* slot_of_col;
@@ -97,7 +167,7 @@ struct AssignArgs {
   float* img;            // [LB][4]: mask, dice, cls sums, matched count
   int* err;
   // dims / params
-  int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, KS, rtiles, Qp;
+  int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, rtiles;
   int rows, nslot;
   float N2;
   float smooth, sigmoid_scale, dice_scale, cls_scale;

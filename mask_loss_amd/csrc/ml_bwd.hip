@@ -118,7 +118,42 @@ __device__ float block_sum_256(float v, float* sh) {
   return ((sh[0] + sh[1]) + (sh[2] + sh[3]));
 }
 
-template <bool STATS>
+// Per-row coefficients of the mask-logit gradient.
+struct RowCoef {
+  float mc, dc, sf, D, num, kd;
+};
+
+__device__ __forceinline__ RowCoef row_coef(const BwdArgs& a, float S, float P, float I, float T,
+                                            float mc, float dc) {
+  RowCoef r;
+  r.mc = mc;
+  r.dc = dc;
+  r.sf = a.sigmoid_scale / S;
+  r.D = P + T + a.smooth;
+  r.num = 2.f * I + a.smooth;
+  r.kd = a.dice_scale / fmaxf(r.D * r.D, 1e-20f);
+  return r;
+}
+
+// d(loss)/dz of one cell with target count tk
+__device__ __forceinline__ float grad_elem(float z, float tk, const ElemParams& ep, float N2,
+                                           const RowCoef& r) {
+  const Sig s = sig_terms(z);
+  const float w = unc_weight(s, ep);
+  float mn, mp;
+  focal_mods(s, ep, mn, mp);
+  const float g = ep.gamma;
+  const float negc = fmaxf(N2 - tk, 0.f);
+  const float gpos = -w * ep.ap * tk * mp * (g * s.p * s.cp + s.q1);
+  const float gneg = w * ep.an * negc * mn * (g * s.q1 * s.cn + s.p);
+  const float gs = (gpos + gneg) * r.sf;
+  const float pp = s.p * s.q1;
+  const float gd = (r.num * (w * pp * N2) - 2.f * r.D * (w * pp * tk)) * r.kd;
+  return r.mc * gs + r.dc * gd;
+}
+
+// Without saved statistics: one workgroup per row, a first pass recomputes
+// S, P, I, T (the reference's two-pass kernel).  grid: L*B*Q
 __global__ __launch_bounds__(256) void bwd_mask_kernel(BwdArgs a) {
   __shared__ float sh[4 * 4];
   const int64_t row = blockIdx.x;
@@ -142,13 +177,7 @@ __global__ __launch_bounds__(256) void bwd_mask_kernel(BwdArgs a) {
   }
   const ElemParams ep = a.mask_ep;
   float S, P, I, T;
-  if (STATS) {
-    const float* st = a.stats + row * ML_STATS;
-    S = st[ML_STAT_S];
-    P = st[ML_STAT_P];
-    I = matched ? st[ML_STAT_I] : 0.f;
-    T = matched ? st[ML_STAT_T] : 0.f;
-  } else {
+  {
     float sP = 0.f, sT = 0.f, sI = 0.f, sS = 0.f;
     for (int64_t ch = tid; ch < nch; ch += 256) {
       const int64_t cell0 = ch * 8;
@@ -175,12 +204,7 @@ __global__ __launch_bounds__(256) void bwd_mask_kernel(BwdArgs a) {
     if (!a.normalize) S = (float)(a.Ht * a.Wt);
     S = fmaxf(S, kEps);
   }
-  const float sf = a.sigmoid_scale / S;
-  const float D = P + T + a.smooth;
-  const float num = 2.f * I + a.smooth;
-  const float D2 = fmaxf(D * D, 1e-20f);
-  const float kd = a.dice_scale / D2;
-  const float g = ep.gamma;
+  const RowCoef rc = row_coef(a, S, P, I, T, mc, dc);
   for (int64_t ch = tid; ch < nch; ch += 256) {
     const int64_t cell0 = ch * 8;
     const int64_t nv = a.HW - cell0;
@@ -188,21 +212,65 @@ __global__ __launch_bounds__(256) void bwd_mask_kernel(BwdArgs a) {
     load8_any(a.logits, a.dtype, rbase + cell0, nv, vec, z);
     if (matched) target8(a, b, act, cell0, t);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const Sig s = sig_terms(z[k]);
-      const float w = unc_weight(s, ep);
-      float mn, mp;
-      focal_mods(s, ep, mn, mp);
-      const float tk = matched ? t[k] : 0.f;
-      const float negc = fmaxf(a.N2 - tk, 0.f);
-      const float gpos = -w * ep.ap * tk * mp * (g * s.p * s.cp + s.q1);
-      const float gneg = w * ep.an * negc * mn * (g * s.q1 * s.cn + s.p);
-      const float gs = (gpos + gneg) * sf;
-      const float pp = s.p * s.q1;
-      const float gd = (num * (w * pp * a.N2) - 2.f * D * (w * pp * tk)) * kd;
-      gr[k] = mc * gs + dc * gd;
-    }
+    for (int k = 0; k < 8; ++k) gr[k] = grad_elem(z[k], matched ? t[k] : 0.f, ep, a.N2, rc);
     store8(a.grad, a.dtype, rbase + cell0, gr, nv, vec);
+  }
+}
+
+// Statistics-driven path: one workgroup per (row, chunk of kBwdChunk cells);
+// each thread issues all kBwdU of its logit / label loads before computing,
+// so a matched row is spread over many workgroups and its loads overlap.
+// grid: L*B*Q * ceil(HW / kBwdChunk)
+constexpr int kBwdU = 4;
+constexpr int64_t kBwdChunk = 256 * 8 * kBwdU;
+
+__global__ __launch_bounds__(256) void bwd_mask_chunk_kernel(BwdArgs a, int64_t nchunk) {
+  const int64_t row = (int64_t)blockIdx.x / nchunk, chunk = (int64_t)blockIdx.x % nchunk;
+  const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
+  const int tid = threadIdx.x;
+  const int64_t out = a.pred_to_gt[row];
+  const int64_t act = out + (out >= a.bg ? 1 : 0);
+  const bool matched = out >= 0 && act < a.GT_total;
+  const bool vec = a.dtype == ML_F32 ? (a.HW % 4 == 0) : (a.HW % 8 == 0);
+  const int64_t rbase = row * a.HW;
+  const float inv_md = a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN];
+  const float mc = a.g_mask[l] * inv_md;
+  const float dc = a.g_dice[l] * inv_md;
+  const int64_t c0 = chunk * kBwdChunk + (int64_t)tid * 8;
+
+  if ((!matched && !a.force_masks) || (mc == 0.f && dc == 0.f)) {
+    const float zero[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < kBwdU; ++u) {
+      const int64_t cell0 = c0 + u * 256 * 8;
+      if (cell0 < a.HW) store8(a.grad, a.dtype, rbase + cell0, zero, a.HW - cell0, vec);
+    }
+    return;
+  }
+  const float* st = a.stats + row * ML_STATS;
+  const float S = st[ML_STAT_S], P = st[ML_STAT_P];
+  const float I = matched ? st[ML_STAT_I] : 0.f;
+  const float T = matched ? st[ML_STAT_T] : 0.f;
+  const RowCoef rc = row_coef(a, S, P, I, T, mc, dc);
+  const ElemParams ep = a.mask_ep;
+  float z[kBwdU][8], t[kBwdU][8];
+#pragma unroll
+  for (int u = 0; u < kBwdU; ++u) {
+    const int64_t cell0 = c0 + u * 256 * 8;
+    if (cell0 < a.HW) {
+      load8_any(a.logits, a.dtype, rbase + cell0, a.HW - cell0, vec, z[u]);
+      if (matched) target8(a, b, act, cell0, t[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kBwdU; ++u) {
+    const int64_t cell0 = c0 + u * 256 * 8;
+    if (cell0 < a.HW) {
+      float gr[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) gr[k] = grad_elem(z[u][k], matched ? t[u][k] : 0.f, ep, a.N2, rc);
+      store8(a.grad, a.dtype, rbase + cell0, gr, a.HW - cell0, vec);
+    }
   }
 }
 
@@ -301,10 +369,12 @@ int launch_bwd(const BwdArgs& a, const Dims& d, hipStream_t st) {
   const int64_t rows = d.L * d.B * d.Q;
   if (rows > 0 && d.HW > 0) {
     ProfScope ps_("bwd_mask", st);
-    if (a.stats)
-      hipLaunchKernelGGL(bwd_mask_kernel<true>, dim3((unsigned)rows), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(bwd_mask_kernel<false>, dim3((unsigned)rows), dim3(256), 0, st, a);
+    if (a.stats) {
+      const int64_t nchunk = ceil_div(d.HW, kBwdChunk);
+      hipLaunchKernelGGL(bwd_mask_chunk_kernel, dim3((unsigned)(rows * nchunk)), dim3(256), 0, st,
+                         a, nchunk);
+    } else
+      hipLaunchKernelGGL(bwd_mask_kernel, dim3((unsigned)rows), dim3(256), 0, st, a);
     int rc = check_launch("bwd_mask");
     if (rc) return rc;
   }

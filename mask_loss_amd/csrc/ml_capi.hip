@@ -162,7 +162,7 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   };
   L.lab16 = take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2);
   L.counts8 = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0);
-  L.area = take((size_t)d.B * d.GT_total * 4);
+  L.present = take((size_t)d.B * d.GT_total * 4);
   L.ncols = take((size_t)d.B * 4);
   L.colmap = take((size_t)d.B * d.nslot * 4);
   L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
@@ -239,7 +239,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.targets = mask_targets;
   pa.lab16 = (uint16_t*)(w + L.lab16);
   pa.counts8 = (uint8_t*)(w + L.counts8);
-  pa.area = (int*)(w + L.area);
+  pa.present = (int*)(w + L.present);
   pa.ncols = (int*)(w + L.ncols);
   pa.colmap = (int*)(w + L.colmap);
   pa.slot_of_col = (int*)(w + L.slot_of_col);
@@ -278,7 +278,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.rowsum = ca.rowsum;
   aa.sched = ca.sched;
   aa.plan = plan;
-  aa.area = pa.area;
   aa.ncols = pa.ncols;
   aa.slot_of_col = pa.slot_of_col;
   aa.sep = sep ? sep : (float*)(w + L.sep);
@@ -439,7 +438,6 @@ size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_para
   size_t o = 0;
   o = align256(o + (d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
   o = align256(o + (d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
-  o = align256(o + (size_t)d.B * d.GT_total * 4);  // area
   o = align256(o + (size_t)d.B * 4);                // ncols
   o = align256(o + (size_t)d.B * d.nslot * 4);      // colmap
   o = align256(o + (size_t)d.B * d.GT_out * 4);     // slot_of_col
@@ -473,7 +471,7 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   PrepArgs pa;
   pa.lab16 = (uint16_t*)(w + take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
   pa.counts8 = (uint8_t*)(w + take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
-  pa.area = (int*)(w + take((size_t)d.B * d.GT_total * 4));
+  pa.present = nullptr;  // labels only
   pa.ncols = (int*)(w + take((size_t)d.B * 4));
   pa.colmap = (int*)(w + take((size_t)d.B * d.nslot * 4));
   pa.slot_of_col = (int*)(w + take((size_t)d.B * d.GT_out * 4));

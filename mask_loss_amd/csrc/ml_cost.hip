@@ -253,7 +253,7 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
   const ElemParams ep = a.ep;
   const bool unw = !TAB && rs_out != nullptr;
   const int64_t b = lb % a.B;
-  const int G = a.ncols[b];
+  const int G = __builtin_amdgcn_readfirstlane(a.ncols[b]);
   const int nt_used = (G + 1 + 15) >> 4;
   const int64_t q0 = rtile * (16 * RT);
 
@@ -351,52 +351,69 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
     }
   };
 
-  if (s0 < s1) {
+  // Software pipeline over this wave's nst steps: D steps of logits and
+  // labels in flight.  Slot j holds step k + j; it is turned into A operands
+  // first and then refilled with step k + j + D (clamped to the last step, so
+  // the loads are unconditional and the wait counts stay exact).  Every
+  // branch here is wave-uniform.
+  const int64_t nst = s1 - s0;
+  auto planes = [&](const Raw8<DT> (&raw)[RT], bf16x8_t (&A)[4][RT][NS]) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      bf16x8_t T[4][NS];
+      if constexpr (TAB) {
+        bf16x8_t T1[4];
+        planes8_lut(raw[rt].w[0], lut, T1);
+#pragma unroll
+        for (int pl = 0; pl < 4; ++pl) T[pl][0] = T1[pl];
+      } else {
+        planes8_formula<DT, NS, false>(raw[rt], ep, 8, unw, T, ub[rt], up[rt]);
+      }
+#pragma unroll
+      for (int pl = 0; pl < 4; ++pl)
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
+    }
+  };
+  if (nst > 0) {
     Raw8<DT> buf[D][RT];
     uint4 lbuf[D];
+    // slot j <- step s0 + min(k, nst - 1): logits, labels
+    auto fetch_z = [&](int j, int64_t k) {
+      const int64_t st = s0 + (k < nst ? k : nst - 1);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) load_raw8<DT>(a.logits, rowoff[rt] + st * kStep, buf[j][rt], vec);
+    };
+    auto fetch_l = [&](int j, int64_t k) {
+      const int64_t st = s0 + (k < nst ? k : nst - 1);
+      lbuf[j] = *(const uint4*)(labp + st * kStep);
+    };
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      if (s0 + j < s1) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-          load_raw8<DT>(a.logits, rowoff[rt] + (s0 + j) * kStep, buf[j][rt], vec);
-        lbuf[j] = *(const uint4*)(labp + (s0 + j) * kStep);
-      }
+      fetch_z(j, j);
+      fetch_l(j, j);
     }
-    for (int64_t sb = s0; sb < s1; sb += D) {
+    int64_t k = 0;
+    for (; k + D <= nst; k += D) {
 #pragma unroll
       for (int j = 0; j < D; ++j) {
-        const int64_t st = sb + j;
-        if (st < s1) {
-          Raw8<DT> cur[RT];
+        bf16x8_t A[4][RT][NS];
+        planes(buf[j], A);
+        // keep each refill below the last read of its slot, so that it reuses
+        // the slot's registers instead of rotating the whole pipeline
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_z(j, k + j + D);
+        mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_l(j, k + j + D);
+      }
+    }
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) cur[rt] = buf[j][rt];
-          const uint4 lcur = lbuf[j];
-          if (st + D < s1) {  // refill this slot with step st + D
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-              load_raw8<DT>(a.logits, rowoff[rt] + (st + D) * kStep, buf[j][rt], vec);
-            lbuf[j] = *(const uint4*)(labp + (st + D) * kStep);
-          }
-          bf16x8_t A[4][RT][NS];
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            bf16x8_t T[4][NS];
-            if constexpr (TAB) {
-              bf16x8_t T1[4];
-              planes8_lut(cur[rt].w[0], lut, T1);
-#pragma unroll
-              for (int pl = 0; pl < 4; ++pl) T[pl][0] = T1[pl];
-            } else {
-              planes8_formula<DT, NS, false>(cur[rt], ep, 8, unw, T, ub[rt], up[rt]);
-            }
-#pragma unroll
-            for (int pl = 0; pl < 4; ++pl)
-#pragma unroll
-              for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
-          }
-          mma_step(A, lcur, st * kStep + g4 * 8);
-        }
+    for (int j = 0; j < D - 1; ++j) {  // the last nst % D steps
+      if (k + j < nst) {
+        bf16x8_t A[4][RT][NS];
+        planes(buf[j], A);
+        mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
       }
     }
   }
@@ -489,13 +506,14 @@ constexpr int kClassOf = NT == 2 ? 0 : NT == 4 ? 1 : NT == 7 ? 2 : 3;
 // and K-split read from the device schedule.  The grid has
 // max(slots, tasks) waves, so every item has a wave.
 template <int DT, int RT, int NT, bool CNT, bool TAB>
-__global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
+__global__ __launch_bounds__(64 * cost_waves(NT)) void cost_kernel(CostArgs a) {
   constexpr int CI = kClassOf<NT>;
   __shared__ __align__(16) unsigned char lut_s[TAB ? kLutBytes : 16];
-  const int wave = threadIdx.x >> 6;
-  const int64_t n = a.sched[CI], KS = a.sched[kClasses + CI];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n = __builtin_amdgcn_readfirstlane(a.sched[CI]);
+  const int64_t KS = __builtin_amdgcn_readfirstlane(a.sched[kClasses + CI]);
   const int64_t total = n * KS;
-  const int64_t w0 = (int64_t)blockIdx.x * kWavesCost;
+  const int64_t w0 = (int64_t)blockIdx.x * cost_waves(NT);
   if (w0 >= total) return;  // the whole workgroup is idle
   if constexpr (TAB) {
     build_lut(lut_s, a.ep);
@@ -504,7 +522,7 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
   const int64_t w = w0 + wave;
   if (w >= total) return;
   const int64_t i = w / KS, ks = w % KS;
-  const int64_t task = a.sched[2 * kClasses + CI * a.plan.ntasks + i];
+  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
   constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
   float* out = a.partials + a.plan.float_base[CI] + w * tile;
@@ -520,9 +538,9 @@ __global__ __launch_bounds__(256) void cost_kernel(CostArgs a) {
 template <int RT, int NT>
 __device__ __noinline__ void cost_wave_formula(const CostArgs& a, int64_t w) {
   constexpr int CI = kClassOf<NT>;
-  const int64_t KS = a.sched[kClasses + CI];
+  const int64_t KS = __builtin_amdgcn_readfirstlane(a.sched[kClasses + CI]);
   const int64_t i = w / KS, ks = w % KS;
-  const int64_t task = a.sched[2 * kClasses + CI * a.plan.ntasks + i];
+  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
   constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
   cost_wave<ML_BF16, RT, NT, false, false>(a, lb, rtile, ks, KS, nullptr,
@@ -533,8 +551,8 @@ __device__ __noinline__ void cost_wave_formula(const CostArgs& a, int64_t w) {
 // is set (a cell with |z| >= 64, inf or nan in its K-range).  Grid-stride
 // over the items of every class; a flag read is the only work for clean ones.
 template <int RT>
-__global__ __launch_bounds__(256) void cost_fix_kernel(CostArgs a) {
-  const int wave = threadIdx.x >> 6;
+__global__ __launch_bounds__(64 * kWavesCost) void cost_fix_kernel(CostArgs a) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t step = (int64_t)gridDim.x * kWavesCost;
 #pragma unroll
   for (int ci = 0; ci < kClasses; ++ci) {
@@ -543,7 +561,7 @@ __global__ __launch_bounds__(256) void cost_fix_kernel(CostArgs a) {
     const int64_t sb = ci == 0 ? a.plan.slot_base[0] : ci == 1 ? a.plan.slot_base[1]
                      : ci == 2 ? a.plan.slot_base[2] : a.plan.slot_base[3];
     for (int64_t w = (int64_t)blockIdx.x * kWavesCost + wave; w < total; w += step) {
-      if (!a.flags[sb + w]) continue;
+      if (!__builtin_amdgcn_readfirstlane(a.flags[sb + w])) continue;
       if (ci == 0) cost_wave_formula<RT, 2>(a, w);
       else if (ci == 1) cost_wave_formula<RT, 4>(a, w);
       else if (ci == 2) cost_wave_formula<RT, 7>(a, w);
@@ -562,12 +580,12 @@ static int occ_slots() {
   int v = cache[dev].load(std::memory_order_relaxed);
   if (v == 0) {
     int nb = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_kernel<DT, RT, NT, CNT, TAB>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_kernel<DT, RT, NT, CNT, TAB>, 64 * cost_waves(NT), 0) !=
             hipSuccess || nb < 1)
       nb = 1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
       cus = 256;
-    v = nb * cus * kWavesCost;
+    v = nb * cus * cost_waves(NT);
     cache[dev].store(v, std::memory_order_relaxed);
   }
   return v;
@@ -592,7 +610,7 @@ static void plan_slots(CostPlan& p, bool cnt, bool tab) {
         if constexpr (RT == 1) v = occ_slots_for<DT, 1, 16>(cnt, tab);
         break;
     }
-    p.slots[ci] = (int)std::min<int64_t>(std::max(v, kWavesCost), kCostSlots);
+    p.slots[ci] = (int)std::min<int64_t>(std::max(v, 8), kCostSlots);
   }
 }
 
@@ -613,13 +631,14 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
 template <int DT, int RT, int NT>
 static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   constexpr int CI = kClassOf<NT>;
-  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), kWavesCost));
+  constexpr int WV = cost_waves(NT);
+  const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), WV));
   if (d.counts_mode)
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true, false>), grid, dim3(64 * WV), 0, st, a);
   else if (DT == ML_BF16 && tab)
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, DT == ML_BF16>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, DT == ML_BF16>), grid, dim3(64 * WV), 0, st, a);
   else
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, false>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, false>), grid, dim3(64 * WV), 0, st, a);
   return check_launch("pair_cost");
 }
 
@@ -634,13 +653,13 @@ static int launch_classes(const CostArgs& a, const Dims& d, bool tab, hipStream_
     if (!rc && a.plan.nclass > 3) rc = launch_one<DT, 1, 16>(a, d, tab, st);
   }
   if (!rc && tab) {
-    hipLaunchKernelGGL((cost_fix_kernel<RT>), dim3(256), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((cost_fix_kernel<RT>), dim3(256), dim3(64 * kWavesCost), 0, st, a);
     rc = check_launch("pair_cost_fix");
   }
   return rc;
 }
 
-int cost_rt_for(int dtype, int NT) { return (dtype == ML_BF16 && NT < 16) ? 2 : 1; }
+int cost_rt_for(int, int) { return 1; }
 
 int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool, hipStream_t st) {
   ProfScope ps_("pair_cost", st);

@@ -21,19 +21,22 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 constexpr int kStep = 32;        // cells per MFMA K-step (16x16x32)
-constexpr int kWavesCost = 4;    // waves per cost workgroup
+constexpr int kWavesCost = 4;    // waves per workgroup of the cost fix-up kernel
 
 // Column-tile classes of the cost contraction: an image with G non-empty GT
 // columns (+ the ones column) is handled by the kernel instance whose tile
 // count NT is the smallest of {2, 4, 7, 16} that holds G + 1 columns.
 constexpr int kClasses = 4;
 __host__ __device__ inline int class_nt(int ci) { return ci == 0 ? 2 : ci == 1 ? 4 : ci == 2 ? 7 : 16; }
+// Waves per cost workgroup (all share one LDS table): 8, except for the
+// widest class, whose accumulators need more than 256 registers per lane.
+__host__ __device__ constexpr int cost_waves(int nt) { return nt >= 16 ? 4 : 8; }
 __host__ __device__ inline int class_of(int ncols_plus_one) {
   const int need = (ncols_plus_one + 15) >> 4;
   return need <= 2 ? 0 : need <= 4 ? 1 : need <= 7 ? 2 : 3;
 }
-// Upper bound of resident cost waves the workspace is sized for (256 CUs x 8).
-constexpr int64_t kCostSlots = 2048;
+// Upper bound of resident cost waves the workspace is sized for (256 CUs x 16).
+constexpr int64_t kCostSlots = 4096;
 
 // Host-side plan of the cost launches.  Each class launch has `slots[c]`
 // waves (what the GPU holds resident at that kernel's occupancy, at most
@@ -102,7 +105,7 @@ int cost_rt_for(int dtype, int NT);
 
 // Byte offsets inside the caller's workspace.
 struct Layout {
-  size_t lab16, counts8, area, ncols, colmap, slot_of_col, sched, partials, rowsum, flags,
+  size_t lab16, counts8, present, ncols, colmap, slot_of_col, sched, partials, rowsum, flags,
       costT, sep, rowstat, img, layer, err, total;
 };
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
@@ -116,7 +119,7 @@ struct PrepArgs {
   const int64_t* targets;
   uint16_t* lab16;
   uint8_t* counts8;
-  int* area;
+  int* present;          // [B][GT_total]: 1 iff the GT has pixels (forward only, else null)
   int* ncols;
   int* colmap;
   int* slot_of_col;
@@ -154,7 +157,6 @@ struct AssignArgs {
   const float* rowsum;
   const int* sched;
   CostPlan plan;
-  const int* area;
   const int* ncols;
   const int* slot_of_col;
   // outputs

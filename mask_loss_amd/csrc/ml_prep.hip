@@ -4,8 +4,10 @@
 //   s  > 1 : u8 count of each label inside the s x s block of every cell
 //            (B, GT_total, HWp), the reference's count tensor
 //            (src/cuda/utils.cuh:6-36)
-// plus the per-GT areas (pixel counts, src/cuda/pw_mask.cu:391) and, per
-// image, the compacted list of output columns whose GT has non-zero area.
+// plus, for the forward, which GTs have pixels (the reference's per-GT areas
+// of src/cuda/pw_mask.cu:391 are only ever tested against zero) and, per
+// image, the compacted list of output columns whose GT is non-empty, and the
+// cost schedule.
 #include "ml_internal.h"
 
 namespace ml {
@@ -25,48 +27,82 @@ int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st) {
   return check_launch("fill");
 }
 
-constexpr int kHistMax = 4096;  // GT slots histogrammed in LDS; larger -> global atomics
+constexpr int kMarkMax = 8192;  // GT slots marked in LDS; more -> direct global marks
 
-// s == 1: one thread per cell.  grid (ceil(HWp/256), B)
+// Mark label `lab` present: an LDS byte, or the global flag when the GT count
+// exceeds the LDS table.  Lanes of a wave that agree with lane 0 skip the
+// store (most cells of a wave carry one label).
+__device__ __forceinline__ void mark_present(unsigned char* pres, int* present, int64_t lab,
+                                             bool lds) {
+  if (lds) pres[lab] = 1;
+  else present[lab] = 1;
+}
+
+// s == 1: each thread converts 8 consecutive cells.  grid (ceil(HWp/2048), B)
 __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
-  __shared__ int hist[kHistMax];
+  __shared__ unsigned char pres[kMarkMax];
   const int64_t b = blockIdx.y;
   const int64_t HW = a.H * a.W;
-  const bool lds_hist = a.GT_total <= kHistMax;
-  if (lds_hist)
-    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) hist[i] = 0;
-  __syncthreads();
-  const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (cell < a.HWp) {
-    uint16_t v = kNoLabel;
-    if (cell < HW) {
-      const int64_t lab = a.targets[b * HW + cell];
-      if ((uint64_t)lab < (uint64_t)a.GT_total) {
-        v = (uint16_t)lab;
-        if (lds_hist) atomicAdd(&hist[lab], 1);
-        else atomicAdd(&a.area[b * a.GT_total + lab], 1);
-      }
-    }
-    a.lab16[b * a.HWp + cell] = v;
+  const bool mark = a.present != nullptr;
+  const bool lds = a.GT_total <= kMarkMax;
+  int* present = mark ? a.present + b * a.GT_total : nullptr;
+  if (mark && lds) {
+    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) pres[i] = 0;
+    __syncthreads();
   }
-  __syncthreads();
-  if (lds_hist)
+  const int64_t cell0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (cell0 < a.HWp) {
+    int64_t lab[8];
+    const int64_t* src = a.targets + b * HW + cell0;
+    if (HW % 8 == 0 && cell0 + 8 <= HW) {  // 64-byte aligned run of 8 labels
+#pragma unroll
+      for (int k = 0; k < 8; k += 2) {
+        const longlong2 v = *(const longlong2*)(src + k);
+        lab[k] = v.x;
+        lab[k + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) lab[k] = cell0 + k < HW ? src[k] : -1;
+    }
+    uint32_t wv[4];
+    int64_t prev = -1;
+    const int64_t lane0 = __shfl(lab[0], 0, 64);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool valid = (uint64_t)lab[k] < (uint64_t)a.GT_total;
+      const uint32_t v = valid ? (uint32_t)lab[k] : (uint32_t)kNoLabel;
+      if (k & 1) wv[k >> 1] |= v << 16;
+      else wv[k >> 1] = v;
+      if (mark && valid && lab[k] != prev && !(k == 0 && lab[0] == lane0 && (threadIdx.x & 63) != 0))
+        mark_present(pres, present, lab[k], lds);
+      prev = lab[k];
+    }
+    *(uint4*)(a.lab16 + b * a.HWp + cell0) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+  }
+  if (mark && lds) {
+    __syncthreads();
     for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x)
-      if (hist[i]) atomicAdd(&a.area[b * a.GT_total + i], hist[i]);
+      if (pres[i]) present[i] = 1;
+  }
 }
 
 // s > 1: one thread per low-res cell, counts[b][lab][cell] (single writer).
 __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
-  __shared__ int hist[kHistMax];
+  __shared__ unsigned char pres[kMarkMax];
   const int64_t b = blockIdx.y;
   const int64_t HW = a.H * a.W;
-  const bool lds_hist = a.GT_total <= kHistMax;
-  if (lds_hist)
-    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) hist[i] = 0;
-  __syncthreads();
+  const bool mark = a.present != nullptr;
+  const bool lds = a.GT_total <= kMarkMax;
+  int* present = mark ? a.present + b * a.GT_total : nullptr;
+  if (mark && lds) {
+    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) pres[i] = 0;
+    __syncthreads();
+  }
   const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (cell < HW) {
     const int64_t i = cell / a.W, j = cell % a.W;
+    int64_t prev = -1;
     for (int64_t dy = 0; dy < a.s; ++dy) {
       const int64_t* row = a.targets + (b * a.Ht + i * a.s + dy) * a.Wt + j * a.s;
       for (int64_t dx = 0; dx < a.s; ++dx) {
@@ -74,16 +110,17 @@ __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
         if ((uint64_t)lab < (uint64_t)a.GT_total) {
           uint8_t* c = a.counts8 + (b * a.GT_total + lab) * a.HWp + cell;
           *c = (uint8_t)(*c + 1);
-          if (lds_hist) atomicAdd(&hist[lab], 1);
-          else atomicAdd(&a.area[b * a.GT_total + lab], 1);
+          if (mark && lab != prev) mark_present(pres, present, lab, lds);
         }
+        prev = lab;
       }
     }
   }
-  __syncthreads();
-  if (lds_hist)
+  if (mark && lds) {
+    __syncthreads();
     for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x)
-      if (hist[i]) atomicAdd(&a.area[b * a.GT_total + i], hist[i]);
+      if (pres[i]) present[i] = 1;
+  }
 }
 
 // One wave per image: compacted list of columns with non-empty GT.
@@ -101,7 +138,7 @@ __global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) {
       bool ok = false;
       if (c < a.GT_out) {
         const int64_t act = c + (c >= a.bg ? 1 : 0);
-        ok = a.area[b * a.GT_total + act] > 0;
+        ok = a.present[b * a.GT_total + act] != 0;
       }
       const uint64_t m = __ballot(ok);
       const int slot = base + __popcll(m & below);
@@ -153,19 +190,22 @@ __global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) {
 
 int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   ProfScope ps_("prep", st);
-  int rc = launch_fill_i32(a.area, 0, d.B * d.GT_total, st);
-  if (rc) return rc;
-  const dim3 grid((unsigned)ceil_div(d.HWp, 256), (unsigned)d.B);
+  int rc;
+  if (a.present && (rc = launch_fill_i32(a.present, 0, d.B * d.GT_total, st))) return rc;
   if (!d.counts_mode) {
+    const dim3 grid((unsigned)ceil_div(d.HWp, 256 * 8), (unsigned)d.B);
     hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);
   } else {
     rc = launch_fill_i32((int*)a.counts8, 0, d.B * d.GT_total * d.HWp / 4, st);
     if (rc) return rc;
+    const dim3 grid((unsigned)ceil_div(d.HW, 256), (unsigned)d.B);
     hipLaunchKernelGGL(prep_counts_kernel, grid, dim3(256), 0, st, a);
   }
   if ((rc = check_launch("prep"))) return rc;
-  hipLaunchKernelGGL(prep_columns_kernel, dim3(1), dim3(1024), 0, st, a);
-  if ((rc = check_launch("prep_columns"))) return rc;
+  if (a.present) {
+    hipLaunchKernelGGL(prep_columns_kernel, dim3(1), dim3(1024), 0, st, a);
+    if ((rc = check_launch("prep_columns"))) return rc;
+  }
   return ML_OK;
 }
 

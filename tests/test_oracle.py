@@ -25,7 +25,9 @@ matching_backward                      central finite differences of the naive
 
 The reference ships no golden vectors, fixtures or known-answer tests for this
 path (its only harness, benchmarks.py, compares CUDA against Python at run
-time); tests/golden/ holds vectors written by this oracle for the GPU tests.
+time); tests/golden/ holds vectors written by this oracle (tests/golden/make_golden.py),
+checked against the oracle on the CPU and against the HIP path on the GPU
+(tests/test_golden.py).
 """
 import itertools
 import math

@@ -70,8 +70,13 @@ typedef struct ml_params {
   int32_t normalize_uncertainty;
 } ml_params;
 
-/* Per-query statistics saved by the forward for the fused backward:
- * stats[(l*B+b)*Q+q][ML_STAT_*] (float). */
+/* State the fused forward leaves for the backward ("saved": ml_saved_bytes()
+ * bytes, 256-byte aligned, written by ml_mask_matching_forward, read by
+ * ml_mask_matching_backward).  Its head is float: per-query statistics
+ * stats[(l*B+b)*Q+q][ML_STAT_*], then the per-layer block layer[l][ML_LAYER_*];
+ * after them (internal layout) the list of matched query rows and, when the
+ * targets are at the logit resolution, the compact label map, so the backward
+ * neither recomputes statistics nor re-reads the int64 label map. */
 enum {
   ML_STAT_S = 0,    /* uncertainty normaliser after normalise/clamp */
   ML_STAT_P = 1,    /* sum_j N2 w p */
@@ -79,9 +84,8 @@ enum {
   ML_STAT_T = 3,    /* sum_j w n    for the matched GT (0 if unmatched) */
   ML_STATS = 4
 };
-/* Per-layer block appended after the per-query stats: layer[l][ML_LAYER_*]. */
 enum { ML_LAYER_INV_MASK_DEN = 0, ML_LAYER_INV_CLS_DEN = 1, ML_LAYERS = 2 };
-size_t ml_stats_floats(const ml_shape* s);
+size_t ml_saved_bytes(const ml_shape* s, const ml_params* p, int mask_dtype);
 
 const char* ml_last_error(void);
 int ml_version(void);
@@ -101,21 +105,29 @@ size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p,
                                        int mask_dtype);
 /* pred_to_gt / pred_round: (L,B,Q) int64; layer_means: (3,L) float
  * [mask, dice, cls]; separate_costs: (3,L,B,Q,GT_out) float or NULL;
- * stats: ml_stats_floats() floats or NULL. */
+ * saved: ml_saved_bytes() bytes for the backward, or NULL.
+ * grad_mask_prefill: NULL, or the (L,B,Q,H,W) mask_dtype buffer that will
+ * receive the mask-logit gradient.  The forward then zero-fills it on a
+ * library-owned side stream while the assignment runs on `stream` (the fill
+ * is joined into `stream` before the forward's last kernel), and the backward
+ * called with grad_prefilled = 1 writes only the matched rows.  Not allowed
+ * with force_unmatched_masks_to_empty (every row has a gradient then). */
 int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
                              const void* mask_logits, const int64_t* mask_targets,
                              int cls_dtype, const void* cls_logits,
                              const int64_t* cls_targets, int64_t* pred_to_gt,
                              int64_t* pred_round, float* layer_means,
-                             float* separate_costs, float* stats, void* workspace,
-                             size_t workspace_bytes, ml_stream_t stream);
+                             float* separate_costs, void* saved, void* grad_mask_prefill,
+                             void* workspace, size_t workspace_bytes, ml_stream_t stream);
 
 /* ---- matching backward ------------------------------------------------------
  * grad_{mask,dice,cls}: (L,) float upstream gradients of the layer means.
  * grad_mask_logits: (L,B,Q,H,W) in mask_dtype; grad_cls_logits: (L,B,Q,C) in
- * cls_dtype.  stats == NULL recomputes the per-query statistics from the
- * logits (the reference's two-pass backward); otherwise the statistics saved
- * by ml_mask_matching_forward are used and the logits are read once. */
+ * cls_dtype.  saved == NULL recomputes the per-query statistics from the
+ * logits (the reference's two-pass backward); otherwise the state saved by
+ * ml_mask_matching_forward is used and each matched logit is read once.
+ * grad_prefilled = 1 (requires `saved`): grad_mask_logits is the buffer the
+ * forward zero-filled, and only matched rows are written. */
 size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,
                                                 int mask_dtype);
 int ml_mask_matching_backward(const ml_shape* s, const ml_params* p,
@@ -124,7 +136,7 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p,
                               const void* mask_logits, const int64_t* mask_targets,
                               int cls_dtype, const void* cls_logits,
                               const int64_t* cls_targets, const int64_t* pred_to_gt,
-                              const float* stats, void* grad_mask_logits,
+                              const void* saved, int grad_prefilled, void* grad_mask_logits,
                               void* grad_cls_logits, void* workspace,
                               size_t workspace_bytes, ml_stream_t stream);
 
@@ -137,11 +149,18 @@ int ml_pairwise_label_loss_forward(int64_t L, int64_t B, int64_t Q, int64_t C,
                                    float alpha, int use_softmax, float* out,
                                    ml_stream_t stream);
 
+/* ---- input validation helper ------------------------------------------------
+ * flag[0] = 1 if any of x[0..n) equals `value`, else 0 (one small kernel, no
+ * synchronisation).  Replaces the device-wide comparison + reduction behind
+ * the reference's void-class check (functions/mask/matching.py:177-178), so
+ * the caller can read the flag asynchronously. */
+int ml_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, ml_stream_t stream);
+
 /* ---- instrumentation (no counterpart in the reference) ---------------------
  * When enabled, every kernel launch of this library is bracketed by HIP events
  * recorded on its own stream.  ml_profile_read() waits for those events and
  * returns, for kernel family `name` ("prep", "pair_cost", "assign", "layer",
- * "bwd_mask", "bwd_cls", "label_cost"), the number of launches and their
+ * "bwd_mask", "bwd_cls", "label_cost", "prefill"), the number of launches and their
  * summed duration in milliseconds since the last reset. */
 int ml_profile_enable(int enable);
 int ml_profile_read(const char* name, int64_t* launches, double* total_ms);

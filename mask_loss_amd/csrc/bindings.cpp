@@ -143,7 +143,8 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
                                          const torch::Tensor& mask_targets,
                                          const torch::Tensor& cls_logits,
                                          const torch::Tensor& cls_targets, const ml_params& p,
-                                         bool want_stats) {
+                                         bool want_saved,
+                                         const c10::optional<torch::Tensor>& grad_prefill) {
   ML_CHECK_INPUT(mask_logits);
   ML_CHECK_INPUT(mask_targets);
   ML_CHECK_INPUT(cls_logits);
@@ -156,8 +157,20 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
   auto pred_to_gt = torch::empty({s.L, s.B, s.Q}, i64);
   auto pred_round = torch::empty({s.L, s.B, s.Q}, i64);
   auto means = torch::empty({3, s.L}, f32);
-  torch::Tensor stats;
-  if (want_stats) stats = torch::empty({(int64_t)ml_stats_floats(&s)}, f32);
+  torch::Tensor saved;
+  if (want_saved)
+    saved = torch::empty({(int64_t)std::max<size_t>(ml_saved_bytes(&s, &p, mdt), 256)},
+                         mask_logits.options().dtype(torch::kUInt8));
+  void* prefill = nullptr;
+  if (grad_prefill.has_value()) {
+    const auto& g = *grad_prefill;
+    ML_CHECK_INPUT(g);
+    TORCH_CHECK(want_saved, "grad_prefill needs the fused forward");
+    TORCH_CHECK(g.sizes() == mask_logits.sizes() && g.scalar_type() == mask_logits.scalar_type() &&
+                    g.device() == mask_logits.device(),
+                "grad_prefill must match mask_logits in shape, dtype and device");
+    prefill = g.data_ptr();
+  }
   const size_t wsb = ml_mask_matching_workspace_size(&s, &p, mdt);
   auto ws = workspace(wsb, mask_logits);
   TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, "unsupported shape for mask_matching");
@@ -165,13 +178,13 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
       &s, &p, mdt, mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt,
       cls_logits.data_ptr(), cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
       pred_round.data_ptr<int64_t>(), means.data_ptr<float>(), nullptr,
-      want_stats ? stats.data_ptr<float>() : nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
+      want_saved ? saved.data_ptr() : nullptr, prefill, ws.data_ptr(), ws.numel(), cur_stream()));
   // means follow the logits dtype (src/cuda/mask_matching_forward.cu:580-583);
   // the fused entry keeps them in float32
-  const auto out_dt = want_stats ? torch::kFloat32 : mask_logits.scalar_type();
+  const auto out_dt = want_saved ? torch::kFloat32 : mask_logits.scalar_type();
   std::vector<torch::Tensor> r = {pred_to_gt, pred_round, means[0].to(out_dt),
                                   means[1].to(out_dt), means[2].to(out_dt)};
-  if (want_stats) r.push_back(stats);
+  if (want_saved) r.push_back(saved);
   return r;
 }
 
@@ -186,7 +199,8 @@ std::vector<torch::Tensor> mask_matching(
                                   ug, ug_min, inf_thresh, num_masks, force_cls, force_masks, topk,
                                   strategy, mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
                                   use_softmax, normalize);
-  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, false);
+  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, false,
+                       c10::nullopt);
 }
 
 // The reference's MaskMatchingFunction passes normalize_uncertainty a second
@@ -206,20 +220,23 @@ std::vector<torch::Tensor> mask_matching_wrapper_order(
                        cls_alpha, void_idx, use_softmax, normalize);
 }
 
-// Same as mask_matching, plus a sixth output: the per-query statistics the
-// fused backward uses to read every logit once.
+// Same as mask_matching, plus a sixth output: the saved state (per-query
+// statistics, matched rows, compact labels) the fused backward uses to read
+// every matched logit once.  With grad_prefill (the tensor that will receive
+// the mask-logit gradient) the forward zero-fills it beside the assignment.
 std::vector<torch::Tensor> mask_matching_fused(
     const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
     const torch::Tensor& cls_logits, const torch::Tensor& cls_targets, double smooth,
     double sigmoid_scale, double dice_scale, double cls_scale, int64_t background_index, double ug,
     double ug_min, double inf_thresh, double num_masks, bool force_cls, bool force_masks,
     int64_t topk, int64_t strategy, double mask_gamma, double mask_alpha, double cls_gamma,
-    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize) {
+    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize,
+    const c10::optional<torch::Tensor>& grad_prefill) {
   const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
                                   ug, ug_min, inf_thresh, num_masks, force_cls, force_masks, topk,
                                   strategy, mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
                                   use_softmax, normalize);
-  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, true);
+  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, true, grad_prefill);
 }
 
 // --------------------------------------------------------------------------
@@ -229,7 +246,8 @@ std::vector<torch::Tensor> backward_impl(
     const torch::Tensor& g_mask, const torch::Tensor& g_dice, const torch::Tensor& g_cls,
     const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
     const torch::Tensor& cls_logits, const torch::Tensor& cls_targets,
-    const torch::Tensor& pred_to_gt, const ml_params& p, const torch::Tensor* stats) {
+    const torch::Tensor& pred_to_gt, const ml_params& p, const torch::Tensor* saved,
+    const c10::optional<torch::Tensor>& grad_prefill) {
   ML_CHECK_INPUT(mask_logits);
   ML_CHECK_INPUT(mask_targets);
   ML_CHECK_INPUT(cls_logits);
@@ -248,11 +266,21 @@ std::vector<torch::Tensor> backward_impl(
               "upstream gradients must have shape (L,)");
   const int mdt = dtype_code(mask_logits, "mask_logits");
   const int cdt = dtype_code(cls_logits, "cls_logits");
-  auto grad_mask = torch::empty_like(mask_logits);
+  torch::Tensor grad_mask;
+  if (grad_prefill.has_value()) {
+    TORCH_CHECK(saved != nullptr, "grad_prefill needs the saved state");
+    grad_mask = *grad_prefill;
+    ML_CHECK_INPUT(grad_mask);
+    TORCH_CHECK(grad_mask.sizes() == mask_logits.sizes() &&
+                    grad_mask.scalar_type() == mask_logits.scalar_type(),
+                "grad_prefill must match mask_logits in shape and dtype");
+  } else {
+    grad_mask = torch::empty_like(mask_logits);
+  }
   auto grad_cls = torch::empty_like(cls_logits);
-  if (stats) {
-    ML_CHECK_INPUT(*stats);
-    TORCH_CHECK(stats->numel() == (int64_t)ml_stats_floats(&s), "stats size mismatch");
+  if (saved) {
+    ML_CHECK_INPUT(*saved);
+    TORCH_CHECK(saved->numel() >= (int64_t)ml_saved_bytes(&s, &p, mdt), "saved state size mismatch");
   }
   const size_t wsb = ml_mask_matching_backward_workspace_size(&s, &p, mdt);
   auto ws = workspace(wsb, mask_logits);
@@ -260,8 +288,8 @@ std::vector<torch::Tensor> backward_impl(
       &s, &p, gm.data_ptr<float>(), gd.data_ptr<float>(), gc.data_ptr<float>(), mdt,
       mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt, cls_logits.data_ptr(),
       cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
-      stats ? stats->data_ptr<float>() : nullptr, grad_mask.data_ptr(), grad_cls.data_ptr(),
-      ws.data_ptr(), ws.numel(), cur_stream()));
+      saved ? saved->data_ptr() : nullptr, grad_prefill.has_value() ? 1 : 0, grad_mask.data_ptr(),
+      grad_cls.data_ptr(), ws.data_ptr(), ws.numel(), cur_stream()));
   return {grad_mask, grad_cls};
 }
 
@@ -278,7 +306,7 @@ std::vector<torch::Tensor> mask_matching_backward(
                                   mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
                                   use_softmax, normalize);
   return backward_impl(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logits, cls_targets,
-                       pred_to_gt, p, nullptr);
+                       pred_to_gt, p, nullptr, c10::nullopt);
 }
 
 std::vector<torch::Tensor> mask_matching_backward_fused(
@@ -289,13 +317,13 @@ std::vector<torch::Tensor> mask_matching_backward_fused(
     double cls_scale, int64_t background_index, double ug, double ug_min, double num_masks,
     bool force_cls, bool force_masks, double mask_gamma, double mask_alpha, double cls_gamma,
     double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize,
-    const torch::Tensor& stats) {
+    const torch::Tensor& saved, const c10::optional<torch::Tensor>& grad_prefill) {
   const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
                                   ug, ug_min, 1e30, num_masks, force_cls, force_masks, 1, 0,
                                   mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
                                   use_softmax, normalize);
   return backward_impl(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logits, cls_targets,
-                       pred_to_gt, p, &stats);
+                       pred_to_gt, p, &saved, grad_prefill);
 }
 
 // --------------------------------------------------------------------------
@@ -335,6 +363,16 @@ torch::Tensor forward_pw_softmax_label_loss(const torch::Tensor& logits,
   return label_impl(logits, targets, background_index, scale, 0.0, -1.0, true);
 }
 
+// Device flag (int32, shape (1,)): 1 if any element of `x` equals `value`.
+torch::Tensor any_equal(const torch::Tensor& x, int64_t value) {
+  ML_CHECK_INPUT(x);
+  TORCH_CHECK(x.scalar_type() == torch::kLong, "x must be int64");
+  auto flag = torch::empty({1}, x.options().dtype(torch::kInt32));
+  ml_ok(ml_any_equal(x.data_ptr<int64_t>(), x.numel(), value, flag.data_ptr<int32_t>(),
+                     cur_stream()));
+  return flag;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -345,12 +383,32 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Mask matching, argument order used by MaskMatchingFunction (HIP)");
   m.def("mask_matching_backward", &mask_matching_backward, "Mask matching backward (HIP)");
   m.def("mask_matching_fused", &mask_matching_fused,
-        "Mask matching forward that also returns per-query statistics (HIP)");
+        "Mask matching forward that also returns the saved state for the fused backward and "
+        "optionally zero-fills the gradient buffer beside the assignment (HIP)",
+        py::arg("mask_logits"), py::arg("mask_targets"), py::arg("cls_logits"),
+        py::arg("cls_targets"), py::arg("smooth"), py::arg("sigmoid_scale"), py::arg("dice_scale"),
+        py::arg("cls_scale"), py::arg("background_index"), py::arg("uncertainty_gamma"),
+        py::arg("uncertainty_gamma_min"), py::arg("inf_thresh"), py::arg("num_masks"),
+        py::arg("force_unmatched_class_to_background"), py::arg("force_unmatched_masks_to_empty"),
+        py::arg("topk_matches"), py::arg("strategy_id"), py::arg("mask_gamma"),
+        py::arg("mask_alpha"), py::arg("cls_gamma"), py::arg("cls_alpha"),
+        py::arg("void_class_index"), py::arg("use_softmax_label_loss"),
+        py::arg("normalize_uncertainty"), py::arg("grad_prefill") = py::none());
   m.def("mask_matching_backward_fused", &mask_matching_backward_fused,
-        "Mask matching backward using saved per-query statistics (HIP)");
+        "Mask matching backward using the forward's saved state (HIP)", py::arg("g_mask"),
+        py::arg("g_dice"), py::arg("g_cls"), py::arg("mask_logits"), py::arg("mask_targets"),
+        py::arg("cls_logits"), py::arg("cls_targets"), py::arg("pred_to_gt"), py::arg("smooth"),
+        py::arg("sigmoid_scale"), py::arg("dice_scale"), py::arg("cls_scale"),
+        py::arg("background_index"), py::arg("uncertainty_gamma"),
+        py::arg("uncertainty_gamma_min"), py::arg("num_masks"),
+        py::arg("force_unmatched_class_to_background"), py::arg("force_unmatched_masks_to_empty"),
+        py::arg("mask_gamma"), py::arg("mask_alpha"), py::arg("cls_gamma"), py::arg("cls_alpha"),
+        py::arg("void_class_index"), py::arg("use_softmax_label_loss"),
+        py::arg("normalize_uncertainty"), py::arg("saved"), py::arg("grad_prefill") = py::none());
   m.def("forward_pw_sigmoid_label_loss", &forward_pw_sigmoid_label_loss,
         "Pairwise sigmoid label cost forward (HIP)");
   m.def("forward_pw_softmax_label_loss", &forward_pw_softmax_label_loss,
         "Pairwise softmax label cost forward (HIP)");
+  m.def("any_equal", &any_equal, "Device flag: any element equal to value (HIP)");
   m.attr("__backend__") = "hip-gfx950";
 }

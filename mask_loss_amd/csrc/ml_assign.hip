@@ -397,6 +397,9 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   int* hrows = (int*)(smem + L.hrows);
   int* asg = (int*)(smem + L.asg);
 
+  // A serial, latency-bound chain: take issue priority over waves of other
+  // kernels sharing the CU (the gradient prefill runs beside this kernel).
+  __builtin_amdgcn_s_setprio(3);
   const int64_t lb = blockIdx.x, b = lb % a.B;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t Q = a.Q, GTo = a.GT_out;
@@ -654,28 +657,55 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
 
 
 // Per-layer means and denominators (src/cuda/mask_matching_forward.cu:549-583).
-__global__ void layer_kernel(LayerArgs a) {
-  const int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (l >= a.L) return;
-  float m = 0.f, d = 0.f, c = 0.f, cnt = 0.f;
-  for (int64_t b = 0; b < a.B; ++b) {
-    const float* s = a.img + (l * a.B + b) * 4;
-    m += s[0];
-    d += s[1];
-    c += s[2];
-    cnt += s[3];
+// With a saved state, workgroup 0 also lists the matched query rows in
+// ascending order (wave ballots, one 1024-row chunk at a time) for the
+// backward.
+__global__ __launch_bounds__(1024) void layer_kernel(LayerArgs a) {
+  for (int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; l < a.L;
+       l += (int64_t)gridDim.x * blockDim.x) {
+    float m = 0.f, d = 0.f, c = 0.f, cnt = 0.f;
+    for (int64_t b = 0; b < a.B; ++b) {
+      const float* s = a.img + (l * a.B + b) * 4;
+      m += s[0];
+      d += s[1];
+      c += s[2];
+      cnt += s[3];
+    }
+    const float total = (float)(a.B * a.Q);
+    const bool has_nm = a.num_masks > 0.0;
+    float md = a.force_masks ? total : (has_nm ? (float)a.num_masks : cnt);
+    float cd = (a.force_cls || a.has_void) ? total : (has_nm ? (float)a.num_masks : cnt);
+    md = fmaxf(md, 1.f);
+    cd = fmaxf(cd, 1.f);
+    a.means[0 * a.L + l] = m / md;
+    a.means[1 * a.L + l] = d / md;
+    a.means[2 * a.L + l] = c / cd;
+    a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN] = 1.f / md;
+    a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / cd;
   }
-  const float total = (float)(a.B * a.Q);
-  const bool has_nm = a.num_masks > 0.0;
-  float md = a.force_masks ? total : (has_nm ? (float)a.num_masks : cnt);
-  float cd = (a.force_cls || a.has_void) ? total : (has_nm ? (float)a.num_masks : cnt);
-  md = fmaxf(md, 1.f);
-  cd = fmaxf(cd, 1.f);
-  a.means[0 * a.L + l] = m / md;
-  a.means[1 * a.L + l] = d / md;
-  a.means[2 * a.L + l] = c / cd;
-  a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN] = 1.f / md;
-  a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / cd;
+  if (a.list == nullptr || blockIdx.x != 0) return;
+  __shared__ int wcnt[16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t n = a.L * a.B * a.Q;
+  int base = 0;
+  for (int64_t r0 = 0; r0 < n; r0 += blockDim.x) {
+    const int64_t r = r0 + threadIdx.x;
+    const bool m = r < n && a.pred_to_gt[r] >= 0;
+    const uint64_t bal = __ballot(m);
+    if (lane == 0) wcnt[wave] = __popcll(bal);
+    __syncthreads();
+    int off = base, tot = base;
+    for (int w = 0; w < nw; ++w) {
+      off += w < wave ? wcnt[w] : 0;
+      tot += wcnt[w];
+    }
+    if (m) a.list[1 + off + __popcll(bal & below)] = (int)r;
+    __syncthreads();
+    base = tot;
+  }
+  if (threadIdx.x == 0) a.list[0] = base;
 }
 
 // Denominators from pred_to_gt alone (backward without saved statistics,
@@ -729,8 +759,6 @@ int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
 }
 
 int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
-  int rc = launch_finalize(a, d, st);
-  if (rc || a.costs_only) return rc;
   const int64_t nj = ceil_div(a.Q, 64);
   if (nj <= 1) return launch_nj<1>(a, d, st);
   if (nj <= 2) return launch_nj<2>(a, d, st);
@@ -743,7 +771,10 @@ int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
 int launch_layer(const LayerArgs& a, hipStream_t st) {
   {
     ProfScope ps_("layer", st);
-    hipLaunchKernelGGL(layer_kernel, dim3((unsigned)ceil_div(a.L, 64)), dim3(64), 0, st, a);
+    if (a.list)
+      hipLaunchKernelGGL(layer_kernel, dim3(1), dim3(1024), 0, st, a);
+    else
+      hipLaunchKernelGGL(layer_kernel, dim3((unsigned)ceil_div(a.L, 64)), dim3(64), 0, st, a);
   }
   return check_launch("layer");
 }

@@ -14,6 +14,9 @@
 // Class logits (src/cuda/mask_matching_backward.cu:218-376): one wave per
 // query row, sigmoid one-hot BCE or softmax CE gradients with the reference's
 // void / background rules.
+#include <algorithm>
+#include <atomic>
+
 #include "ml_internal.h"
 
 namespace ml {
@@ -223,9 +226,10 @@ __global__ __launch_bounds__(256) void bwd_mask_kernel(BwdArgs a) {
 // grid: L*B*Q * ceil(HW / kBwdChunk)
 constexpr int kBwdU = 4;
 constexpr int64_t kBwdChunk = 256 * 8 * kBwdU;
+constexpr int64_t kBwdListGrid = 2048;  // workgroups of the matched-list kernel (8 per CU)
 
-__global__ __launch_bounds__(256) void bwd_mask_chunk_kernel(BwdArgs a, int64_t nchunk) {
-  const int64_t row = (int64_t)blockIdx.x / nchunk, chunk = (int64_t)blockIdx.x % nchunk;
+// One chunk of kBwdChunk cells of one row.
+__device__ __forceinline__ void bwd_chunk(const BwdArgs& a, int64_t row, int64_t chunk) {
   const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
   const int tid = threadIdx.x;
   const int64_t out = a.pred_to_gt[row];
@@ -271,6 +275,231 @@ __global__ __launch_bounds__(256) void bwd_mask_chunk_kernel(BwdArgs a, int64_t 
       for (int k = 0; k < 8; ++k) gr[k] = grad_elem(z[u][k], matched ? t[u][k] : 0.f, ep, a.N2, rc);
       store8(a.grad, a.dtype, rbase + cell0, gr, a.HW - cell0, vec);
     }
+  }
+}
+
+// Every row.  grid: L*B*Q * nchunk
+__global__ __launch_bounds__(256) void bwd_mask_chunk_kernel(BwdArgs a, int64_t nchunk) {
+  bwd_chunk(a, (int64_t)blockIdx.x / nchunk, (int64_t)blockIdx.x % nchunk);
+}
+
+// Only the rows of the forward's matched list (the rest of the gradient
+// already holds zeros); the grid strides over (list entry, chunk) items, so
+// its size does not depend on the device-side match count.
+__global__ __launch_bounds__(256) void bwd_mask_list_kernel(BwdArgs a, int64_t nchunk) {
+  const int64_t rows = a.L * a.B * a.Q;
+  const int64_t n = min((int64_t)a.list[0], rows);
+  for (int64_t it = blockIdx.x; it < n * nchunk; it += gridDim.x) {
+    const int64_t row = a.list[1 + it / nchunk];
+    if (row >= 0 && row < rows) bwd_chunk(a, row, it % nchunk);
+  }
+}
+
+// ---- bf16 logits: the per-logit gradient terms from an LDS table ------------
+// The mask-logit gradient of a cell with target count tk is
+//   mc sf (Fpos tk + Fneg (N2 - tk)) + dc kd Fd (num N2 - 2 D tk)
+// with three functions of the logit alone,
+//   Fneg = w an mn (g (1-p) cn + p),  Fpos = -w ap mp (g p cp + 1-p),  Fd = w p (1-p),
+// which the table holds in float32 (16 bytes per entry) for every bf16 value
+// with |z| in [2^-16, 64); |z| < 2^-16 reads the z = 0 entry (relative change
+// below 2^-17); |z| >= 64, inf and nan read a NaN marker, and such cells are
+// recomputed from the formulas.
+constexpr uint32_t kGBase = 111u << 7;          // bf16 magnitude bits of 2^-16
+constexpr uint32_t kGOver = 0x4280u;            // bf16 magnitude bits of 64.0
+constexpr uint32_t kGN = kGOver - kGBase;       // 2816 regular entries
+constexpr uint32_t kGSub = kGBase - 1;          // idx = sat(m - kGSub): 0 = tiny
+constexpr uint32_t kGBlock = kGN + 2;           // tiny + regular + overflow slot
+constexpr uint32_t kGBytes = 2 * kGBlock * 16;  // both signs: 90176 bytes
+constexpr int kLutThreads = 1024;
+constexpr int kLutU = 2;                        // 8-cell groups per thread per item
+constexpr int64_t kLutChunk = (int64_t)kLutThreads * 8 * kLutU;
+
+__device__ __forceinline__ float4 grad_terms(float z, const ElemParams& ep) {
+  const Sig s = sig_terms(z);
+  const float w = unc_weight(s, ep);
+  float mn, mp;
+  focal_mods(s, ep, mn, mp);
+  const float g = ep.gamma;
+  return make_float4(w * ep.an * mn * (g * s.q1 * s.cn + s.p),
+                     -w * ep.ap * mp * (g * s.p * s.cp + s.q1), w * s.p * s.q1, 0.f);
+}
+
+__device__ void build_grad_lut(float4* lut, const ElemParams& ep) {
+  for (uint32_t e = threadIdx.x; e < 2 * kGBlock; e += blockDim.x) {
+    const uint32_t sgn = e >= kGBlock ? 1u : 0u;
+    const uint32_t j = e - sgn * kGBlock;
+    float4 v;
+    if (j <= kGN) {
+      const uint32_t mag = j == 0 ? 0u : kGSub + j;
+      v = grad_terms(__uint_as_float(((sgn << 15) | mag) << 16), ep);
+    } else {
+      v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), 0.f);
+    }
+    lut[e] = v;
+  }
+}
+
+// table entries of the two bf16 logits packed in `u`
+__device__ __forceinline__ void lut_pair(uint32_t u, const float4* lut, float4& lo, float4& hi) {
+  const uint32_t m = u & 0x7FFF7FFFu;
+  uint32_t idx = pk_min_u16(pk_sub_sat_u16(m, kGSub * 0x10001u), (kGN + 1) * 0x10001u);
+  idx += ((u >> 15) & 0x00010001u) * kGBlock;  // negative block (no carry: idx < 2^15)
+  lo = lut[idx & 0xFFFFu];
+  hi = lut[idx >> 16];
+}
+
+// One work item of the table kernel: kLutU groups of 8 cells of one row, as
+// loaded (raw bf16 logits and raw targets) plus the row's scalars.
+struct LutItem {
+  int64_t row, cell0;
+  int64_t out;           // pred_to_gt of the row
+  float S, P, I, T, mc, dc;
+  uint4 z[kLutU];        // 8 bf16 logits per group
+  uint4 lab[kLutU];      // 8 u16 labels (s == 1) or 8 u8 counts in .x/.y (s > 1)
+};
+
+template <bool CNT>
+__device__ __forceinline__ void lut_load(const BwdArgs& a, int64_t it, int64_t nchunk, bool vec,
+                                         LutItem& m) {
+  m.row = a.list ? a.list[1 + it / nchunk] : it / nchunk;
+  if (m.row < 0 || m.row >= a.L * a.B * a.Q) {  // not a row of this call: skip the item
+    m.row = -1;
+    return;
+  }
+  const int64_t lb = m.row / a.Q, l = lb / a.B, b = lb % a.B;
+  m.cell0 = (it % nchunk) * kLutChunk + (int64_t)threadIdx.x * 8;
+  m.out = a.pred_to_gt[m.row];
+  const float* st = a.stats + m.row * ML_STATS;
+  m.S = st[ML_STAT_S];
+  m.P = st[ML_STAT_P];
+  m.I = st[ML_STAT_I];
+  m.T = st[ML_STAT_T];
+  const float inv_md = a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN];
+  m.mc = a.g_mask[l] * inv_md;
+  m.dc = a.g_dice[l] * inv_md;
+  const int64_t act = m.out + (m.out >= a.bg ? 1 : 0);
+  const int64_t actc = m.out >= 0 && act < a.GT_total ? act : 0;  // a valid slot to read
+  const int64_t rbase = m.row * a.HW;
+#pragma unroll
+  for (int u = 0; u < kLutU; ++u) {
+    const int64_t c = m.cell0 + u * kLutThreads * 8;
+    m.z[u] = make_uint4(0, 0, 0, 0);
+    m.lab[u] = make_uint4(0, 0, 0, 0);
+    if (c < a.HW) {
+      if (vec) {
+        m.z[u] = *(const uint4*)((const uint16_t*)a.logits + rbase + c);
+      } else {
+        const uint16_t* h = (const uint16_t*)a.logits + rbase + c;
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = c + 2 * k < a.HW ? h[2 * k] : 0u;
+          const uint32_t hi = c + 2 * k + 1 < a.HW ? h[2 * k + 1] : 0u;
+          w[k] = lo | (hi << 16);
+        }
+        m.z[u] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+      if constexpr (CNT) {
+        const uint2 cv = *(const uint2*)(a.counts8 + (b * a.GT_total + actc) * a.HWp + c);
+        m.lab[u] = make_uint4(cv.x, cv.y, 0, 0);
+      } else {
+        m.lab[u] = *(const uint4*)(a.lab16 + b * a.HWp + c);
+      }
+    }
+  }
+}
+
+template <bool CNT>
+__device__ __forceinline__ void lut_compute_store(const BwdArgs& a, const LutItem& m,
+                                                  const float4* lut, bool vec) {
+  if (m.row < 0) return;
+  const int64_t act = m.out + (m.out >= a.bg ? 1 : 0);
+  const bool matched = m.out >= 0 && act < a.GT_total;
+  const int64_t rbase = m.row * a.HW;
+  if ((!matched && !a.force_masks) || (m.mc == 0.f && m.dc == 0.f)) {
+    const float zero[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < kLutU; ++u) {
+      const int64_t c = m.cell0 + u * kLutThreads * 8;
+      if (c < a.HW) store8(a.grad, ML_BF16, rbase + c, zero, a.HW - c, vec);
+    }
+    return;
+  }
+  const RowCoef rc = row_coef(a, m.S, m.P, matched ? m.I : 0.f, matched ? m.T : 0.f, m.mc, m.dc);
+  const float cs = rc.mc * rc.sf;
+  const float c2 = rc.dc * rc.kd * rc.num * a.N2;
+  const float c3 = rc.dc * rc.kd * 2.f * rc.D;
+  const uint32_t act32 = matched ? (uint32_t)act : 0xFFFFFFFFu;
+#pragma unroll
+  for (int u = 0; u < kLutU; ++u) {
+    const int64_t c = m.cell0 + u * kLutThreads * 8;
+    if (c >= a.HW) continue;
+    const uint32_t zw[4] = {m.z[u].x, m.z[u].y, m.z[u].z, m.z[u].w};
+    float t[8];
+    if constexpr (CNT) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        t[k] = matched ? (float)(((k < 4 ? m.lab[u].x : m.lab[u].y) >> ((k & 3) * 8)) & 0xFFu) : 0.f;
+    } else {
+      const uint32_t lw[4] = {m.lab[u].x, m.lab[u].y, m.lab[u].z, m.lab[u].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        t[2 * k] = (lw[k] & 0xFFFFu) == act32 ? 1.f : 0.f;
+        t[2 * k + 1] = (lw[k] >> 16) == act32 ? 1.f : 0.f;
+      }
+    }
+    float gr[8];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float4 e[2];
+      lut_pair(zw[i], lut, e[0], e[1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float tk = t[2 * i + h];
+        float g;
+        if constexpr (CNT) {
+          g = cs * (e[h].y * tk + e[h].x * fmaxf(a.N2 - tk, 0.f)) + e[h].z * (c2 - c3 * tk);
+        } else {  // tk in {0, 1}, N2 = 1
+          const bool pos = tk != 0.f;
+          g = cs * (pos ? e[h].y : e[h].x) + e[h].z * (pos ? c2 - c3 : c2);
+        }
+        bad |= g != g;
+        gr[2 * i + h] = g;
+      }
+    }
+    if (__builtin_expect(bad, 0)) {  // table overflow marker (|z| >= 64, inf, nan): formulas
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float z = (k & 1) ? bf16_hi(zw[k >> 1]) : bf16_lo(zw[k >> 1]);
+        if (gr[k] != gr[k]) gr[k] = grad_elem(z, t[k], a.mask_ep, a.N2, rc);
+      }
+    }
+    store8(a.grad, ML_BF16, rbase + c, gr, a.HW - c, vec);
+  }
+}
+
+// Persistent: one workgroup per CU builds the table, then strides over the
+// (row, chunk) items -- the forward's matched rows when `list` is set, every
+// row otherwise -- loading item i+1 while item i is computed and stored.
+template <bool CNT>
+__global__ __launch_bounds__(kLutThreads) void bwd_mask_lut_kernel(BwdArgs a, int64_t nchunk) {
+  __shared__ float4 lut[2 * kGBlock];
+  build_grad_lut(lut, a.mask_ep);
+  __syncthreads();
+  const int64_t rows = a.L * a.B * a.Q;
+  const int64_t nrows = a.list ? min((int64_t)a.list[0], rows) : rows;
+  const int64_t total = nrows * nchunk;
+  const bool vec = a.HW % 8 == 0;
+  int64_t it = blockIdx.x;
+  if (it >= total) return;
+  LutItem cur, nxt;
+  lut_load<CNT>(a, it, nchunk, vec, cur);
+  for (; it < total; it += gridDim.x) {
+    const int64_t it2 = it + gridDim.x;
+    if (it2 < total) lut_load<CNT>(a, it2, nchunk, vec, nxt);
+    lut_compute_store<CNT>(a, cur, lut, vec);
+    cur = nxt;
   }
 }
 
@@ -365,11 +594,38 @@ __global__ __launch_bounds__(256) void bwd_cls_kernel(BwdArgs a) {
   }
 }
 
+// One persistent workgroup per CU (the 90 KB table allows one per CU).
+static int lut_grid() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1)
+      v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 int launch_bwd(const BwdArgs& a, const Dims& d, hipStream_t st) {
   const int64_t rows = d.L * d.B * d.Q;
   if (rows > 0 && d.HW > 0) {
     ProfScope ps_("bwd_mask", st);
-    if (a.stats) {
+    if (a.stats && a.dtype == ML_BF16 && g_use_lut) {
+      const int64_t nchunk = ceil_div(d.HW, kLutChunk);
+      const int64_t grid = std::min<int64_t>(rows * nchunk, lut_grid());
+      if (d.counts_mode)
+        hipLaunchKernelGGL(bwd_mask_lut_kernel<true>, dim3((unsigned)grid), dim3(kLutThreads), 0,
+                           st, a, nchunk);
+      else
+        hipLaunchKernelGGL(bwd_mask_lut_kernel<false>, dim3((unsigned)grid), dim3(kLutThreads), 0,
+                           st, a, nchunk);
+    } else if (a.stats && a.list) {
+      const int64_t nchunk = ceil_div(d.HW, kBwdChunk);
+      const int64_t grid = std::min<int64_t>(rows * nchunk, kBwdListGrid);
+      hipLaunchKernelGGL(bwd_mask_list_kernel, dim3((unsigned)grid), dim3(256), 0, st, a, nchunk);
+    } else if (a.stats) {
       const int64_t nchunk = ceil_div(d.HW, kBwdChunk);
       hipLaunchKernelGGL(bwd_mask_chunk_kernel, dim3((unsigned)(rows * nchunk)), dim3(256), 0, st,
                          a, nchunk);

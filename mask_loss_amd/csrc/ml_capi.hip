@@ -78,6 +78,36 @@ void prof_end(const char* name, hipStream_t st) {
   }
 }
 
+// ---- side stream for the gradient prefill --------------------------------------
+// One non-blocking stream (default priority) and a fork / join event pair per
+// device, created on first use and kept for the life of the process.  The
+// mutex keeps each record -> wait pair of one call together when several host
+// threads share a device.
+namespace {
+struct Side {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_side_mu;
+Side g_side[kMaxDevices];
+}  // namespace
+
+static int side_stream(Side** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(ML_ELAUNCH, "prefill: no current HIP device");
+  Side& sd = g_side[dev];
+  if (!sd.s) {
+    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess)
+      return fail(ML_ELAUNCH, "prefill: cannot create the side stream");
+  }
+  *out = &sd;
+  return ML_OK;
+}
+
 constexpr size_t kMaxLds = 160 * 1024;
 
 bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
@@ -219,14 +249,22 @@ static bool dtype_ok(int dt) { return dt == ML_F32 || dt == ML_BF16 || dt == ML_
 static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                         const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
                         const void* cls_logits, const int64_t* cls_targets, int64_t* pred_to_gt,
-                        int64_t* pred_round, float* layer_means, float* sep, float* stats,
-                        void* ws, size_t ws_bytes, hipStream_t st, bool costs_only) {
+                        int64_t* pred_round, float* layer_means, float* sep, void* saved,
+                        void* prefill, void* ws, size_t ws_bytes, hipStream_t st,
+                        bool costs_only) {
   if (!dtype_ok(mask_dtype) || !dtype_ok(cls_dtype)) return fail(ML_EINVAL, "unsupported dtype");
   Dims d;
   std::string err;
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
   const bool force_masks = !costs_only && p->force_unmatched_masks_to_empty;
+  if (prefill && (force_masks || costs_only || !saved))
+    return fail(ML_EINVAL, "gradient prefill needs a saved state and unforced unmatched masks");
+  if (((uintptr_t)prefill & 15) || ((uintptr_t)saved & 255))
+    return fail(ML_EINVAL, "the prefill buffer must be 16-byte and the saved state 256-byte aligned");
   const bool in_lds = cost_fits_lds(d);
+  const SavedLayout SL = saved_layout(d);
+  unsigned char* sv = (unsigned char*)saved;
+  float* stats = saved ? (float*)(sv + SL.stats) : nullptr;
   const Layout L = make_layout(d, force_masks, !in_lds);
   if (ws_bytes < L.total) return fail(ML_EWORKSPACE, "workspace too small");
   unsigned char* w = (unsigned char*)ws;
@@ -237,7 +275,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   const CostPlan plan = make_cost_plan(d, mask_dtype, tab);
   PrepArgs pa;
   pa.targets = mask_targets;
-  pa.lab16 = (uint16_t*)(w + L.lab16);
+  // with a saved state the compact labels go straight into it (the backward reuses them)
+  pa.lab16 = (uint16_t*)(saved && !d.counts_mode ? sv + SL.lab16 : w + L.lab16);
   pa.counts8 = (uint8_t*)(w + L.counts8);
   pa.present = (int*)(w + L.present);
   pa.ncols = (int*)(w + L.ncols);
@@ -320,13 +359,41 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.strategy = (int)p->strategy_id;
   aa.costs_only = costs_only;
   aa.cost_in_lds = in_lds;
-  if (d.LB > 0 && (rc = launch_assign(aa, d, st))) return rc;
+  if (d.LB > 0 && (rc = launch_finalize(aa, d, st))) return rc;
   if (costs_only) return ML_OK;
+  // The assignment occupies one workgroup per image and leaves HBM idle: the
+  // zero fill of the gradient buffer runs beside it on the side stream.
+  const size_t prefill_bytes =
+      prefill ? (size_t)(d.LB * d.Q * d.HW) * (mask_dtype == ML_F32 ? 4 : 2) : 0;
+  Side* sd = nullptr;
+  std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
+  if (prefill_bytes) {
+    side_lock.lock();
+    if ((rc = side_stream(&sd))) return rc;
+    if (hipEventRecord(sd->fork, st) != hipSuccess ||
+        hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
+      return fail(ML_ELAUNCH, "prefill: fork failed");
+    {
+      ProfScope ps_("prefill", sd->s);
+      if ((rc = launch_zero_fill(prefill, prefill_bytes, sd->s))) return rc;
+    }
+    if (hipEventRecord(sd->join, sd->s) != hipSuccess)
+      return fail(ML_ELAUNCH, "prefill: join record failed");
+  }
+  rc = d.LB > 0 ? launch_assign(aa, d, st) : ML_OK;
+  if (prefill_bytes) {  // join even after a failed launch: the buffer is the caller's
+    if (hipStreamWaitEvent(st, sd->join, 0) != hipSuccess && rc == ML_OK)
+      rc = fail(ML_ELAUNCH, "prefill: join failed");
+    side_lock.unlock();
+  }
+  if (rc) return rc;
 
   LayerArgs la;
   la.img = aa.img;
   la.layer = stats ? stats + d.LB * d.Q * ML_STATS : (float*)(w + L.layer);
   la.means = layer_means;
+  la.pred_to_gt = pred_to_gt;
+  la.list = saved ? (int*)(sv + SL.list) : nullptr;
   la.L = d.L; la.B = d.B; la.Q = d.Q;
   la.num_masks = p->num_masks;
   la.force_masks = force_masks;
@@ -386,8 +453,16 @@ int ml_profile_read(const char* name, int64_t* launches, double* total_ms) {
 }
 int ml_version(void) { return 1; }
 
-size_t ml_stats_floats(const ml_shape* s) {
-  return (size_t)(s->L * s->B * s->Q * ML_STATS + s->L * ML_LAYERS);
+int ml_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, ml_stream_t stream) {
+  if (n < 0 || (n > 0 && !x) || !flag) return fail(ML_EINVAL, "any_equal: bad arguments");
+  return launch_any_equal(x, n, value, flag, (hipStream_t)stream);
+}
+
+size_t ml_saved_bytes(const ml_shape* s, const ml_params* p, int mask_dtype) {
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  return saved_layout(d).total;
 }
 
 size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p, int mask_dtype) {
@@ -409,13 +484,13 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
                              const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
                              const void* cls_logits, const int64_t* cls_targets,
                              int64_t* pred_to_gt, int64_t* pred_round, float* layer_means,
-                             float* separate_costs, float* stats, void* workspace,
-                             size_t workspace_bytes, ml_stream_t stream) {
+                             float* separate_costs, void* saved, void* grad_mask_prefill,
+                             void* workspace, size_t workspace_bytes, ml_stream_t stream) {
   int rc = check_params(p, s->C, true);
   if (rc) return rc;
   return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
-                      cls_targets, pred_to_gt, pred_round, layer_means, separate_costs, stats,
-                      workspace, workspace_bytes, (hipStream_t)stream, false);
+                      cls_targets, pred_to_gt, pred_round, layer_means, separate_costs, saved,
+                      grad_mask_prefill, workspace, workspace_bytes, (hipStream_t)stream, false);
 }
 
 int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
@@ -426,8 +501,8 @@ int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mas
   int rc = check_params(p, s->C, false);
   if (rc) return rc;
   return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
-                      cls_targets, nullptr, nullptr, nullptr, separate_costs, nullptr, workspace,
-                      workspace_bytes, (hipStream_t)stream, true);
+                      cls_targets, nullptr, nullptr, nullptr, separate_costs, nullptr, nullptr,
+                      workspace, workspace_bytes, (hipStream_t)stream, true);
 }
 
 size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,
@@ -449,9 +524,9 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
                               const float* grad_dice, const float* grad_cls, int mask_dtype,
                               const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
                               const void* cls_logits, const int64_t* cls_targets,
-                              const int64_t* pred_to_gt, const float* stats,
-                              void* grad_mask_logits, void* grad_cls_logits, void* workspace,
-                              size_t workspace_bytes, ml_stream_t stream) {
+                              const int64_t* pred_to_gt, const void* saved,
+                              int grad_prefilled, void* grad_mask_logits, void* grad_cls_logits,
+                              void* workspace, size_t workspace_bytes, ml_stream_t stream) {
   int rc = check_params(p, s->C, true);
   if (rc) return rc;
   if (!dtype_ok(mask_dtype) || !dtype_ok(cls_dtype)) return fail(ML_EINVAL, "unsupported dtype");
@@ -460,6 +535,11 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
   if (workspace_bytes < ml_mask_matching_backward_workspace_size(s, p, mask_dtype))
     return fail(ML_EWORKSPACE, "workspace too small");
+  if (grad_prefilled && (!saved || p->force_unmatched_masks_to_empty))
+    return fail(ML_EINVAL, "a prefilled gradient needs the saved state and unforced unmatched masks");
+  const SavedLayout SL = saved_layout(d);
+  const unsigned char* sv = (const unsigned char*)saved;
+  const float* stats = saved ? (const float*)(sv + SL.stats) : nullptr;
   hipStream_t st = (hipStream_t)stream;
   unsigned char* w = (unsigned char*)workspace;
   size_t o = 0;
@@ -481,7 +561,10 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
   pa.sched = nullptr;
   pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = CostPlan{};
-  if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
+  // the forward's saved state holds the compact label map for s == 1
+  const bool saved_labels = saved && !d.counts_mode;
+  if (saved_labels) pa.lab16 = (uint16_t*)(sv + SL.lab16);
+  else if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
 
   const int64_t void_idx =
       (p->void_class_index >= 0 && p->void_class_index < d.C) ? p->void_class_index : -1;
@@ -503,6 +586,7 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   ba.counts8 = d.counts_mode ? pa.counts8 : nullptr;
   ba.pred_to_gt = pred_to_gt;
   ba.stats = stats;
+  ba.list = grad_prefilled ? (const int*)(sv + SL.list) : nullptr;
   ba.layer = layer;
   ba.g_mask = grad_mask;
   ba.g_dice = grad_dice;

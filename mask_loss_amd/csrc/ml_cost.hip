@@ -58,11 +58,6 @@ constexpr uint32_t kLutNegOff = 32768;
 constexpr uint32_t kLutBytes = kLutNegOff + kLutBlock * 8;
 constexpr int kDepth = 4;  // K-steps of logits in flight per wave
 
-__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
 __device__ __forceinline__ uint32_t pk_lshl3_u16(uint32_t a) {
   uint32_t r;
   asm("v_pk_lshlrev_b16 %0, %1, %2" : "=v"(r) : "v"(0x00030003u), "v"(a));

@@ -12,6 +12,9 @@
 
 namespace ml {
 
+// bf16 per-cell terms from LDS tables (1, default) or from the formulas (0, tests).
+extern int g_use_lut;
+
 // Set the thread-local error message returned by ml_last_error().
 void set_error(const std::string& msg);
 int fail(int code, const std::string& msg);
@@ -103,6 +106,23 @@ struct Dims {
 bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d, std::string& err);
 int cost_rt_for(int dtype, int NT);
 
+// Byte offsets inside the forward's saved state (see ml_saved_bytes): the
+// float head (per-query stats, then the per-layer block), the matched-row list
+// (int32 count, then (l*B+b)*Q+q of every matched row, ascending), and for
+// s == 1 the compact label map lab16 [B][HWp].
+struct SavedLayout {
+  size_t stats, layer, list, lab16, total;
+};
+inline SavedLayout saved_layout(const Dims& d) {
+  SavedLayout S;
+  S.stats = 0;
+  S.layer = (size_t)d.LB * d.Q * ML_STATS * 4;
+  S.list = align256(S.layer + (size_t)d.L * ML_LAYERS * 4);
+  S.lab16 = align256(S.list + (size_t)(1 + d.LB * d.Q) * 4);
+  S.total = align256(S.lab16 + (d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
+  return S;
+}
+
 // Byte offsets inside the caller's workspace.
 struct Layout {
   size_t lab16, counts8, present, ncols, colmap, slot_of_col, sched, partials, rowsum, flags,
@@ -189,6 +209,8 @@ struct LayerArgs {
   const float* img;
   float* layer;        // [L][ML_LAYERS]
   float* means;        // (3, L)
+  const int64_t* pred_to_gt;
+  int* list;           // matched-row list of the saved state, or null
   int64_t L, B, Q;
   double num_masks;
   int force_masks, force_cls, has_void;
@@ -201,6 +223,7 @@ struct BwdArgs {
   const uint8_t* counts8;
   const int64_t* pred_to_gt;
   const float* stats;     // per-query stats or null
+  const int* list;        // matched-row list (count, rows): only these rows are written
   const float* layer;     // [L][ML_LAYERS]
   const float* g_mask;
   const float* g_dice;
@@ -233,6 +256,7 @@ struct ProfScope {
 // ---- launchers (defined in the kernels' translation units) ---------------------
 int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st);
 int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool force_masks, hipStream_t st);
+int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st);
 int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st);
 int launch_layer(const LayerArgs& a, hipStream_t st);
 int launch_layer_from_p2g(const int64_t* p2g, float* layer, int64_t L, int64_t B, int64_t Q,
@@ -244,5 +268,7 @@ int launch_label_cost(const void* cls_logits, int cls_dtype, const int64_t* cls_
                       int64_t GT_out, int64_t bg, float scale, const ElemParams& ep,
                       int use_softmax, float* out, hipStream_t st);
 int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st);
+int launch_zero_fill(void* p, size_t bytes, hipStream_t st);
+int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, hipStream_t st);
 
 }  // namespace ml

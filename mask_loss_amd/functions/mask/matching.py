@@ -8,8 +8,13 @@ differences are on the device side only:
   matching.py:109-112); gradients come back in the logits' dtype, which is
   what autograd produces from the reference's float32 gradients;
 * the forward keeps per-query statistics (uncertainty normaliser, mass,
-  intersection, target mass) so the backward reads every matched logit once
-  instead of twice (reference backward: mask_matching_backward.cu:110-215).
+  intersection, target mass), the matched rows and the compact label map, so
+  the backward reads every matched logit once instead of twice (reference
+  backward: mask_matching_backward.cu:110-215) and skips target preparation;
+* when the mask logits need a gradient (and unmatched masks are not forced to
+  empty, so unmatched rows have zero gradient), the forward allocates the
+  gradient tensor and zero-fills it on a side stream while the assignment
+  runs; the first backward then writes only the matched rows into it.
 """
 from __future__ import annotations
 
@@ -87,29 +92,49 @@ class MaskMatchingFunction(Function):
             void = int(void_class_index)
             if not (0 <= void < C):
                 raise ValueError("incorrect void index")
-        if void != -1 and torch.any(cls_targets == void):
-            raise ValueError("cls_targets must not contain the void class index")
+        # The void-class check (reference: a synchronous torch.any before any
+        # work) is started here and read at the end of forward: its flag
+        # travels to pinned host memory while the forward's kernels are
+        # queued, so the host never drains the GPU before launching them.
+        void_flag = None
+        if void != -1:
+            void_flag = mask_loss.any_equal(cls_targets, void).to("cpu", non_blocking=True)
+            void_ready = torch.cuda.Event()
+            void_ready.record()
         use_softmax = label_kind(label_loss)
         if use_softmax and force_cls and void == -1:
             raise ValueError("void_class_index must be provided when using softmax label loss "
                              "and forcing unmatched predictions to background")
 
         args = (smooth_val, sigmoid_scale_val, dice_scale_val, cls_scale_val, bg, ug, ugm)
-        pred_to_gt, pred_round, m, d, c, stats = mask_loss.mask_matching_fused(
+        prefill = None
+        if ctx.needs_input_grad[0] and not force_masks:
+            prefill = torch.empty_like(mask_logits, memory_format=torch.contiguous_format)
+        pred_to_gt, pred_round, m, d, c, saved = mask_loss.mask_matching_fused(
             mask_logits, mask_targets, cls_logits, cls_targets, *args, inf_thresh_val,
             num_masks_val, force_cls, force_masks, K_val, STRATEGIES[strategy], mg, ma, cg, ca,
-            void, use_softmax, normalize)
+            void, use_softmax, normalize, prefill)
         ctx.save_for_backward(mask_logits.detach(), mask_targets.detach(), cls_logits.detach(),
-                              cls_targets.detach(), pred_to_gt.detach(), stats)
+                              cls_targets.detach(), pred_to_gt.detach(), saved)
+        # the zero-filled gradient buffer serves the first backward only (a
+        # second backward through a retained graph gets a fresh tensor)
+        ctx.prefill = prefill
         ctx.bwd_args = (smooth_val, sigmoid_scale_val, dice_scale_val, cls_scale_val, bg, ug, ugm,
                         num_masks_val, force_cls, force_masks, mg, ma, cg, ca, void, use_softmax,
                         normalize)
+        if void_flag is not None:
+            void_ready.synchronize()
+            if int(void_flag[0]):
+                raise ValueError("cls_targets must not contain the void class index")
         ctx.mark_non_differentiable(pred_to_gt, pred_round)
+        # no zero gradients for the integer outputs (or unused means)
+        ctx.set_materialize_grads(False)
         return pred_to_gt, pred_round, m, d, c
 
     @staticmethod
     def backward(ctx, _, __, grad_layer_mask_mean, grad_layer_dice_mean, grad_layer_cls_mean):
-        mask_logits, mask_targets, cls_logits, cls_targets, pred_to_gt, stats = ctx.saved_tensors
+        mask_logits, mask_targets, cls_logits, cls_targets, pred_to_gt, saved = ctx.saved_tensors
+        prefill, ctx.prefill = ctx.prefill, None
 
         def g(x):
             return x.detach().float().contiguous() if x is not None else \
@@ -117,5 +142,6 @@ class MaskMatchingFunction(Function):
 
         grad_mask, grad_cls = mask_loss.mask_matching_backward_fused(
             g(grad_layer_mask_mean), g(grad_layer_dice_mean), g(grad_layer_cls_mean),
-            mask_logits, mask_targets, cls_logits, cls_targets, pred_to_gt, *ctx.bwd_args, stats)
+            mask_logits, mask_targets, cls_logits, cls_targets, pred_to_gt, *ctx.bwd_args, saved,
+            prefill)
         return (grad_mask, None, grad_cls) + (None,) * 21

@@ -151,13 +151,13 @@ def test_label_cost_ops(ml, softmax):
     close(got, ref, 1e-5, 1e-2)
 
 
-def matching_call(ml, x, P, M):
+def matching_call(ml, x, P, M, prefill=None):
     ss, ds, cs = P["scales"]
     return ml.mask_matching_fused(
         x["z"], x["tgt"], x["zc"], x["ct"], P["smooth"], ss, ds, cs, P["bg"], P["ug"], P["ug_min"],
         M["inf_thresh"], M["num_masks"], M["force_cls"], M["force_masks"], M["K"], M["strategy"],
         P["mask_gamma"], P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["void"],
-        P["use_softmax"], P["normalize"])
+        P["use_softmax"], P["normalize"], prefill)
 
 
 MATCH_CASES = [
@@ -192,7 +192,7 @@ def mparams(m):
 def test_matching_forward(ml, case):
     x = make_case(21, **case["kw"])
     P, M = params(case["p"]), mparams(case["m"])
-    p2g, pr, m, d, c, stats = [t.cpu() for t in matching_call(ml, x, P, M)]
+    p2g, pr, m, d, c, saved = [t.cpu() for t in matching_call(ml, x, P, M)]
     # 1. solver bit-exactness on the GPU's own float32 cost matrix
     sep = gpu_costs(ml, x, P)
     total = ((sep[0] + sep[1]) + sep[2]).double().cpu().numpy()
@@ -234,13 +234,19 @@ BWD_CASES = [
 ]
 
 
-@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("mode", ["saved", "prefilled", "two_pass"])
 @pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: c["name"])
-def test_matching_backward(ml, case, fused):
+def test_matching_backward(ml, case, mode):
     x = make_case(33, **case["kw"])
     P, M = params(case["p"]), mparams(case["m"])
-    outs = matching_call(ml, x, P, M)
-    p2g, stats = outs[0], outs[5]
+    prefill = None
+    if mode == "prefilled":
+        if M["force_masks"]:
+            pytest.skip("no prefill when unmatched masks are forced to empty")
+        # garbage in the buffer: the forward's side-stream fill must clear it
+        prefill = torch.full_like(x["z"], 7.0)
+    outs = matching_call(ml, x, P, M, prefill)
+    p2g, saved = outs[0], outs[5]
     L = x["z"].shape[0]
     gm = torch.tensor([0.7] * L, device="cuda")
     gd = torch.tensor([1.3] * L, device="cuda")
@@ -250,8 +256,11 @@ def test_matching_backward(ml, case, fused):
             P["ug"], P["ug_min"], M["num_masks"], M["force_cls"], M["force_masks"], P["mask_gamma"],
             P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["void"], P["use_softmax"],
             P["normalize"])
-    if fused:
-        gz, gzc = ml.mask_matching_backward_fused(*args, stats)
+    if mode == "saved":
+        gz, gzc = ml.mask_matching_backward_fused(*args, saved)
+    elif mode == "prefilled":
+        gz, gzc = ml.mask_matching_backward_fused(*args, saved, prefill)
+        assert gz.data_ptr() == prefill.data_ptr()
     else:
         gz, gzc = ml.mask_matching_backward(*args)
     assert gz.dtype == x["z"].dtype and gzc.dtype == x["zc"].dtype
@@ -287,6 +296,27 @@ def test_function_autograd_bf16(ml):
     close(zc.grad.cpu().numpy(), rzc, 1e-5, 1e-2 * np.abs(rzc).max())
 
 
+def test_function_double_backward_fresh_buffer(ml):
+    """The prefilled gradient buffer serves the first backward only; a second
+    backward through the retained graph allocates anew, so the first result
+    (held as .grad) is not overwritten."""
+    from mask_loss_amd.functions import MaskMatchingFunction
+    x = make_case(45, dtype="bfloat16", sigma=3.0, Q=40, G=12)
+    z = x["z"].clone().requires_grad_(True)
+    zc = x["zc"].clone().requires_grad_(True)
+    outs = MaskMatchingFunction.apply(
+        z, x["tgt"], zc, x["ct"], 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, True, 1e30, -1.0, True, False,
+        1, "global", 0.0, None, 0.0, None, 8, "softmax")
+    m, d, c = outs[2:]
+    g1 = torch.autograd.grad(m.sum() + d.sum() + c.sum(), [z], retain_graph=True)[0]
+    first = g1.clone()
+    g2 = torch.autograd.grad(2.0 * (m.sum() + d.sum() + c.sum()), [z])[0]
+    assert g1.data_ptr() != g2.data_ptr()
+    assert torch.equal(g1, first)
+    close(g2.float().cpu().numpy(), 2.0 * first.float().cpu().numpy(), 1e-2,
+          1e-2 * first.float().abs().max().item())
+
+
 def test_reference_wrapper_argument_order(ml):
     """The reference's MaskMatchingFunction calls mask_matching with 25
     positional arguments (normalize_uncertainty twice); both orders work."""
@@ -305,5 +335,8 @@ def test_deterministic(ml):
     P, M = params(dict(use_softmax=True)), mparams(dict(force_cls=True, void=8))
     a = [t.clone() for t in matching_call(ml, x, P, M)]
     b = [t.clone() for t in matching_call(ml, x, P, M)]
+    L, B, Q = a[0].shape
+    head = (L * B * Q * 4 + L * 2) * 4  # float head of the saved state: stats + layer block
+    a[5], b[5] = a[5][:head], b[5][:head]
     for u, v in zip(a, b):
         assert torch.equal(u, v)

@@ -22,6 +22,13 @@
  *   ml_pairwise_label_loss_forward  src/cuda/pw_sigmoid_label_loss.cu:108-187 and
  *                                   src/cuda/pw_softmax_label_loss.cu:105-173
  *                                   (bound at src/bindings.cpp:167-168)
+ *   ml_pairwise_sigmoid_dice_forward src/cuda/pw_sigmoid_ce.cu:199-316 and
+ *                                   src/cuda/pw_dice_loss.cu:111-221
+ *                                   (bound at src/bindings.cpp:159,162)
+ *   ml_sigmoid_ce_forward/backward  src/cuda/sigmoid_ce.cu:207-332
+ *                                   (bound at src/bindings.cpp:157-158)
+ *   ml_dice_loss_forward/backward   src/cuda/dice_loss.cu:159-289
+ *                                   (bound at src/bindings.cpp:160-161)
  */
 #ifndef MASK_LOSS_HIP_H
 #define MASK_LOSS_HIP_H
@@ -148,6 +155,54 @@ int ml_pairwise_label_loss_forward(int64_t L, int64_t B, int64_t Q, int64_t C,
                                    int64_t background_index, float scale, float gamma,
                                    float alpha, int use_softmax, float* out,
                                    ml_stream_t stream);
+
+/* ---- standalone pairwise sigmoid-BCE and dice costs (L,B,C,GT_out) float ----
+ * logits (L,B,C,H,W) as mask logits with s->Q = C channels; s->GT_total = the
+ * number of label slots (the reference takes targets.max()+1,
+ * src/cuda/pw_sigmoid_ce.cu:222-224, src/cuda/pw_dice_loss.cu:132-134);
+ * s->C and the class fields of `p` are unused.  bce_out / dice_out may each
+ * be NULL.  Fields used: background_index, sigmoid_scale (BCE scale),
+ * dice_scale (dice scale), smooth, mask_gamma / mask_alpha (BCE focal),
+ * uncertainty_gamma(_min), normalize_uncertainty (BCE).  Workspace: the
+ * size ml_pairwise_mask_loss_workspace_size() returns for the same shape.
+ * Replaces src/cuda/pw_sigmoid_ce.cu:199-316 (bound at src/bindings.cpp:159)
+ * and src/cuda/pw_dice_loss.cu:111-221 (bound at src/bindings.cpp:162). */
+int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int dtype,
+                                     const void* logits, const int64_t* targets,
+                                     float* bce_out, float* dice_out, void* workspace,
+                                     size_t workspace_bytes, ml_stream_t stream);
+
+/* ---- non-pairwise sigmoid-CE and dice losses over dense class logits --------
+ * logits (L,B,C,H,W) in `dtype`, targets (B,Ht,Wt) int64 class labels
+ * (labels outside [0,C) count for no class).  Workspace from
+ * ml_dense_loss_workspace_size(s, dtype, dice, backward).
+ *   ml_sigmoid_ce_forward   src/cuda/sigmoid_ce.cu:207-268  (src/bindings.cpp:157)
+ *   ml_sigmoid_ce_backward  src/cuda/sigmoid_ce.cu:270-332  (src/bindings.cpp:158)
+ *   ml_dice_loss_forward    src/cuda/dice_loss.cu:159-222   (src/bindings.cpp:160)
+ *   ml_dice_loss_backward   src/cuda/dice_loss.cu:224-289   (src/bindings.cpp:161)
+ * loss: (L,) float; I, P, T: (L,B,C) float; grad_out: (L,) float; grad: (L,B,C,H,W)
+ * in `dtype`.  Sums are float64 and reduced in a fixed order. */
+typedef struct ml_dense_shape {
+  int64_t L, B, C, H, W, Ht, Wt;
+} ml_dense_shape;
+size_t ml_dense_loss_workspace_size(const ml_dense_shape* s, int dtype, int dice, int backward);
+int ml_sigmoid_ce_forward(const ml_dense_shape* s, int dtype, const void* logits,
+                          const int64_t* targets, float num_masks, float scale, float gamma,
+                          float alpha, float* loss, void* workspace, size_t workspace_bytes,
+                          ml_stream_t stream);
+int ml_sigmoid_ce_backward(const ml_dense_shape* s, int dtype, const float* grad_out,
+                           const void* logits, const int64_t* targets, float num_masks,
+                           float scale, float gamma, float alpha, void* grad, void* workspace,
+                           size_t workspace_bytes, ml_stream_t stream);
+int ml_dice_loss_forward(const ml_dense_shape* s, int dtype, const void* logits,
+                         const int64_t* targets, float smooth, float num_masks, float scale,
+                         float* loss, float* I, float* P, float* T, void* workspace,
+                         size_t workspace_bytes, ml_stream_t stream);
+int ml_dice_loss_backward(const ml_dense_shape* s, int dtype, const float* grad_out,
+                          const void* logits, const int64_t* targets, const float* I,
+                          const float* P, const float* T, float smooth, float num_masks,
+                          float scale, void* grad, void* workspace, size_t workspace_bytes,
+                          ml_stream_t stream);
 
 /* ---- input validation helper ------------------------------------------------
  * flag[0] = 1 if any of x[0..n) equals `value`, else 0 (one small kernel, no

@@ -363,6 +363,170 @@ torch::Tensor forward_pw_softmax_label_loss(const torch::Tensor& logits,
   return label_impl(logits, targets, background_index, scale, 0.0, -1.0, true);
 }
 
+// --------------------------------------------------------------------------
+// standalone pairwise sigmoid CE / dice  (src/bindings.cpp:159,162)
+// --------------------------------------------------------------------------
+// GT_total = targets.max() + 1, read back to the host as the reference does
+// (src/cuda/pw_sigmoid_ce.cu:222-224, src/cuda/pw_dice_loss.cu:132-134).
+torch::Tensor pairwise_bd_impl(const torch::Tensor& logits, const torch::Tensor& targets,
+                               const ml_params& p, bool dice) {
+  ML_CHECK_INPUT(logits);
+  ML_CHECK_INPUT(targets);
+  TORCH_CHECK(logits.dim() == 5, "logits must be (L,B,C,H,W)");
+  TORCH_CHECK(targets.dim() == 3, "targets must be (B,H_t,W_t)");
+  TORCH_CHECK(targets.scalar_type() == torch::kLong, "targets must be int64");
+  TORCH_CHECK(targets.size(0) == logits.size(1), "Batch size mismatch between logits and targets");
+  TORCH_CHECK(targets.device() == logits.device(), "all tensors must be on the same device");
+  const int64_t gt_total =
+      targets.numel() > 0 ? std::max<int64_t>(targets.max().item<int64_t>() + 1, 0) : 0;
+  ml_shape s;
+  s.L = logits.size(0);
+  s.B = logits.size(1);
+  s.Q = logits.size(2);
+  s.H = logits.size(3);
+  s.W = logits.size(4);
+  s.Ht = targets.size(1);
+  s.Wt = targets.size(2);
+  s.C = 0;
+  s.GT_total = gt_total;
+  const int64_t GT_out = gt_out_of(gt_total, p.background_index);
+  auto f32 = logits.options().dtype(torch::kFloat32);
+  if (GT_out == 0) return torch::zeros({s.L, s.B, s.Q, 0}, f32);
+  auto out = torch::empty({s.L, s.B, s.Q, GT_out}, f32);
+  const int dt = dtype_code(logits, "logits");
+  const size_t wsb = ml_pairwise_mask_loss_workspace_size(&s, &p, dt);
+  TORCH_CHECK(wsb > 0 || s.B == 0, ml_last_error());
+  auto ws = workspace(wsb, logits);
+  ml_ok(ml_pairwise_sigmoid_dice_forward(&s, &p, dt, logits.data_ptr(),
+                                         targets.data_ptr<int64_t>(),
+                                         dice ? nullptr : out.data_ptr<float>(),
+                                         dice ? out.data_ptr<float>() : nullptr, ws.data_ptr(),
+                                         ws.numel(), cur_stream()));
+  return out;
+}
+
+torch::Tensor forward_pw_sigmoid_ce_loss(const torch::Tensor& logits, const torch::Tensor& targets,
+                                         int64_t background_index, double scale, double gamma,
+                                         double alpha, double ug, double ug_min, bool normalize) {
+  ml_params p = make_params(1.0, scale, 1.0, 1.0, background_index, ug, ug_min, 1e30, -1.0, false,
+                            false, 1, 0, gamma, alpha, 0.0, -1.0, -1, false, normalize);
+  return pairwise_bd_impl(logits, targets, p, false);
+}
+
+torch::Tensor forward_pw_dice_loss(const torch::Tensor& logits, const torch::Tensor& targets,
+                                   double smooth, int64_t background_index, double scale,
+                                   double ug, double ug_min) {
+  ml_params p = make_params(smooth, 1.0, scale, 1.0, background_index, ug, ug_min, 1e30, -1.0,
+                            false, false, 1, 0, 0.0, -1.0, 0.0, -1.0, -1, false, true);
+  return pairwise_bd_impl(logits, targets, p, true);
+}
+
+// --------------------------------------------------------------------------
+// non-pairwise sigmoid CE / dice  (src/bindings.cpp:157-158,160-161)
+// --------------------------------------------------------------------------
+ml_dense_shape dense_shape(const torch::Tensor& logits, const torch::Tensor& targets) {
+  ML_CHECK_INPUT(logits);
+  ML_CHECK_INPUT(targets);
+  TORCH_CHECK(logits.dim() == 5, "logits must be (L,B,C,H,W)");
+  TORCH_CHECK(targets.dim() == 3, "targets must be (B,H_t,W_t)");
+  TORCH_CHECK(targets.scalar_type() == torch::kLong, "targets must be int64");
+  TORCH_CHECK(targets.size(0) == logits.size(1), "Batch size mismatch between logits and targets");
+  TORCH_CHECK(targets.device() == logits.device(), "all tensors must be on the same device");
+  ml_dense_shape s;
+  s.L = logits.size(0);
+  s.B = logits.size(1);
+  s.C = logits.size(2);
+  s.H = logits.size(3);
+  s.W = logits.size(4);
+  s.Ht = targets.size(1);
+  s.Wt = targets.size(2);
+  return s;
+}
+
+torch::Tensor dense_ws(const ml_dense_shape& s, int dt, bool dice, bool backward,
+                       const torch::Tensor& like) {
+  const size_t wsb = ml_dense_loss_workspace_size(&s, dt, dice, backward);
+  TORCH_CHECK(wsb > 0, "unsupported shape (the target resolution must be the same integer "
+                       "multiple, at most 15, of the logit resolution in both dimensions)");
+  return workspace(wsb, like);
+}
+
+torch::Tensor grad_levels(const torch::Tensor& grad_out, const torch::Tensor& logits, int64_t L) {
+  auto g = grad_out.to(logits.options().dtype(torch::kFloat32)).contiguous();
+  TORCH_CHECK(g.numel() == L, "grad_out must have shape (L,)");
+  return g;
+}
+
+torch::Tensor forward_sigmoid_ce_loss(const torch::Tensor& logits, const torch::Tensor& targets,
+                                      double num_masks, double scale, double gamma, double alpha) {
+  const ml_dense_shape s = dense_shape(logits, targets);
+  auto loss = torch::empty({s.L}, logits.options().dtype(torch::kFloat32));
+  if (s.L == 0) return loss;
+  const int dt = dtype_code(logits, "logits");
+  auto ws = dense_ws(s, dt, false, false, logits);
+  ml_ok(ml_sigmoid_ce_forward(&s, dt, logits.data_ptr(), targets.data_ptr<int64_t>(),
+                              (float)num_masks, (float)scale, (float)gamma, (float)alpha,
+                              loss.data_ptr<float>(), ws.data_ptr(), ws.numel(), cur_stream()));
+  return loss;
+}
+
+torch::Tensor backward_sigmoid_ce_loss(const torch::Tensor& grad_out, const torch::Tensor& logits,
+                                       const torch::Tensor& targets, double num_masks,
+                                       double scale, double gamma, double alpha) {
+  const ml_dense_shape s = dense_shape(logits, targets);
+  auto grad = torch::empty_like(logits);
+  if (logits.numel() == 0) return grad;
+  auto g = grad_levels(grad_out, logits, s.L);
+  const int dt = dtype_code(logits, "logits");
+  auto ws = dense_ws(s, dt, false, true, logits);
+  ml_ok(ml_sigmoid_ce_backward(&s, dt, g.data_ptr<float>(), logits.data_ptr(),
+                               targets.data_ptr<int64_t>(), (float)num_masks, (float)scale,
+                               (float)gamma, (float)alpha, grad.data_ptr(), ws.data_ptr(),
+                               ws.numel(), cur_stream()));
+  return grad;
+}
+
+std::vector<torch::Tensor> forward_dice_loss(const torch::Tensor& logits,
+                                             const torch::Tensor& targets, double smooth,
+                                             double num_masks, double scale) {
+  const ml_dense_shape s = dense_shape(logits, targets);
+  auto f32 = logits.options().dtype(torch::kFloat32);
+  auto loss = torch::empty({s.L}, f32);
+  auto I = torch::empty({s.L, s.B, s.C}, f32);
+  auto P = torch::empty({s.L, s.B, s.C}, f32);
+  auto T = torch::empty({s.L, s.B, s.C}, f32);
+  if (s.L == 0) return {loss, I, P, T};
+  const int dt = dtype_code(logits, "logits");
+  auto ws = dense_ws(s, dt, true, false, logits);
+  ml_ok(ml_dice_loss_forward(&s, dt, logits.data_ptr(), targets.data_ptr<int64_t>(),
+                             (float)smooth, (float)num_masks, (float)scale,
+                             loss.data_ptr<float>(), I.data_ptr<float>(), P.data_ptr<float>(),
+                             T.data_ptr<float>(), ws.data_ptr(), ws.numel(), cur_stream()));
+  return {loss, I, P, T};
+}
+
+torch::Tensor backward_dice_loss(const torch::Tensor& grad_out, const torch::Tensor& logits,
+                                 const torch::Tensor& targets, const torch::Tensor& I,
+                                 const torch::Tensor& P, const torch::Tensor& T, double smooth,
+                                 double num_masks, double scale) {
+  const ml_dense_shape s = dense_shape(logits, targets);
+  auto grad = torch::empty_like(logits);
+  if (logits.numel() == 0) return grad;
+  auto g = grad_levels(grad_out, logits, s.L);
+  auto f32 = logits.options().dtype(torch::kFloat32);
+  auto Ic = I.to(f32).contiguous(), Pc = P.to(f32).contiguous(), Tc = T.to(f32).contiguous();
+  TORCH_CHECK(Ic.numel() == s.L * s.B * s.C && Pc.numel() == Ic.numel() && Tc.numel() == Ic.numel(),
+              "I, P, T must have shape (L,B,C)");
+  const int dt = dtype_code(logits, "logits");
+  auto ws = dense_ws(s, dt, true, true, logits);
+  ml_ok(ml_dice_loss_backward(&s, dt, g.data_ptr<float>(), logits.data_ptr(),
+                              targets.data_ptr<int64_t>(), Ic.data_ptr<float>(),
+                              Pc.data_ptr<float>(), Tc.data_ptr<float>(), (float)smooth,
+                              (float)num_masks, (float)scale, grad.data_ptr(), ws.data_ptr(),
+                              ws.numel(), cur_stream()));
+  return grad;
+}
+
 // Device flag (int32, shape (1,)): 1 if any element of `x` equals `value`.
 torch::Tensor any_equal(const torch::Tensor& x, int64_t value) {
   ML_CHECK_INPUT(x);
@@ -409,6 +573,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "Pairwise sigmoid label cost forward (HIP)");
   m.def("forward_pw_softmax_label_loss", &forward_pw_softmax_label_loss,
         "Pairwise softmax label cost forward (HIP)");
+  m.def("forward_sigmoid_ce_loss", &forward_sigmoid_ce_loss, "Sigmoid cross entropy forward (HIP)");
+  m.def("backward_sigmoid_ce_loss", &backward_sigmoid_ce_loss,
+        "Sigmoid cross entropy backward (HIP)");
+  m.def("forward_pw_sigmoid_ce_loss", &forward_pw_sigmoid_ce_loss,
+        "Pairwise sigmoid cross entropy forward (HIP)");
+  m.def("forward_dice_loss", &forward_dice_loss, "Dice loss forward (HIP)");
+  m.def("backward_dice_loss", &backward_dice_loss, "Dice loss backward (HIP)");
+  m.def("forward_pw_dice_loss", &forward_pw_dice_loss, "Pairwise dice loss forward (HIP)");
   m.def("any_equal", &any_equal, "Device flag: any element equal to value (HIP)");
   m.attr("__backend__") = "hip-gfx950";
 }

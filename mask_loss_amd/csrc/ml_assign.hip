@@ -117,13 +117,16 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
   if (!a.normalize) S = (float)(a.Ht * a.Wt);
   S = fmaxf(S, kEps);
 
-  // label row term and unmatched class penalty
+  // label row term and unmatched class penalty (none without class logits:
+  // the standalone pairwise BCE / dice operators)
+  const bool labels = a.cls_logits != nullptr;
   const int64_t zb = row * C;
   const int64_t void_idx = a.void_idx;
   const bool has_void = void_idx >= 0;
   const bool softmax_bg = a.use_softmax && a.force_cls && has_void;
-  float rowv, pen = 0.f;
-  if (a.use_softmax) {
+  float rowv = 0.f, pen = 0.f;
+  if (!labels) {
+  } else if (a.use_softmax) {
     float m = -INFINITY;
     for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_elem(a.cls_logits, a.cls_dtype, zb + c));
     m = wave_max(m);
@@ -164,6 +167,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
 
   // all output columns of this row
   const int64_t term = a.L * a.B * a.Q * GTo;
+  (void)term;
   for (int64_t c = lane; c < GTo; c += 64) {
     const int slot = a.slot_of_col[b * GTo + c];
     float bce = INFINITY, dice = INFINITY, cls;
@@ -173,8 +177,10 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
              a.dice_scale;
     }
     const int64_t act = c + (c >= a.bg ? 1 : 0);
-    const int64_t y = a.cls_targets[b * a.GT_total + act];
-    if (y < 0 || y >= C) {
+    const int64_t y = labels ? a.cls_targets[b * a.GT_total + act] : 0;
+    if (!labels) {
+      cls = 0.f;
+    } else if (y < 0 || y >= C) {
       cls = INFINITY;
     } else {
       const float zy = cls_elem(a.cls_logits, a.cls_dtype, zb + y);
@@ -186,9 +192,9 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
       }
     }
     const int64_t o = row * GTo + c;
-    a.sep[o] = bce;
-    a.sep[term + o] = dice;
-    a.sep[2 * term + o] = cls;
+    if (a.out_bce) a.out_bce[o] = bce;
+    if (a.out_dice) a.out_dice[o] = dice;
+    if (labels) a.sep[2 * term + o] = cls;
   }
   if (lane == 0 && a.rowstat) {
     float mp = 0.f, dp = 0.f;

@@ -251,8 +251,10 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                         const void* cls_logits, const int64_t* cls_targets, int64_t* pred_to_gt,
                         int64_t* pred_round, float* layer_means, float* sep, void* saved,
                         void* prefill, void* ws, size_t ws_bytes, hipStream_t st,
-                        bool costs_only) {
-  if (!dtype_ok(mask_dtype) || !dtype_ok(cls_dtype)) return fail(ML_EINVAL, "unsupported dtype");
+                        bool costs_only, float* bce_out = nullptr, float* dice_out = nullptr) {
+  if (!dtype_ok(mask_dtype) || (cls_logits && !dtype_ok(cls_dtype)))
+    return fail(ML_EINVAL, "unsupported dtype");
+  if (!cls_logits && !costs_only) return fail(ML_EINVAL, "matching needs class logits");
   Dims d;
   std::string err;
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
@@ -320,6 +322,13 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.ncols = pa.ncols;
   aa.slot_of_col = pa.slot_of_col;
   aa.sep = sep ? sep : (float*)(w + L.sep);
+  if (cls_logits) {
+    aa.out_bce = aa.sep;
+    aa.out_dice = aa.sep + d.LB * d.Q * d.GT_out;
+  } else {  // standalone pairwise BCE / dice: planes straight to the caller's outputs
+    aa.out_bce = bce_out;
+    aa.out_dice = dice_out;
+  }
   aa.rowstat = (float*)(w + L.rowstat);
   aa.costT = in_lds ? nullptr : (float*)(w + L.costT);
   aa.pred_to_gt = pred_to_gt;
@@ -505,6 +514,21 @@ int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mas
                       workspace, workspace_bytes, (hipStream_t)stream, true);
 }
 
+int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int dtype,
+                                     const void* logits, const int64_t* targets, float* bce_out,
+                                     float* dice_out, void* workspace, size_t workspace_bytes,
+                                     ml_stream_t stream) {
+  int rc = check_focal(p->mask_gamma, p->mask_alpha, "pairwise sigmoid");
+  if (rc) return rc;
+  if (!(p->uncertainty_gamma >= 0.f))
+    return fail(ML_EINVAL, "uncertainty_gamma must be non-negative");
+  if (!(p->uncertainty_gamma_min >= 0.f && p->uncertainty_gamma_min <= 1.f))
+    return fail(ML_EINVAL, "uncertainty_gamma_min must be in [0, 1]");
+  return forward_impl(s, p, dtype, logits, targets, ML_F32, nullptr, nullptr, nullptr, nullptr,
+                      nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes,
+                      (hipStream_t)stream, true, bce_out, dice_out);
+}
+
 size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,
                                                 int mask_dtype) {
   Dims d;
@@ -610,6 +634,158 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
                              : make_elem_params(p->cls_gamma, p->cls_alpha, 0.f, 0.f);
   ba.cls_gamma = ba.use_softmax ? 0.f : p->cls_gamma;
   return launch_bwd(ba, d, st);
+}
+
+// ---- dense (non-pairwise) sigmoid CE / dice -------------------------------------
+namespace {
+struct DensePlan {
+  Dims d;             // B, H, W, Ht, Wt, s, HW, HWp, counts_mode; GT_total := C
+  size_t tgt_bytes, partial_off, total;
+};
+
+bool dense_plan(const ml_dense_shape* s, bool dice, bool backward, DensePlan& P,
+                std::string& err) {
+  if (!s || s->L < 0 || s->B < 0 || s->C < 0 || s->H <= 0 || s->W <= 0) {
+    err = "dense loss: invalid shape";
+    return false;
+  }
+  Dims& d = P.d;
+  d = Dims{};
+  d.L = s->L; d.B = s->B; d.Q = 0; d.H = s->H; d.W = s->W; d.Ht = s->Ht; d.Wt = s->Wt;
+  d.C = s->C; d.GT_total = s->C;
+  if (d.Ht % d.H != 0 || d.Wt % d.W != 0 || d.Ht / d.H != d.Wt / d.W || d.Ht == 0) {
+    err = "High-res dims must be the same integer multiple of the low-res dims";
+    return false;
+  }
+  d.s = d.Ht / d.H;
+  if (d.s > 15) {
+    err = "target/logit scale factor above 15 overflows the per-cell uint8 counts";
+    return false;
+  }
+  if (d.C > 65535) {
+    err = "at most 65535 classes are supported";
+    return false;
+  }
+  d.N2 = d.s * d.s;
+  d.LB = d.L * d.B;
+  d.HW = d.H * d.W;
+  d.HWp = ceil_div(d.HW, kStep) * kStep;
+  d.counts_mode = d.s > 1;
+  P.tgt_bytes = align256(d.counts_mode ? (size_t)d.B * d.C * d.HWp : (size_t)d.B * d.HWp * 2);
+  P.partial_off = P.tgt_bytes;
+  P.total = P.tgt_bytes + (backward ? 0 : align256(dense_partials_bytes(d.L, d.B, d.C, d.HW, dice)));
+  return true;
+}
+
+int dense_prep(const DensePlan& P, const int64_t* targets, unsigned char* w, DenseArgs& a,
+               hipStream_t st) {
+  const Dims& d = P.d;
+  PrepArgs pa{};
+  pa.targets = targets;
+  pa.lab16 = d.counts_mode ? nullptr : (uint16_t*)w;
+  pa.counts8 = d.counts_mode ? (uint8_t*)w : nullptr;
+  pa.present = nullptr;
+  pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
+  pa.GT_total = d.C; pa.GT_out = d.C; pa.bg = d.C;
+  a.lab16 = pa.lab16;
+  a.counts8 = pa.counts8;
+  a.L = d.L; a.B = d.B; a.C = d.C; a.HW = d.HW; a.HWp = d.HWp; a.HtWt = d.Ht * d.Wt;
+  a.N2 = (float)d.N2;
+  if (d.B == 0) return ML_OK;
+  return launch_prep(pa, d, st);
+}
+}  // namespace
+
+size_t ml_dense_loss_workspace_size(const ml_dense_shape* s, int dtype, int dice, int backward) {
+  DensePlan P;
+  std::string err;
+  if (!dtype_ok(dtype) || !dense_plan(s, dice != 0, backward != 0, P, err)) return 0;
+  return P.total;
+}
+
+static int dense_call(const ml_dense_shape* s, int dtype, bool dice, bool backward,
+                      const int64_t* targets, void* ws, size_t ws_bytes, DenseArgs& a,
+                      hipStream_t st) {
+  if (!dtype_ok(dtype)) return fail(ML_EINVAL, "unsupported dtype");
+  DensePlan P;
+  std::string err;
+  if (!dense_plan(s, dice, backward, P, err)) return fail(ML_EINVAL, err);
+  if (ws_bytes < P.total) return fail(ML_EWORKSPACE, "workspace too small");
+  unsigned char* w = (unsigned char*)ws;
+  a.dtype = dtype;
+  a.partials = backward ? nullptr : (double*)(w + P.partial_off);
+  int rc = dense_prep(P, targets, w, a, st);
+  if (rc) return rc;
+  return launch_dense(a, dice, backward, st);
+}
+
+int ml_sigmoid_ce_forward(const ml_dense_shape* s, int dtype, const void* logits,
+                          const int64_t* targets, float num_masks, float scale, float gamma,
+                          float alpha, float* loss, void* workspace, size_t workspace_bytes,
+                          ml_stream_t stream) {
+  int rc = check_focal(gamma, alpha, "sigmoid_ce");
+  if (rc) return rc;
+  DenseArgs a{};
+  a.logits = logits;
+  a.ep = make_elem_params(gamma, alpha, 0.f, 0.f);
+  a.scale = scale;
+  a.num_masks = (double)num_masks;
+  a.loss = loss;
+  return dense_call(s, dtype, false, false, targets, workspace, workspace_bytes, a,
+                    (hipStream_t)stream);
+}
+
+int ml_sigmoid_ce_backward(const ml_dense_shape* s, int dtype, const float* grad_out,
+                           const void* logits, const int64_t* targets, float num_masks,
+                           float scale, float gamma, float alpha, void* grad, void* workspace,
+                           size_t workspace_bytes, ml_stream_t stream) {
+  int rc = check_focal(gamma, alpha, "sigmoid_ce");
+  if (rc) return rc;
+  DenseArgs a{};
+  a.logits = logits;
+  a.ep = make_elem_params(gamma, alpha, 0.f, 0.f);
+  a.scale = scale;
+  a.num_masks = (double)num_masks;
+  a.grad_out = grad_out;
+  a.grad = grad;
+  return dense_call(s, dtype, false, true, targets, workspace, workspace_bytes, a,
+                    (hipStream_t)stream);
+}
+
+int ml_dice_loss_forward(const ml_dense_shape* s, int dtype, const void* logits,
+                         const int64_t* targets, float smooth, float num_masks, float scale,
+                         float* loss, float* I, float* P, float* T, void* workspace,
+                         size_t workspace_bytes, ml_stream_t stream) {
+  DenseArgs a{};
+  a.logits = logits;
+  a.smooth = smooth;
+  a.scale = scale;
+  a.num_masks = (double)num_masks;
+  a.loss = loss;
+  a.I_out = I;
+  a.P_out = P;
+  a.T_out = T;
+  return dense_call(s, dtype, true, false, targets, workspace, workspace_bytes, a,
+                    (hipStream_t)stream);
+}
+
+int ml_dice_loss_backward(const ml_dense_shape* s, int dtype, const float* grad_out,
+                          const void* logits, const int64_t* targets, const float* I,
+                          const float* P, const float* T, float smooth, float num_masks,
+                          float scale, void* grad, void* workspace, size_t workspace_bytes,
+                          ml_stream_t stream) {
+  DenseArgs a{};
+  a.logits = logits;
+  a.smooth = smooth;
+  a.scale = scale;
+  a.num_masks = (double)num_masks;
+  a.grad_out = grad_out;
+  a.I_in = I;
+  a.P_in = P;
+  a.T_in = T;
+  a.grad = grad;
+  return dense_call(s, dtype, true, true, targets, workspace, workspace_bytes, a,
+                    (hipStream_t)stream);
 }
 
 int ml_pairwise_label_loss_forward(int64_t L, int64_t B, int64_t Q, int64_t C, int64_t GT_total,

@@ -180,7 +180,9 @@ struct AssignArgs {
   const int* ncols;
   const int* slot_of_col;
   // outputs
-  float* sep;            // (3, L, B, Q, GT_out) or null
+  float* sep;            // (3, L, B, Q, GT_out): bce, dice, label cost
+  float* out_bce;        // where finalize writes the bce / dice planes (sep's
+  float* out_dice;       // first two planes, or a standalone operator's outputs, or null)
   float* costT;          // [LB][GT_out][Q] transposed total cost (global fallback)
   int64_t* pred_to_gt;   // (L,B,Q) or null (costs-only mode)
   int64_t* pred_round;
@@ -243,6 +245,25 @@ struct BwdArgs {
   float cls_gamma;
 };
 
+// Non-pairwise sigmoid-CE / dice over dense class logits (L, B, C, H, W).
+struct DenseArgs {
+  const void* logits;
+  int dtype;
+  const uint16_t* lab16;   // s == 1: label per cell (0xFFFF outside [0, C))
+  const uint8_t* counts8;  // s > 1: [B][C][HWp] per-cell counts
+  int64_t L, B, C, HW, HWp, HtWt;
+  float N2;
+  ElemParams ep;           // focal terms (sigmoid CE)
+  float scale, smooth;
+  double num_masks;
+  double* partials;        // forward: per (plane, chunk) float64 sums
+  float* loss;             // (L,)
+  float *I_out, *P_out, *T_out;                // dice forward: (L, B, C)
+  const float* grad_out;                       // backward: (L,)
+  const float *I_in, *P_in, *T_in;             // dice backward
+  void* grad;                                  // (L, B, C, H, W) in dtype
+};
+
 // ---- instrumentation: bracket a launch with events when profiling is on ------
 void prof_begin(const char* name, hipStream_t st);
 void prof_end(const char* name, hipStream_t st);
@@ -268,6 +289,8 @@ int launch_label_cost(const void* cls_logits, int cls_dtype, const int64_t* cls_
                       int64_t GT_out, int64_t bg, float scale, const ElemParams& ep,
                       int use_softmax, float* out, hipStream_t st);
 int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st);
+int launch_dense(const DenseArgs& a, bool dice, bool backward, hipStream_t st);
+size_t dense_partials_bytes(int64_t L, int64_t B, int64_t C, int64_t HW, bool dice);
 int launch_zero_fill(void* p, size_t bytes, hipStream_t st);
 int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, hipStream_t st);
 

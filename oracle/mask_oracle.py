@@ -217,6 +217,106 @@ def pairwise_mask_loss_forward(mask_logits, mask_targets, cls_logits, cls_target
 
 
 # ---------------------------------------------------------------------------
+# standalone pairwise costs (GT slots from the label map itself)
+# ---------------------------------------------------------------------------
+def gt_total_from_targets(targets) -> int:
+    """GT_total = targets.max() + 1, reference src/cuda/pw_sigmoid_ce.cu:222-224
+    and src/cuda/pw_dice_loss.cu:132-134 (not the cls_targets width)."""
+    t = np.asarray(targets)
+    return max(int(t.max()) + 1, 0) if t.size else 0
+
+
+def pairwise_sigmoid_ce(logits, targets, background_index=-1, scale=1.0, gamma=0.0,
+                        alpha=-1.0, ug=1.0, ug_min=0.05, normalize=True):
+    """(L, B, C, GT_out), reference src/cuda/pw_sigmoid_ce.cu:12-197 (kernel: the
+    BCE half of pw_mask.cu's) and :199-316 (host)."""
+    bce, _ = pairwise_mask_costs(logits, targets, gt_total_from_targets(targets),
+                                 background_index, 1.0, scale, 1.0, ug, ug_min, gamma, alpha,
+                                 normalize)
+    return bce
+
+
+def pairwise_dice(logits, targets, smooth=1.0, background_index=-1, scale=1.0, ug=1.0,
+                  ug_min=0.05):
+    """(L, B, C, GT_out), reference src/cuda/pw_dice_loss.cu:12-108 (kernel:
+    I = sum w p n, P = sum N2 w p, T = sum w n) and :111-221 (host)."""
+    _, dice = pairwise_mask_costs(logits, targets, gt_total_from_targets(targets),
+                                  background_index, smooth, 1.0, scale, ug, ug_min)
+    return dice
+
+
+# ---------------------------------------------------------------------------
+# non-pairwise (per-class) losses over dense class logits
+# ---------------------------------------------------------------------------
+def sigmoid_ce_loss(logits, targets, num_masks, scale=1.0, gamma=0.0, alpha=-1.0):
+    """(L,), reference src/cuda/sigmoid_ce.cu:13-114 (kernel) and :207-268 (host):
+    sum over (b, c, cell) of ap mp cp n + an mn cn (N2 - n), n = count of class c
+    in the cell's s x s block, times scale / (num_masks Ht Wt)."""
+    z = np.asarray(logits, dtype=np.float64)
+    L, B, C, H, W = z.shape
+    _, Ht, Wt = targets.shape
+    N2 = float((Ht // H) ** 2)
+    n = label_counts(targets, H, W, C).astype(np.float64)   # (B, C, HW)
+    e = elementwise(z.reshape(L, B, C, H * W), gamma, 0.0, 0.0)
+    ap, an = _alphas(alpha)
+    loss = ap * e.mp * e.cp * n + an * e.mn * e.cn * (N2 - n)
+    return loss.sum(axis=(1, 2, 3)) * scale / (num_masks * Ht * Wt)
+
+
+def sigmoid_ce_backward(grad_out, logits, targets, num_masks, scale=1.0, gamma=0.0,
+                        alpha=-1.0):
+    """(L, B, C, H, W), reference src/cuda/sigmoid_ce.cu:116-205 and :270-332:
+    -ap n mp (gamma p cp + 1-p) + an (N2-n) mn (gamma (1-p) cn + p), times
+    grad_out[l] scale / (num_masks Ht Wt)."""
+    z = np.asarray(logits, dtype=np.float64)
+    L, B, C, H, W = z.shape
+    _, Ht, Wt = targets.shape
+    N2 = float((Ht // H) ** 2)
+    n = label_counts(targets, H, W, C).astype(np.float64).reshape(1, B, C, H, W)
+    e = elementwise(z, gamma, 0.0, 0.0)
+    ap, an = _alphas(alpha)
+    g = (-ap * n * e.mp * (gamma * e.p * e.cp + (1.0 - e.p))
+         + an * (N2 - n) * e.mn * (gamma * (1.0 - e.p) * e.cn + e.p))
+    coef = np.asarray(grad_out, dtype=np.float64).reshape(L, 1, 1, 1, 1) * scale / (num_masks * Ht * Wt)
+    return g * coef
+
+
+def dice_loss(logits, targets, smooth, num_masks, scale=1.0):
+    """(loss (L,), I, P, T (L, B, C)), reference src/cuda/dice_loss.cu:13-82 and
+    :159-222: I = sum p n, P = sum N2 p, T = sum n; loss = scale / num_masks *
+    sum_{b,c} 1 - (2I + smooth) / (P + T + smooth)."""
+    z = np.asarray(logits, dtype=np.float64)
+    L, B, C, H, W = z.shape
+    _, Ht, Wt = targets.shape
+    N2 = float((Ht // H) ** 2)
+    n = label_counts(targets, H, W, C).astype(np.float64)   # (B, C, HW)
+    p = 1.0 / (1.0 + np.exp(-z.reshape(L, B, C, H * W)))
+    I = (p * n).sum(-1)
+    P = N2 * p.sum(-1)
+    T = np.broadcast_to(n.sum(-1), I.shape).copy()
+    dice = (2.0 * I + smooth) / (P + T + smooth)
+    loss = (1.0 - dice).reshape(L, -1).sum(1) / num_masks * scale
+    return loss, I, P, T
+
+
+def dice_loss_backward(grad_out, logits, targets, I, P, T, smooth, num_masks, scale=1.0):
+    """(L, B, C, H, W), reference src/cuda/dice_loss.cu:84-157 and :224-289:
+    -grad_out[l] scale / num_masks * (2 n D - N2 (2I + smooth)) / D^2 * p (1-p),
+    D = P + T + smooth, with the forward's I, P, T."""
+    z = np.asarray(logits, dtype=np.float64)
+    L, B, C, H, W = z.shape
+    _, Ht, Wt = targets.shape
+    N2 = float((Ht // H) ** 2)
+    n = label_counts(targets, H, W, C).astype(np.float64).reshape(1, B, C, H, W)
+    p = 1.0 / (1.0 + np.exp(-z))
+    I = np.asarray(I, dtype=np.float64)[..., None, None]
+    D = (np.asarray(P, dtype=np.float64) + np.asarray(T, dtype=np.float64) + smooth)[..., None, None]
+    g = (2.0 * n * D - N2 * (2.0 * I + smooth)) / (D * D) * p * (1.0 - p)
+    coef = -np.asarray(grad_out, dtype=np.float64).reshape(L, 1, 1, 1, 1) / num_masks * scale
+    return g * coef
+
+
+# ---------------------------------------------------------------------------
 # matched-loss forward
 # ---------------------------------------------------------------------------
 def denominators(pred_to_gt, B, Q, num_masks, force_masks, force_cls, has_void):

@@ -71,7 +71,10 @@ def test_extension_surface_and_host_tensors_rejected():
     import torch
     import mask_loss_amd
     ml = mask_loss_amd.mask_loss
-    for n in ["mask_matching", "mask_matching_backward", "pairwise_mask_loss_forward",
+    # the reference module's 11 operators (src/bindings.cpp:157-169)
+    for n in ["forward_sigmoid_ce_loss", "backward_sigmoid_ce_loss", "forward_pw_sigmoid_ce_loss",
+              "forward_dice_loss", "backward_dice_loss", "forward_pw_dice_loss",
+              "pairwise_mask_loss_forward", "mask_matching", "mask_matching_backward",
               "forward_pw_sigmoid_label_loss", "forward_pw_softmax_label_loss"]:
         assert hasattr(ml, n)
     z = torch.zeros(1, 1, 2, 4, 4)
@@ -84,6 +87,32 @@ def test_extension_surface_and_host_tensors_rejected():
     with pytest.raises(RuntimeError, match="CUDA tensor"):
         ml.pairwise_mask_loss_forward(z, t, zc, ct, 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, 0.0, -1.0,
                                       0.0, -1.0, False, True)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.forward_sigmoid_ce_loss(z, t, 1.0, 1.0, 0.0, -1.0)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.forward_dice_loss(z, t, 1.0, 1.0, 1.0)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.forward_pw_dice_loss(z, t, 1.0, -1, 1.0, 1.0, 0.05)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.forward_pw_sigmoid_ce_loss(z, t, -1, 1.0, 0.0, -1.0, 1.0, 0.05, True)
+
+
+def test_dense_workspace_query():
+    import torch  # noqa: F401
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(LIB)
+
+    class DShape(ctypes.Structure):
+        _fields_ = [(k, ctypes.c_int64) for k in ["L", "B", "C", "H", "W", "Ht", "Wt"]]
+
+    lib.ml_dense_loss_workspace_size.restype = ctypes.c_size_t
+    good = DShape(1, 2, 133, 64, 64, 256, 256)
+    for dice in (0, 1):
+        for bwd in (0, 1):
+            assert lib.ml_dense_loss_workspace_size(ctypes.byref(good), 1, dice, bwd) > 0
+    assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 64, 64, 256, 250)), 1, 0, 0) == 0
+    assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 4, 4, 64, 64)), 1, 0, 0) == 0  # s = 16
 
 
 def test_function_validation_errors():

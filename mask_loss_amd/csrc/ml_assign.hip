@@ -90,6 +90,35 @@ __device__ __forceinline__ bool cost_ok(double c, double thr) { return isfinite(
 // classes, and the row terms used later: normaliser S, mass P, and the
 // unmatched-query penalties (src/cuda/mask_matching_forward.cu:125-277).
 // ---------------------------------------------------------------------------
+// Sum the K-split partials k0, k0 + step, ... of slot s: four independent
+// accumulators, so twelve loads are in flight per round trip.
+__device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0, int step,
+                                           float& v0, float& v1, float& v2) {
+  float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f}, a2[4] = {0.f, 0.f, 0.f, 0.f};
+  int ks = k0;
+  for (; ks + 3 * step < rp.KS; ks += 4 * step) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* P = rp.p0 + (int64_t)(ks + u * step) * rp.ks_stride + s;
+      a0[u] += P[0];
+      a1[u] += P[rp.plane];
+      a2[u] += P[2 * rp.plane];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {  // at most three splits remain
+    if (ks + u * step < rp.KS) {
+      const float* P = rp.p0 + (int64_t)(ks + u * step) * rp.ks_stride + s;
+      a0[u] += P[0];
+      a1[u] += P[rp.plane];
+      a2[u] += P[2 * rp.plane];
+    }
+  }
+  v0 = (a0[0] + a0[1]) + (a0[2] + a0[3]);
+  v1 = (a1[0] + a1[1]) + (a1[2] + a1[3]);
+  v2 = (a2[0] + a2[1]) + (a2[2] + a2[3]);
+}
+
 __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
   __shared__ float sl[4][3][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -99,17 +128,28 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
   const int64_t GTo = a.GT_out, C = a.C;
   const int G = a.ncols[b];
   const RowPartials rp = row_partials(a.partials, a.sched, a.plan, lb, q, a.rows, a.rtiles, G);
-  for (int s = lane; s <= G; s += 64) {
+  const int nsl = G + 1;  // GT columns + the ones column
+  if (nsl <= 32) {
+    // two lanes per slot, each summing every other K-split; fixed-order combine
+    const int s = lane & 31, half = lane >> 5;
     float v0 = 0.f, v1 = 0.f, v2 = 0.f;
-    for (int ks = 0; ks < rp.KS; ++ks) {
-      const float* P = rp.p0 + ks * rp.ks_stride;
-      v0 += P[s];
-      v1 += P[rp.plane + s];
-      v2 += P[2 * rp.plane + s];
+    if (s < nsl) sum_splits(rp, s, half, 2, v0, v1, v2);
+    v0 += __shfl_xor(v0, 32, 64);
+    v1 += __shfl_xor(v1, 32, 64);
+    v2 += __shfl_xor(v2, 32, 64);
+    if (half == 0 && s < nsl) {
+      sl[wave][0][s] = v0;
+      sl[wave][1][s] = v1;
+      sl[wave][2][s] = v2;
     }
-    sl[wave][0][s] = v0;
-    sl[wave][1][s] = v1;
-    sl[wave][2][s] = v2;
+  } else {
+    for (int s = lane; s < nsl; s += 64) {
+      float v0 = 0.f, v1 = 0.f, v2 = 0.f;
+      sum_splits(rp, s, 0, 1, v0, v1, v2);
+      sl[wave][0][s] = v0;
+      sl[wave][1][s] = v1;
+      sl[wave][2][s] = v2;
+    }
   }
   wave_sync();
   float S = sl[wave][2][G];
@@ -389,6 +429,66 @@ __device__ void greedy_wave(const float* cost, int64_t ldq, const int* preds, in
   }
 }
 
+// Per-layer means and denominators (src/cuda/mask_matching_forward.cu:549-583),
+// then, with a saved state, the list of matched query rows in ascending order
+// (wave ballots, one blockDim-row chunk at a time) for the backward.  One
+// workgroup.
+__device__ void layer_pass(const LayerArgs& a) {
+  for (int64_t l = threadIdx.x; l < a.L; l += blockDim.x) {
+    float m = 0.f, d = 0.f, c = 0.f, cnt = 0.f;
+    for (int64_t b = 0; b < a.B; ++b) {
+      const float* s = a.img + (l * a.B + b) * 4;
+      m += s[0];
+      d += s[1];
+      c += s[2];
+      cnt += s[3];
+    }
+    const float total = (float)(a.B * a.Q);
+    const bool has_nm = a.num_masks > 0.0;
+    float md = a.force_masks ? total : (has_nm ? (float)a.num_masks : cnt);
+    float cd = (a.force_cls || a.has_void) ? total : (has_nm ? (float)a.num_masks : cnt);
+    md = fmaxf(md, 1.f);
+    cd = fmaxf(cd, 1.f);
+    a.means[0 * a.L + l] = m / md;
+    a.means[1 * a.L + l] = d / md;
+    a.means[2 * a.L + l] = c / cd;
+    a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN] = 1.f / md;
+    a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / cd;
+  }
+  if (a.list == nullptr) return;
+  __shared__ int wcnt[16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int64_t n = a.L * a.B * a.Q;
+  int base = 0;
+  constexpr int U = 4;  // rows per thread whose loads are in flight together
+  for (int64_t r0 = 0; r0 < n; r0 += U * (int64_t)blockDim.x) {
+    bool m[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + u * (int64_t)blockDim.x + threadIdx.x;
+      m[u] = r < n && a.pred_to_gt[r] >= 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + u * (int64_t)blockDim.x + threadIdx.x;
+      const uint64_t bal = __ballot(m[u]);
+      if (lane == 0) wcnt[wave] = __popcll(bal);
+      __syncthreads();
+      int off = base, tot = base;
+      for (int w = 0; w < nw; ++w) {
+        off += w < wave ? wcnt[w] : 0;
+        tot += wcnt[w];
+      }
+      if (m[u]) a.list[1 + off + __popcll(bal & below)] = (int)r;
+      __syncthreads();
+      base = tot;
+    }
+  }
+  if (threadIdx.x == 0) a.list[0] = base;
+}
+
 template <int NJ>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -662,57 +762,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
 }
 
 
-// Per-layer means and denominators (src/cuda/mask_matching_forward.cu:549-583).
-// With a saved state, workgroup 0 also lists the matched query rows in
-// ascending order (wave ballots, one 1024-row chunk at a time) for the
-// backward.
-__global__ __launch_bounds__(1024) void layer_kernel(LayerArgs a) {
-  for (int64_t l = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; l < a.L;
-       l += (int64_t)gridDim.x * blockDim.x) {
-    float m = 0.f, d = 0.f, c = 0.f, cnt = 0.f;
-    for (int64_t b = 0; b < a.B; ++b) {
-      const float* s = a.img + (l * a.B + b) * 4;
-      m += s[0];
-      d += s[1];
-      c += s[2];
-      cnt += s[3];
-    }
-    const float total = (float)(a.B * a.Q);
-    const bool has_nm = a.num_masks > 0.0;
-    float md = a.force_masks ? total : (has_nm ? (float)a.num_masks : cnt);
-    float cd = (a.force_cls || a.has_void) ? total : (has_nm ? (float)a.num_masks : cnt);
-    md = fmaxf(md, 1.f);
-    cd = fmaxf(cd, 1.f);
-    a.means[0 * a.L + l] = m / md;
-    a.means[1 * a.L + l] = d / md;
-    a.means[2 * a.L + l] = c / cd;
-    a.layer[l * ML_LAYERS + ML_LAYER_INV_MASK_DEN] = 1.f / md;
-    a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / cd;
-  }
-  if (a.list == nullptr || blockIdx.x != 0) return;
-  __shared__ int wcnt[16];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nw = blockDim.x >> 6;
-  const uint64_t below = (1ull << lane) - 1ull;
-  const int64_t n = a.L * a.B * a.Q;
-  int base = 0;
-  for (int64_t r0 = 0; r0 < n; r0 += blockDim.x) {
-    const int64_t r = r0 + threadIdx.x;
-    const bool m = r < n && a.pred_to_gt[r] >= 0;
-    const uint64_t bal = __ballot(m);
-    if (lane == 0) wcnt[wave] = __popcll(bal);
-    __syncthreads();
-    int off = base, tot = base;
-    for (int w = 0; w < nw; ++w) {
-      off += w < wave ? wcnt[w] : 0;
-      tot += wcnt[w];
-    }
-    if (m) a.list[1 + off + __popcll(bal & below)] = (int)r;
-    __syncthreads();
-    base = tot;
-  }
-  if (threadIdx.x == 0) a.list[0] = base;
-}
+__global__ __launch_bounds__(1024) void layer_kernel(LayerArgs a) { layer_pass(a); }
 
 // Denominators from pred_to_gt alone (backward without saved statistics,
 // src/cuda/mask_matching_backward.cu:480-508).  One wave per layer.
@@ -741,14 +791,18 @@ size_t assign_smem_bytes(int64_t Q, int64_t GTo, bool cost_in_lds) {
 template <int NJ>
 static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const size_t sm = smem_layout(a.Q, a.GT_out, a.cost_in_lds != 0).total;
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute((const void*)assign_kernel<NJ>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             160 * 1024);
-    if (e != hipSuccess) return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
-    attr_set = true;
+  static size_t max_dyn = 0;  // 160 KB of LDS less the kernel's static part
+  if (max_dyn == 0) {
+    hipFuncAttributes fa;
+    if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ>) != hipSuccess)
+      return fail(ML_ELAUNCH, "assign: cannot query the kernel attributes");
+    const size_t dyn = 160 * 1024 - fa.sharedSizeBytes;
+    if (hipFuncSetAttribute((const void*)assign_kernel<NJ>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
+      return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
+    max_dyn = dyn;
   }
+  if (sm > max_dyn) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
   {
     ProfScope ps_("assign", st);
     hipLaunchKernelGGL(assign_kernel<NJ>, dim3((unsigned)d.LB), dim3(256), sm, st, a);
@@ -777,10 +831,7 @@ int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
 int launch_layer(const LayerArgs& a, hipStream_t st) {
   {
     ProfScope ps_("layer", st);
-    if (a.list)
-      hipLaunchKernelGGL(layer_kernel, dim3(1), dim3(1024), 0, st, a);
-    else
-      hipLaunchKernelGGL(layer_kernel, dim3((unsigned)ceil_div(a.L, 64)), dim3(64), 0, st, a);
+    hipLaunchKernelGGL(layer_kernel, dim3(1), dim3(1024), 0, st, a);
   }
   return check_launch("layer");
 }

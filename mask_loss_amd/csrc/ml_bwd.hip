@@ -295,6 +295,100 @@ __global__ __launch_bounds__(256) void bwd_mask_list_kernel(BwdArgs a, int64_t n
   }
 }
 
+__device__ __forceinline__ float cls_in(const void* p, int dt, int64_t i) {
+  if (dt == ML_F32) return ((const float*)p)[i];
+  const uint16_t h = ((const uint16_t*)p)[i];
+  if (dt == ML_BF16) return __uint_as_float(((uint32_t)h) << 16);
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ void cls_out(void* p, int dt, int64_t i, float v) {
+  if (dt == ML_F32) {
+    ((float*)p)[i] = v;
+  } else if (dt == ML_BF16) {
+    ((uint16_t*)p)[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFF);
+  } else {
+    ((uint16_t*)p)[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+}
+
+// Class-logit gradient of one (l,b,q) row, on one wave.
+__device__ void cls_row(const BwdArgs& a, int64_t row) {
+  const int lane = threadIdx.x & 63;
+  const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
+  const int64_t C = a.C;
+  const int64_t base = row * C;
+  const int64_t out = a.pred_to_gt[row];
+  const int64_t act = out + (out >= a.bg ? 1 : 0);
+  const bool matched = out >= 0 && act < a.GT_total;
+  const bool has_void = a.void_idx >= 0;
+  const bool need_cls = a.force_cls || has_void;
+  const float coeff = a.g_cls[l] * (a.cls_scale * a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN]);
+  int64_t y = -1;
+  bool zero = (!matched && !need_cls) || coeff == 0.f;
+  if (!zero && matched) {
+    y = a.cls_targets[b * a.GT_total + act];
+    if (y < 0 || y >= C) zero = true;
+  }
+  if (zero) {
+    for (int64_t c = lane; c < C; c += 64) cls_out(a.grad_cls, a.cls_dtype, base + c, 0.f);
+    return;
+  }
+  if (a.use_softmax) {
+    if (matched || (a.force_cls && has_void)) {
+      const int64_t tgt = matched ? y : a.void_idx;
+      float m = -INFINITY;
+      for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_in(a.cls_logits, a.cls_dtype, base + c));
+      m = wave_max(m);
+      float se = 0.f;
+      for (int64_t c = lane; c < C; c += 64) se += __expf(cls_in(a.cls_logits, a.cls_dtype, base + c) - m);
+      se = wave_sum(se);
+      const float inv = se > 0.f ? 1.f / se : 0.f;
+      for (int64_t c = lane; c < C; c += 64) {
+        float gv = __expf(cls_in(a.cls_logits, a.cls_dtype, base + c) - m) * inv;
+        if (c == tgt) gv -= 1.f;
+        cls_out(a.grad_cls, a.cls_dtype, base + c, coeff * gv);
+      }
+    } else {  // has_void only
+      for (int64_t c = lane; c < C; c += 64) {
+        float gv = 0.f;
+        if (c == a.void_idx) {
+          const float z = cls_in(a.cls_logits, a.cls_dtype, base + c);
+          gv = coeff * (sig_terms(z).p - 1.f);
+        }
+        cls_out(a.grad_cls, a.cls_dtype, base + c, gv);
+      }
+    }
+    return;
+  }
+  const ElemParams ep = a.cls_ep;
+  const float g = a.cls_gamma;
+  const float invC = C > 0 ? 1.f / (float)C : 0.f;
+  for (int64_t c = lane; c < C; c += 64) {
+    const float z = cls_in(a.cls_logits, a.cls_dtype, base + c);
+    const Sig s = sig_terms(z);
+    float mn, mp;
+    focal_mods(s, ep, mn, mp);
+    const float posg = -ep.ap * mp * (g * s.p * s.cp + s.q1);
+    const float negg = ep.an * mn * (g * s.q1 * s.cn + s.p);
+    const bool is_void = has_void && c == a.void_idx;
+    float gv;
+    if (matched) {
+      gv = coeff * invC * (c == y ? posg : negg);
+    } else if (a.force_cls) {
+      gv = coeff * invC * (is_void ? posg : negg);
+    } else {
+      gv = is_void ? coeff * posg : 0.f;
+    }
+    cls_out(a.grad_cls, a.cls_dtype, base + c, gv);
+  }
+}
+
+// one wave per (l,b,q) row; 4 rows per workgroup
+__global__ __launch_bounds__(256) void bwd_cls_kernel(BwdArgs a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row < a.L * a.B * a.Q) cls_row(a, row);
+}
+
 // ---- bf16 logits: the per-logit gradient terms from an LDS table ------------
 // The mask-logit gradient of a cell with target count tk is
 //   mc sf (Fpos tk + Fneg (N2 - tk)) + dc kd Fd (num N2 - 2 D tk)
@@ -492,105 +586,22 @@ __global__ __launch_bounds__(kLutThreads) void bwd_mask_lut_kernel(BwdArgs a, in
   const int64_t total = nrows * nchunk;
   const bool vec = a.HW % 8 == 0;
   int64_t it = blockIdx.x;
-  if (it >= total) return;
-  LutItem cur, nxt;
-  lut_load<CNT>(a, it, nchunk, vec, cur);
-  for (; it < total; it += gridDim.x) {
-    const int64_t it2 = it + gridDim.x;
-    if (it2 < total) lut_load<CNT>(a, it2, nchunk, vec, nxt);
-    lut_compute_store<CNT>(a, cur, lut, vec);
-    cur = nxt;
-  }
-}
-
-__device__ __forceinline__ float cls_in(const void* p, int dt, int64_t i) {
-  if (dt == ML_F32) return ((const float*)p)[i];
-  const uint16_t h = ((const uint16_t*)p)[i];
-  if (dt == ML_BF16) return __uint_as_float(((uint32_t)h) << 16);
-  return (float)__builtin_bit_cast(_Float16, h);
-}
-__device__ __forceinline__ void cls_out(void* p, int dt, int64_t i, float v) {
-  if (dt == ML_F32) {
-    ((float*)p)[i] = v;
-  } else if (dt == ML_BF16) {
-    ((uint16_t*)p)[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFF);
-  } else {
-    ((uint16_t*)p)[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
-  }
-}
-
-// one wave per (l,b,q) row; 4 rows per workgroup
-__global__ __launch_bounds__(256) void bwd_cls_kernel(BwdArgs a) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int64_t nrows = a.L * a.B * a.Q;
-  if (row >= nrows) return;
-  const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
-  const int64_t C = a.C;
-  const int64_t base = row * C;
-  const int64_t out = a.pred_to_gt[row];
-  const int64_t act = out + (out >= a.bg ? 1 : 0);
-  const bool matched = out >= 0 && act < a.GT_total;
-  const bool has_void = a.void_idx >= 0;
-  const bool need_cls = a.force_cls || has_void;
-  const float coeff = a.g_cls[l] * (a.cls_scale * a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN]);
-  int64_t y = -1;
-  bool zero = (!matched && !need_cls) || coeff == 0.f;
-  if (!zero && matched) {
-    y = a.cls_targets[b * a.GT_total + act];
-    if (y < 0 || y >= C) zero = true;
-  }
-  if (zero) {
-    for (int64_t c = lane; c < C; c += 64) cls_out(a.grad_cls, a.cls_dtype, base + c, 0.f);
-    return;
-  }
-  if (a.use_softmax) {
-    if (matched || (a.force_cls && has_void)) {
-      const int64_t tgt = matched ? y : a.void_idx;
-      float m = -INFINITY;
-      for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_in(a.cls_logits, a.cls_dtype, base + c));
-      m = wave_max(m);
-      float se = 0.f;
-      for (int64_t c = lane; c < C; c += 64) se += __expf(cls_in(a.cls_logits, a.cls_dtype, base + c) - m);
-      se = wave_sum(se);
-      const float inv = se > 0.f ? 1.f / se : 0.f;
-      for (int64_t c = lane; c < C; c += 64) {
-        float gv = __expf(cls_in(a.cls_logits, a.cls_dtype, base + c) - m) * inv;
-        if (c == tgt) gv -= 1.f;
-        cls_out(a.grad_cls, a.cls_dtype, base + c, coeff * gv);
-      }
-    } else {  // has_void only
-      for (int64_t c = lane; c < C; c += 64) {
-        float gv = 0.f;
-        if (c == a.void_idx) {
-          const float z = cls_in(a.cls_logits, a.cls_dtype, base + c);
-          gv = coeff * (sig_terms(z).p - 1.f);
-        }
-        cls_out(a.grad_cls, a.cls_dtype, base + c, gv);
-      }
+  if (it < total) {
+    LutItem cur, nxt;
+    lut_load<CNT>(a, it, nchunk, vec, cur);
+    for (; it < total; it += gridDim.x) {
+      const int64_t it2 = it + gridDim.x;
+      if (it2 < total) lut_load<CNT>(a, it2, nchunk, vec, nxt);
+      lut_compute_store<CNT>(a, cur, lut, vec);
+      cur = nxt;
     }
-    return;
   }
-  const ElemParams ep = a.cls_ep;
-  const float g = a.cls_gamma;
-  const float invC = C > 0 ? 1.f / (float)C : 0.f;
-  for (int64_t c = lane; c < C; c += 64) {
-    const float z = cls_in(a.cls_logits, a.cls_dtype, base + c);
-    const Sig s = sig_terms(z);
-    float mn, mp;
-    focal_mods(s, ep, mn, mp);
-    const float posg = -ep.ap * mp * (g * s.p * s.cp + s.q1);
-    const float negg = ep.an * mn * (g * s.q1 * s.cn + s.p);
-    const bool is_void = has_void && c == a.void_idx;
-    float gv;
-    if (matched) {
-      gv = coeff * invC * (c == y ? posg : negg);
-    } else if (a.force_cls) {
-      gv = coeff * invC * (is_void ? posg : negg);
-    } else {
-      gv = is_void ? coeff * posg : 0.f;
-    }
-    cls_out(a.grad_cls, a.cls_dtype, base + c, gv);
+  // then the class-logit gradients, one row per wave (no separate launch)
+  if (a.cls_fused) {
+    constexpr int kWaves = kLutThreads / 64;
+    const int wave = threadIdx.x >> 6;
+    for (int64_t r0 = (int64_t)blockIdx.x * kWaves; r0 < rows; r0 += (int64_t)gridDim.x * kWaves)
+      if (r0 + wave < rows) cls_row(a, r0 + wave);
   }
 }
 
@@ -610,17 +621,22 @@ static int lut_grid() {
 
 int launch_bwd(const BwdArgs& a, const Dims& d, hipStream_t st) {
   const int64_t rows = d.L * d.B * d.Q;
+  bool cls_done = false;  // class-logit gradients fused into the mask kernel
   if (rows > 0 && d.HW > 0) {
     ProfScope ps_("bwd_mask", st);
     if (a.stats && a.dtype == ML_BF16 && g_use_lut) {
       const int64_t nchunk = ceil_div(d.HW, kLutChunk);
-      const int64_t grid = std::min<int64_t>(rows * nchunk, lut_grid());
+      const int64_t grid = std::max<int64_t>(
+          1, std::min<int64_t>(std::max(rows * nchunk, ceil_div(rows, kLutThreads / 64)), lut_grid()));
+      BwdArgs b = a;
+      b.cls_fused = d.C > 0 ? 1 : 0;
+      cls_done = true;
       if (d.counts_mode)
         hipLaunchKernelGGL(bwd_mask_lut_kernel<true>, dim3((unsigned)grid), dim3(kLutThreads), 0,
-                           st, a, nchunk);
+                           st, b, nchunk);
       else
         hipLaunchKernelGGL(bwd_mask_lut_kernel<false>, dim3((unsigned)grid), dim3(kLutThreads), 0,
-                           st, a, nchunk);
+                           st, b, nchunk);
     } else if (a.stats && a.list) {
       const int64_t nchunk = ceil_div(d.HW, kBwdChunk);
       const int64_t grid = std::min<int64_t>(rows * nchunk, kBwdListGrid);
@@ -634,7 +650,7 @@ int launch_bwd(const BwdArgs& a, const Dims& d, hipStream_t st) {
     int rc = check_launch("bwd_mask");
     if (rc) return rc;
   }
-  if (rows > 0 && d.C > 0) {
+  if (rows > 0 && d.C > 0 && !cls_done) {
     ProfScope ps_("bwd_cls", st);
     hipLaunchKernelGGL(bwd_cls_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, a);
     return check_launch("bwd_cls");

@@ -192,7 +192,9 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   };
   L.lab16 = take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2);
   L.counts8 = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0);
+  // present flags and the error word are contiguous: one fill clears them
   L.present = take((size_t)d.B * d.GT_total * 4);
+  L.err = take(16);
   L.ncols = take((size_t)d.B * 4);
   L.colmap = take((size_t)d.B * d.nslot * 4);
   L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
@@ -207,13 +209,13 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
   L.img = take((size_t)d.LB * 4 * 4);
   L.layer = take((size_t)d.L * ML_LAYERS * 4);
-  L.err = take(16);
   L.total = o;
   return L;
 }
 
 static bool cost_fits_lds(const Dims& d) {
-  return assign_smem_bytes(d.Q, d.GT_out, true) <= kMaxLds;
+  // 1 KB stays free for the assignment kernel's static LDS
+  return assign_smem_bytes(d.Q, d.GT_out, true) <= kMaxLds - 1024;
 }
 
 static int check_focal(float gamma, float alpha, const char* who) {
@@ -271,7 +273,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   if (ws_bytes < L.total) return fail(ML_EWORKSPACE, "workspace too small");
   unsigned char* w = (unsigned char*)ws;
   int rc;
-  if ((rc = launch_fill_i32((int*)(w + L.err), 0, 4, st))) return rc;
 
   const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
   const CostPlan plan = make_cost_plan(d, mask_dtype, tab);
@@ -281,6 +282,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.lab16 = (uint16_t*)(saved && !d.counts_mode ? sv + SL.lab16 : w + L.lab16);
   pa.counts8 = (uint8_t*)(w + L.counts8);
   pa.present = (int*)(w + L.present);
+  pa.fill_ints = (int64_t)((L.err + 16 - L.present) / 4);
   pa.ncols = (int*)(w + L.ncols);
   pa.colmap = (int*)(w + L.colmap);
   pa.slot_of_col = (int*)(w + L.slot_of_col);
@@ -389,14 +391,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
     if (hipEventRecord(sd->join, sd->s) != hipSuccess)
       return fail(ML_ELAUNCH, "prefill: join record failed");
   }
-  rc = d.LB > 0 ? launch_assign(aa, d, st) : ML_OK;
-  if (prefill_bytes) {  // join even after a failed launch: the buffer is the caller's
-    if (hipStreamWaitEvent(st, sd->join, 0) != hipSuccess && rc == ML_OK)
-      rc = fail(ML_ELAUNCH, "prefill: join failed");
-    side_lock.unlock();
-  }
-  if (rc) return rc;
-
+  // per-layer means and the matched-row list, after the assignment
   LayerArgs la;
   la.img = aa.img;
   la.layer = stats ? stats + d.LB * d.Q * ML_STATS : (float*)(w + L.layer);
@@ -408,6 +403,13 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   la.force_masks = force_masks;
   la.force_cls = p->force_unmatched_class_to_background;
   la.has_void = void_idx >= 0;
+  rc = d.LB > 0 ? launch_assign(aa, d, st) : ML_OK;
+  if (prefill_bytes) {  // join even after a failed launch: the buffer is the caller's
+    if (hipStreamWaitEvent(st, sd->join, 0) != hipSuccess && rc == ML_OK)
+      rc = fail(ML_ELAUNCH, "prefill: join failed");
+    side_lock.unlock();
+  }
+  if (rc) return rc;
   if (d.L > 0 && (rc = launch_layer(la, st))) return rc;
   return ML_OK;
 }
@@ -633,6 +635,7 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   ba.cls_ep = ba.use_softmax ? make_elem_params(0.f, -1.f, 0.f, 0.f)
                              : make_elem_params(p->cls_gamma, p->cls_alpha, 0.f, 0.f);
   ba.cls_gamma = ba.use_softmax ? 0.f : p->cls_gamma;
+  ba.cls_fused = 0;
   return launch_bwd(ba, d, st);
 }
 

@@ -140,6 +140,7 @@ struct PrepArgs {
   uint16_t* lab16;
   uint8_t* counts8;
   int* present;          // [B][GT_total]: 1 iff the GT has pixels (forward only, else null)
+  int64_t fill_ints;     // ints cleared from `present` on (flags, error word)
   int* ncols;
   int* colmap;
   int* slot_of_col;
@@ -166,6 +167,17 @@ struct CostArgs {
   float N2;
   ElemParams ep;
   int use_lut;       // bf16 logits: per-cell planes from the LDS table
+};
+
+struct LayerArgs {
+  const float* img;
+  float* layer;        // [L][ML_LAYERS]
+  float* means;        // (3, L)
+  const int64_t* pred_to_gt;
+  int* list;           // matched-row list of the saved state, or null
+  int64_t L, B, Q;
+  double num_masks;
+  int force_masks, force_cls, has_void;
 };
 
 struct AssignArgs {
@@ -207,16 +219,6 @@ struct AssignArgs {
   int cost_in_lds;
 };
 
-struct LayerArgs {
-  const float* img;
-  float* layer;        // [L][ML_LAYERS]
-  float* means;        // (3, L)
-  const int64_t* pred_to_gt;
-  int* list;           // matched-row list of the saved state, or null
-  int64_t L, B, Q;
-  double num_masks;
-  int force_masks, force_cls, has_void;
-};
 
 struct BwdArgs {
   const void* logits;
@@ -243,6 +245,7 @@ struct BwdArgs {
   ElemParams mask_ep;
   ElemParams cls_ep;
   float cls_gamma;
+  int cls_fused;          // the mask kernel also writes the class-logit gradients
 };
 
 // Non-pairwise sigmoid-CE / dice over dense class logits (L, B, C, H, W).

@@ -88,6 +88,72 @@ __device__ __forceinline__ void mark_present(unsigned char* pres, int* present, 
   else present[lab] = 1;
 }
 
+// Compacted list of the columns whose GT is non-empty, one wave per image
+// (images w, w + nwaves, ...), then, on wave 0, the cost schedule (per
+// column-tile class: its tasks in ascending order, their count and K-split;
+// per task: its position in its class list).  Run by one workgroup after the
+// target-preparation grid.
+__device__ void columns_and_schedule(const PrepArgs& a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const uint64_t below = (1ull << lane) - 1ull;
+  for (int64_t b = wave; b < a.B; b += nw) {
+    int base = 0;
+    for (int64_t c0 = 0; c0 < a.GT_out; c0 += 64) {
+      const int64_t c = c0 + lane;
+      bool ok = false;
+      if (c < a.GT_out) {
+        const int64_t act = c + (c >= a.bg ? 1 : 0);
+        ok = a.present[b * a.GT_total + act] != 0;
+      }
+      const uint64_t m = __ballot(ok);
+      const int slot = base + __popcll(m & below);
+      if (c < a.GT_out) {
+        a.slot_of_col[b * a.GT_out + c] = ok ? slot : -1;
+        if (ok) a.colmap[b * a.nslot + slot] = (int)c;
+      }
+      base += __popcll(m);
+    }
+    for (int s = base + lane; s < a.nslot; s += 64) a.colmap[b * a.nslot + s] = -1;
+    if (lane == 0) a.ncols[b] = base;
+  }
+  if (!a.sched) return;
+  __syncthreads();
+  if (wave != 0) return;
+  const int64_t nt = a.plan.ntasks;
+  int* list = a.sched + 2 * kClasses;
+  int* idx = list + kClasses * nt;
+  int cnt[kClasses] = {0, 0, 0, 0};
+  for (int64_t t0 = 0; t0 < nt; t0 += 64) {
+    const int64_t t = t0 + lane;
+    int ci = -1;
+    if (t < nt) ci = class_of(a.ncols[(t / a.rtiles) % a.B] + 1);
+#pragma unroll
+    for (int c = 0; c < kClasses; ++c) {
+      const uint64_t m = __ballot(ci == c);
+      if (ci == c) {
+        const int pos = cnt[c] + __popcll(m & below);
+        list[c * nt + pos] = (int)t;
+        idx[t] = pos;
+      }
+      cnt[c] += __popcll(m);
+    }
+  }
+  if (lane < kClasses) {
+    int n = 0, slots = 0;
+#pragma unroll
+    for (int c = 0; c < kClasses; ++c)
+      if (c == lane) {
+        n = cnt[c];
+        slots = a.plan.slots[c];
+      }
+    int64_t ks = n > 0 ? slots / n : 1;
+    ks = ks < 1 ? 1 : (ks > a.plan.ks_max ? a.plan.ks_max : ks);
+    a.sched[lane] = n;
+    a.sched[kClasses + lane] = (int)ks;
+  }
+}
+
 // s == 1: each thread converts 8 consecutive cells.  grid (ceil(HWp/2048), B)
 __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
   __shared__ unsigned char pres[kMarkMax];
@@ -173,75 +239,14 @@ __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
   }
 }
 
-// One wave per image: compacted list of columns with non-empty GT.
-// One workgroup: wave w compacts the columns of images w, w + 16, ...; then
-// wave 0 builds the cost schedule (per column-tile class: its tasks in
-// ascending order, their count and K-split; per task: its position in its
-// class list).
-__global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const uint64_t below = (1ull << lane) - 1ull;
-  for (int64_t b = wave; b < a.B; b += 16) {
-    int base = 0;
-    for (int64_t c0 = 0; c0 < a.GT_out; c0 += 64) {
-      const int64_t c = c0 + lane;
-      bool ok = false;
-      if (c < a.GT_out) {
-        const int64_t act = c + (c >= a.bg ? 1 : 0);
-        ok = a.present[b * a.GT_total + act] != 0;
-      }
-      const uint64_t m = __ballot(ok);
-      const int slot = base + __popcll(m & below);
-      if (c < a.GT_out) {
-        a.slot_of_col[b * a.GT_out + c] = ok ? slot : -1;
-        if (ok) a.colmap[b * a.nslot + slot] = (int)c;
-      }
-      base += __popcll(m);
-    }
-    for (int s = base + lane; s < a.nslot; s += 64) a.colmap[b * a.nslot + s] = -1;
-    if (lane == 0) a.ncols[b] = base;
-  }
-  if (!a.sched) return;
-  __syncthreads();
-  if (wave != 0) return;
-  const int64_t nt = a.plan.ntasks;
-  int* list = a.sched + 2 * kClasses;
-  int* idx = list + kClasses * nt;
-  int cnt[kClasses] = {0, 0, 0, 0};
-  for (int64_t t0 = 0; t0 < nt; t0 += 64) {
-    const int64_t t = t0 + lane;
-    int ci = -1;
-    if (t < nt) ci = class_of(a.ncols[(t / a.rtiles) % a.B] + 1);
-#pragma unroll
-    for (int c = 0; c < kClasses; ++c) {
-      const uint64_t m = __ballot(ci == c);
-      if (ci == c) {
-        const int pos = cnt[c] + __popcll(m & below);
-        list[c * nt + pos] = (int)t;
-        idx[t] = pos;
-      }
-      cnt[c] += __popcll(m);
-    }
-  }
-  if (lane < kClasses) {
-    int n = 0, slots = 0;
-#pragma unroll
-    for (int c = 0; c < kClasses; ++c)
-      if (c == lane) {
-        n = cnt[c];
-        slots = a.plan.slots[c];
-      }
-    int64_t ks = n > 0 ? slots / n : 1;
-    ks = ks < 1 ? 1 : (ks > a.plan.ks_max ? a.plan.ks_max : ks);
-    a.sched[lane] = n;
-    a.sched[kClasses + lane] = (int)ks;
-  }
-}
+// One workgroup: runs once every presence mark of the preparation grid is in.
+__global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) { columns_and_schedule(a); }
 
 int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   ProfScope ps_("prep", st);
   int rc;
-  if (a.present && (rc = launch_fill_i32(a.present, 0, d.B * d.GT_total, st))) return rc;
+  // presence flags, error word and grid tickets in one fill
+  if (a.present && (rc = launch_fill_i32(a.present, 0, a.fill_ints, st))) return rc;
   if (!d.counts_mode) {
     const dim3 grid((unsigned)ceil_div(d.HWp, 256 * 8), (unsigned)d.B);
     hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);

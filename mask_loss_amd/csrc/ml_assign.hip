@@ -152,6 +152,10 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
     }
   }
   wave_sync();
+  if (a.rowIT) {  // summed intersection / target mass of every real slot (backward statistics)
+    float2* it = (float2*)a.rowIT + row * a.nslot;
+    for (int s = lane; s < G; s += 64) it[s] = make_float2(sl[wave][1][s], sl[wave][2][s]);
+  }
   float S = sl[wave][2][G];
   const float P = sl[wave][1][G];
   if (!a.normalize) S = (float)(a.Ht * a.Wt);
@@ -235,6 +239,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
     if (a.out_bce) a.out_bce[o] = bce;
     if (a.out_dice) a.out_dice[o] = dice;
     if (labels) a.sep[2 * term + o] = cls;
+    if (a.tot) a.tot[lb * a.tot_stride + q * GTo + c] = (bce + dice) + cls;  // matching.cpp:665
   }
   if (lane == 0 && a.rowstat) {
     float mp = 0.f, dp = 0.f;
@@ -258,53 +263,120 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
   }
 }
 // ---------------------------------------------------------------------------
+// wave64 helpers: DPP lane exchanges and a min-reduction without LDS traffic
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const uint64_t u = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// Minimum over the wave, returned in every lane: DPP swaps within each row of
+// 16 lanes (xor 1, xor 2, half-row mirror, row mirror), then the four row
+// minima through readlane.  min is exact, so the order does not matter.
+__device__ __forceinline__ double wave_min_dpp(double v) {
+  v = fmin(v, dpp_d<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmin(v, dpp_d<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmin(v, dpp_d<0x141>(v));  // row_half_mirror
+  v = fmin(v, dpp_d<0x140>(v));  // row_mirror
+  return fmin(fmin(readlane_d(v, 0), readlane_d(v, 16)), fmin(readlane_d(v, 32), readlane_d(v, 48)));
+}
+
+// ---------------------------------------------------------------------------
 // e-maxx Hungarian on one wave.  Rows = hrows[0..M) (GT columns), columns =
 // preds[0..n) (queries).  asg[k] = row index assigned to column k, or -1.
 // Mirrors src/cpu/matching.cpp:95-186 operation by operation.
+//
+// Column j = 1 + lane + 64 t lives in lane `lane`, register slot t: its
+// potential v, its matched row p (0 = free), and, for that row, the row
+// potential u[p] and its cost-matrix row; the row being inserted keeps its
+// potential and cost row in wave-uniform registers.  So the Dijkstra steps
+// touch LDS only for the cost entries: every potential update is a register
+// add, the row of a newly reached column is a readlane, and the minimum is a
+// DPP reduction.  Each row potential receives the same float64 additions in
+// the same order as in the reference (one += delta per step in which its
+// column is in the tree), so the assignment is the reference's bit for bit.
 // ---------------------------------------------------------------------------
+// Register slot t of lane l, broadcast: every slot is read with readlane and
+// the uniform index picks one (a select chain over registers would be folded
+// back into a dynamically indexed array in scratch memory).
+template <int NJ>
+__device__ __forceinline__ int rl_i(const int (&x)[NJ], int t, int l) {
+  int r = __builtin_amdgcn_readlane(x[0], l);
+#pragma unroll
+  for (int k = 1; k < NJ; ++k) {
+    const int y = __builtin_amdgcn_readlane(x[k], l);
+    r = k == t ? y : r;
+  }
+  return r;
+}
+template <int NJ>
+__device__ __forceinline__ double rl_d(const double (&x)[NJ], int t, int l) {
+  double r = readlane_d(x[0], l);
+#pragma unroll
+  for (int k = 1; k < NJ; ++k) {
+    const double y = readlane_d(x[k], l);
+    r = k == t ? y : r;
+  }
+  return r;
+}
+
 template <int NJ>
 __device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds, int n,
                                const int* hrows, int M, double thr, double BIG, int* p, int* way,
                                double* u, int* asg) {
+  (void)p;
+  (void)way;
+  (void)u;
   const int lane = threadIdx.x & 63;
   for (int k = lane; k < n; k += 64) asg[k] = -1;
   wave_sync();
   if (M == 0 || n == 0 || n < M) return true;
-  for (int j = lane; j <= n; j += 64) p[j] = 0;
-  for (int i = lane; i <= M; i += 64) u[i] = 0.0;
-  double v[NJ];
-  int pj[NJ];
-  int predj[NJ];
+  double v[NJ], ucol[NJ];
+  int pj[NJ], rcol[NJ], predj[NJ];
+  bool valid[NJ];
 #pragma unroll
   for (int t = 0; t < NJ; ++t) {
-    v[t] = 0.0;
-    pj[t] = 0;
     const int j = 1 + lane + 64 * t;
-    predj[t] = j <= n ? preds[j - 1] : 0;
+    valid[t] = j <= n;
+    v[t] = 0.0;
+    ucol[t] = 0.0;
+    pj[t] = 0;
+    rcol[t] = 0;
+    predj[t] = valid[t] ? preds[j - 1] : 0;
   }
-  wave_sync();
   bool ok = true;
   for (int i = 1; i <= M && ok; ++i) {
     double minv[NJ];
     int wy[NJ];
-    unsigned used = 0;  // bit t: column 1+lane+64t visited
+    unsigned used = 0;  // bit t: column 1 + lane + 64 t is in the tree
 #pragma unroll
     for (int t = 0; t < NJ; ++t) {
       minv[t] = INFINITY;
       wy[t] = 0;
     }
+    double ucur = 0.0;  // potential of row i (column 0 of the reference)
+    const int colcur = hrows[i - 1];
     int j0 = 0;
-    int i0 = i;
+    double ui0 = ucur;
+    int col = colcur;
     for (;;) {
-      const int col = hrows[i0 - 1];
-      const double ui0 = u[i0];
       const float* crow = cost + (int64_t)col * ldq;
+      float rawf[NJ];  // all reads issued together (predj is in range for every lane)
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
       double lmin = INFINITY;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const int j = 1 + lane + 64 * t;
-        if (j <= n && !((used >> t) & 1u)) {
-          const double raw = (double)crow[predj[t]];
+        if (valid[t] && !((used >> t) & 1u)) {
+          const double raw = (double)rawf[t];
           const double cij = cost_ok(raw, thr) ? raw : BIG;
           const double cur = cij - ui0 - v[t];
           if (cur < minv[t]) {
@@ -314,7 +386,7 @@ __device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds,
           lmin = fmin(lmin, minv[t]);
         }
       }
-      const double delta = wave_min_d(lmin);
+      const double delta = wave_min_dpp(lmin);
       if (!isfinite(delta)) {
         ok = false;
         break;
@@ -323,68 +395,70 @@ __device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds,
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
         if (j1 == 0) {
-          const int j = 1 + lane + 64 * t;
-          const bool hit = j <= n && !((used >> t) & 1u) && minv[t] == delta;
+          const bool hit = valid[t] && !((used >> t) & 1u) && minv[t] == delta;
           const uint64_t m = __ballot(hit);
           if (m) j1 = 1 + (__ffsll((unsigned long long)m) - 1) + 64 * t;
         }
       }
-      if (j1 == 0) {  // unreachable with finite costs; keeps the walk below bounded
+      if (j1 == 0) {  // unreachable with finite costs
         ok = false;
         break;
       }
-      // potentials: used columns (and column 0 -> current row i), others' minv
+      // potentials: columns in the tree (and column 0 = row i), others' minv
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const int j = 1 + lane + 64 * t;
-        if (j <= n) {
+        if (valid[t]) {
           if ((used >> t) & 1u) {
-            u[pj[t]] += delta;
+            ucol[t] += delta;
             v[t] -= delta;
           } else {
             minv[t] -= delta;
           }
         }
       }
-      if (lane == 0) u[i] += delta;
-      // mark j1 used
-      const int o_lane = (j1 - 1) & 63, o_t = (j1 - 1) >> 6;
-      if (lane == o_lane) used |= 1u << o_t;
+      ucur += delta;
+      const int ol = (j1 - 1) & 63, ot = (j1 - 1) >> 6;
+      if (lane == ol) used |= 1u << ot;
       j0 = j1;
-      wave_sync();
-      const int pj0 = p[j0];
+      const int pj0 = rl_i<NJ>(pj, ot, ol);
       if (pj0 == 0) break;
-      i0 = pj0;
+      // next row of the tree: the one matched to column j1
+      ui0 = rl_d<NJ>(ucol, ot, ol);
+      col = rl_i<NJ>(rcol, ot, ol);
     }
     if (!ok) break;
-    // augment along way[]
+    // augment along way[] from the free column j0 back to column 0: each
+    // column on the path takes the row (and that row's potential and cost
+    // row) of the column it was reached from; column 0 holds row i.
+    for (int steps = 0; j0 != 0 && steps <= n; ++steps) {
+      const int ol = (j0 - 1) & 63, ot = (j0 - 1) >> 6;
+      const int jp = rl_i<NJ>(wy, ot, ol);
+      int np, nr;
+      double nu;
+      if (jp == 0) {
+        np = i;
+        nu = ucur;
+        nr = colcur;
+      } else {
+        const int pl = (jp - 1) & 63, pt = (jp - 1) >> 6;
+        np = rl_i<NJ>(pj, pt, pl);
+        nu = rl_d<NJ>(ucol, pt, pl);
+        nr = rl_i<NJ>(rcol, pt, pl);
+      }
 #pragma unroll
-    for (int t = 0; t < NJ; ++t) {
-      const int j = 1 + lane + 64 * t;
-      if (j <= n) way[j] = wy[t];
-    }
-    wave_sync();
-    if (lane == 0) {
-      p[0] = i;
-      way[0] = 0;
-      int jj = j0;
-      int steps = 0;
-      do {
-        const int j1 = way[jj];
-        p[jj] = p[j1];
-        jj = j1;
-      } while (jj != 0 && ++steps <= n);
-    }
-    wave_sync();
-#pragma unroll
-    for (int t = 0; t < NJ; ++t) {
-      const int j = 1 + lane + 64 * t;
-      pj[t] = j <= n ? p[j] : 0;
+      for (int t = 0; t < NJ; ++t) {
+        const bool mine = lane == ol && t == ot;
+        pj[t] = mine ? np : pj[t];
+        ucol[t] = mine ? nu : ucol[t];
+        rcol[t] = mine ? nr : rcol[t];
+      }
+      j0 = jp;
     }
   }
   if (ok) {
-    for (int j = 1 + lane; j <= n; j += 64)
-      if (p[j] > 0) asg[j - 1] = p[j] - 1;
+#pragma unroll
+    for (int t = 0; t < NJ; ++t)
+      if (valid[t] && pj[t] > 0) asg[lane + 64 * t] = pj[t] - 1;
   }
   wave_sync();
   return ok;
@@ -489,10 +563,13 @@ __device__ void layer_pass(const LayerArgs& a) {
   if (threadIdx.x == 0) a.list[0] = base;
 }
 
-template <int NJ>
+// INLDS: the image's cost matrix fits in LDS (else it lives in the costT
+// workspace); a compile-time choice, so cost reads are ds_read (or global)
+// rather than flat loads.
+template <int NJ, bool INLDS>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const SmemLayout L = smem_layout(a.Q, a.GT_out, a.cost_in_lds != 0);
+  const SmemLayout L = smem_layout(a.Q, a.GT_out, INLDS);
   float* contrib = (float*)(smem + L.contrib);
   int* colok = (int*)(smem + L.colok);
   int* vcols = (int*)(smem + L.vcols);
@@ -509,7 +586,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   const int64_t lb = blockIdx.x, b = lb % a.B;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t Q = a.Q, GTo = a.GT_out;
-  float* costL = a.cost_in_lds ? (float*)(smem + L.costL) : a.costT + lb * GTo * Q;
+  float* costL = INLDS ? (float*)(smem + L.costL) : a.costT + lb * GTo * Q;
   const int64_t term = a.L * a.B * Q * GTo;
   const float* sep = a.sep + lb * Q * GTo;
 
@@ -518,27 +595,36 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   for (int64_t c = tid; c <= GTo; c += 256) colok[c] = 0;
   __syncthreads();
   {
-    const int64_t n = Q * GTo;
-    constexpr int U = 8;  // independent loads in flight per thread
-    for (int64_t i0 = tid; i0 < n; i0 += 256 * U) {
-      float v0[U], v1[U], v2[U];
+    // the image's (bce + dice) + cls plane from finalize: [q][c], a padded
+    // stride of whole 16-byte words; every thread issues all of its 16-byte
+    // loads before the first transposed LDS store
+    const uint32_t n = (uint32_t)(Q * GTo), n4 = (n + 3) / 4;
+    const float4* tot = (const float4*)(a.tot + lb * a.tot_stride);
+    const uint32_t gto = (uint32_t)GTo, q32 = (uint32_t)Q;
+    constexpr int U = 24;  // 24 x 256 x 16 B = 96 KB per round
+    for (uint32_t v0 = tid; v0 < n4; v0 += 256 * U) {
+      float4 v[U];
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        const int64_t i = i0 + k * 256;
-        if (i < n) {
-          v0[k] = sep[i];
-          v1[k] = sep[term + i];
-          v2[k] = sep[2 * term + i];
-        }
+        const uint32_t vi = v0 + k * 256;
+        if (vi < n4) v[k] = tot[vi];
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        const int64_t i = i0 + k * 256;
-        if (i < n) {
-          const int64_t q = i / GTo, c = i % GTo;
-          const float tot = (v0[k] + v1[k]) + v2[k];
-          costL[c * Q + q] = tot;
-          if (cost_ok((double)tot, a.inf_thresh)) colok[c] = 1;  // benign race: all store 1
+        const uint32_t vi = v0 + k * 256;
+        if (vi >= n4) continue;
+        uint32_t i = vi * 4, q = i / gto, c = i - q * gto;
+        const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+        for (int h = 0; h < 4; ++h, ++i) {
+          if (i < n) {
+            costL[c * q32 + q] = e[h];
+            if (cost_ok((double)e[h], a.inf_thresh)) colok[c] = 1;  // benign race: all store 1
+          }
+          if (++c == gto) {
+            c = 0;
+            ++q;
+          }
         }
       }
     }
@@ -712,13 +798,10 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       cd = sep[term + q * GTo + c];
       cc = sep[2 * term + q * GTo + c];
       const int slot = a.slot_of_col[b * GTo + c];
-      if (slot >= 0 && a.stats) {
-        const RowPartials rp =
-            row_partials(a.partials, a.sched, a.plan, lb, q, a.rows, a.rtiles, a.ncols[b]);
-        for (int ks = 0; ks < rp.KS; ++ks) {
-          I += rp.p0[ks * rp.ks_stride + rp.plane + slot];
-          T += rp.p0[ks * rp.ks_stride + 2 * rp.plane + slot];
-        }
+      if (slot >= 0 && a.rowIT) {
+        const float2 it = ((const float2*)a.rowIT)[(lb * Q + q) * a.nslot + slot];
+        I = it.x;
+        T = it.y;
       }
     } else {
       if (a.force_masks) {
@@ -788,16 +871,16 @@ size_t assign_smem_bytes(int64_t Q, int64_t GTo, bool cost_in_lds) {
   return smem_layout(Q, GTo, cost_in_lds).total;
 }
 
-template <int NJ>
-static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
-  const size_t sm = smem_layout(a.Q, a.GT_out, a.cost_in_lds != 0).total;
+template <int NJ, bool INLDS>
+static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
+  const size_t sm = smem_layout(a.Q, a.GT_out, INLDS).total;
   static size_t max_dyn = 0;  // 160 KB of LDS less the kernel's static part
   if (max_dyn == 0) {
     hipFuncAttributes fa;
-    if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ>) != hipSuccess)
+    if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ, INLDS>) != hipSuccess)
       return fail(ML_ELAUNCH, "assign: cannot query the kernel attributes");
     const size_t dyn = 160 * 1024 - fa.sharedSizeBytes;
-    if (hipFuncSetAttribute((const void*)assign_kernel<NJ>,
+    if (hipFuncSetAttribute((const void*)assign_kernel<NJ, INLDS>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
       return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
     max_dyn = dyn;
@@ -805,11 +888,14 @@ static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
   if (sm > max_dyn) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
   {
     ProfScope ps_("assign", st);
-    hipLaunchKernelGGL(assign_kernel<NJ>, dim3((unsigned)d.LB), dim3(256), sm, st, a);
+    hipLaunchKernelGGL((assign_kernel<NJ, INLDS>), dim3((unsigned)d.LB), dim3(256), sm, st, a);
   }
   return check_launch("assign");
 }
-
+template <int NJ>
+static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
+  return a.cost_in_lds ? launch_nj_l<NJ, true>(a, d, st) : launch_nj_l<NJ, false>(a, d, st);
+}
 int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const int64_t rows = d.LB * d.Q;
   if (rows == 0) return ML_OK;

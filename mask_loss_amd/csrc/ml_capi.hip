@@ -206,6 +206,8 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   L.flags = take((size_t)pl.nclass * cap * 4);
   L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
+  L.tot = take((size_t)d.LB * ceil_div(d.Q * d.GT_out, 4) * 16);
+  L.rowIT = take((size_t)d.LB * d.Q * d.nslot * 8);
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
   L.img = take((size_t)d.LB * 4 * 4);
   L.layer = take((size_t)d.L * ML_LAYERS * 4);
@@ -333,6 +335,9 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   }
   aa.rowstat = (float*)(w + L.rowstat);
   aa.costT = in_lds ? nullptr : (float*)(w + L.costT);
+  aa.tot = costs_only ? nullptr : (float*)(w + L.tot);
+  aa.tot_stride = ceil_div(d.Q * d.GT_out, 4) * 4;
+  aa.rowIT = costs_only || !stats ? nullptr : (float*)(w + L.rowIT);
   aa.pred_to_gt = pred_to_gt;
   aa.pred_round = pred_round;
   aa.stats = stats;

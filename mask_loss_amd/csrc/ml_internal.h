@@ -126,7 +126,7 @@ inline SavedLayout saved_layout(const Dims& d) {
 // Byte offsets inside the caller's workspace.
 struct Layout {
   size_t lab16, counts8, present, ncols, colmap, slot_of_col, sched, partials, rowsum, flags,
-      costT, sep, rowstat, img, layer, err, total;
+      costT, sep, tot, rowIT, rowstat, img, layer, err, total;
 };
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
 // Plan slots / offsets of the cost launches (queries kernel occupancy on the
@@ -196,6 +196,9 @@ struct AssignArgs {
   float* out_bce;        // where finalize writes the bce / dice planes (sep's
   float* out_dice;       // first two planes, or a standalone operator's outputs, or null)
   float* costT;          // [LB][GT_out][Q] transposed total cost (global fallback)
+  float* tot;            // [LB][tot_stride] total cost (bce + dice) + label per (q, c), or null
+  int64_t tot_stride;    // Q * GT_out rounded up to whole 16-byte words
+  float* rowIT;          // [LB*Q][nslot][2] summed I, T per column slot, or null
   int64_t* pred_to_gt;   // (L,B,Q) or null (costs-only mode)
   int64_t* pred_round;
   float* stats;          // (L,B,Q,ML_STATS) or null

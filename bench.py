@@ -33,8 +33,12 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg3_dense_headline")
-    ap.add_argument("--cpu-sample-queries", type=int, default=50)
+    ap.add_argument("--cpu-sample-images", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the per-config lines of the other BASELINE configurations")
+    ap.add_argument("--other-steps", type=int, default=10)
+    ap.add_argument("--other-warmup", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of 512 MiB (3 launches), the reference "
                          "point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -85,68 +89,67 @@ def read_prof(lib, name):
     return n.value, t.value
 
 
-def cpu_baseline(cfg, x_cpu, p2g_gpu, total_gpu, q_sample):
-    """Float64 oracle on image 0 with the first q_sample queries (cost, forward
-    losses, backward) + the C assignment restatement on every image's GPU cost
-    matrix; scaled to one full step."""
+def cpu_baseline(cfg, x, z, zc, p2g_gpu, total_gpu, n_img):
+    """Float64 oracle (cost, matched-loss forward, backward) on the first n_img
+    images with all of their queries, one image at a time, plus the C
+    assignment restatement on every image's GPU cost matrix; scaled to one
+    full step (B images)."""
     import numpy as np
     from oracle import assign as OA
     from oracle import mask_oracle as O
     k = cfg.kwargs
-    qs = min(q_sample, cfg.Q)
-    z = x_cpu["mask_logits"][:, :1, :qs].astype(np.float64)
-    tgt = x_cpu["mask_targets"][:1]
-    zc = x_cpu["cls_logits"][:, :1, :qs].astype(np.float64)
-    ct = x_cpu["cls_targets"][:1]
-    t0 = time.perf_counter()
-    sep = O.pairwise_mask_loss_forward(z, tgt, zc, ct, k["smooth"], k["sigmoid_scale"],
-                                       k["dice_scale"], k["cls_scale"], k["background_index"],
-                                       k["uncertainty_gamma"], k["uncertainty_gamma_min"], 0.0,
-                                       -1.0, 0.0, -1.0, True, True)
-    p2g = p2g_gpu[:, :1, :qs]
-    O.matching_forward_losses(sep, p2g, z, zc, tgt.shape, force_cls=True,
-                              void_class_index=cfg.C, use_softmax=True)
-    O.matching_backward(np.ones(1), np.ones(1), np.ones(1), z, tgt, zc, ct, p2g,
-                        background_index=0, force_cls=True, void_class_index=cfg.C,
-                        use_softmax=True)
-    t_img = time.perf_counter() - t0
+    n_img = max(1, min(n_img, cfg.B))
+    t_img = 0.0
+    for b in range(n_img):
+        zb = z.detach()[:, b:b + 1].float().cpu().numpy().astype(np.float64)
+        zcb = zc.detach()[:, b:b + 1].float().cpu().numpy().astype(np.float64)
+        tgt = x["mask_targets"][b:b + 1].cpu().numpy()
+        ct = x["cls_targets"][b:b + 1].cpu().numpy()
+        p2g = p2g_gpu[:, b:b + 1]
+        t0 = time.perf_counter()
+        sep = O.pairwise_mask_loss_forward(zb, tgt, zcb, ct, k["smooth"], k["sigmoid_scale"],
+                                           k["dice_scale"], k["cls_scale"], k["background_index"],
+                                           k["uncertainty_gamma"], k["uncertainty_gamma_min"], 0.0,
+                                           -1.0, 0.0, -1.0, True, True)
+        O.matching_forward_losses(sep, p2g, zb, zcb, tgt.shape, force_cls=True,
+                                  void_class_index=cfg.C, use_softmax=True)
+        O.matching_backward(np.ones(1), np.ones(1), np.ones(1), zb, tgt, zcb, ct, p2g,
+                            background_index=0, force_cls=True, void_class_index=cfg.C,
+                            use_softmax=True)
+        t_img += time.perf_counter() - t0
     t0 = time.perf_counter()
     L, B, Q, G = total_gpu.shape
     OA.assign_batch(total_gpu.reshape(L * B, Q, G), 1e30, 1, 0, nthreads=1)
     t_match = time.perf_counter() - t0
-    scale = (cfg.L * cfg.B * cfg.Q) / qs
+    scale = cfg.B / n_img
     ms = (t_img * scale + t_match) * 1e3
     return {
         "value": round(ms, 1), "unit": "ms/step", "cores": 1, "kind": "port",
-        "sample": (f"float64 NumPy oracle on 1 image x {qs} of {cfg.Q} queries (cost + matched "
-                   f"loss fwd/bwd, {t_img:.1f} s) scaled x{scale:.0f}, plus the C assignment "
-                   f"restatement on all {L * B} GPU cost matrices ({t_match * 1e3:.1f} ms)"),
+        "sample": (f"float64 NumPy oracle on {n_img} of {cfg.B} images, all {cfg.Q} queries each "
+                   f"(cost + matched loss fwd/bwd, {t_img:.1f} s) scaled x{scale:.0f}, plus the C "
+                   f"assignment restatement on all {L * B} GPU cost matrices "
+                   f"({t_match * 1e3:.1f} ms)"),
     }
 
 
-def main():
-    a = parse()
-    if a.copy_calibration:
-        copy_calibration()
-        return
-    if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not built)"}))
-        sys.exit(2)
-    import numpy as np
-    import torch
+def step_bytes_of(cfg, e, M):
+    """Algorithmic HBM bytes of one step: logits read by the forward, matched
+    logits read and all gradients written by the backward, the int64 label
+    map once, class logits read twice and their gradient written once."""
+    K = cfg.H * cfg.W
+    LBQ = cfg.L * cfg.B * cfg.Q
+    Ht, Wt = cfg.H * cfg.scale, cfg.W * cfg.scale
+    return e * K * (LBQ + M + LBQ) + 8 * cfg.B * Ht * Wt + 12 * LBQ * (cfg.C + 1)
 
-    import mask_loss_amd
+
+def make_step(cfg, dev):
+    import torch
     from mask_loss_amd import synth
     from mask_loss_amd.functions import MaskMatchingFunction
-
-    cfg = synth.BY_NAME[a.config]
-    dev = torch.device("cuda:0")
     x = synth.make_torch(cfg, dev, logits_on_device_rng=True)
     z = x["mask_logits"].requires_grad_(True)
     zc = x["cls_logits"].requires_grad_(True)
     args = synth.call_args(cfg, dict(x, mask_logits=z, cls_logits=zc))
-
     state = {}
     # upstream gradients of the three per-layer means: ones(L) each, i.e. the
     # gradient of loss = sum of the layer means
@@ -159,17 +162,59 @@ def main():
         torch.autograd.backward((m, d, c), ones)
         state["p2g"] = p2g
 
-    for _ in range(a.warmup):
+    return x, z, zc, step, state
+
+
+def time_steps(step, steps, warmup):
+    import torch
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    # timed region: K steps, no instrumentation
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(a.steps):
+    for _ in range(steps):
         step()
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / a.steps
+    return e0.elapsed_time(e1) / steps
+
+
+def other_config(cfg, dev, steps, warmup):
+    """ms/step, images/s and the step's fraction of the HBM / MFMA roofline for
+    another BASELINE configuration (same step, fewer timed steps)."""
+    x, z, zc, step, state = make_step(cfg, dev)
+    ms = time_steps(step, steps, warmup)
+    M = int((state["p2g"] >= 0).sum().item())
+    e = z.element_size()
+    sb = step_bytes_of(cfg, e, M)
+    t_hbm = sb / HBM_PEAK_GBS / 1e3  # us
+    t_roof = t_hbm  # HBM binds in every configuration (the contraction's MFMA time is lower)
+    return {"workload": cfg.name, "ms_per_step": round(ms, 4),
+            "images_per_s": round(cfg.B * cfg.L / (ms * 1e-3), 1), "dtype": cfg.dtype,
+            "matched": M, "step_algorithmic_bytes": sb, "hbm_floor_us": round(t_hbm, 1),
+            "roofline_frac": round(t_roof / (ms * 1e3), 4), "steps": steps, "warmup": warmup}
+
+
+def main():
+    a = parse()
+    if a.copy_calibration:
+        copy_calibration()
+        return
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                                   "(the step shards over images across GPUs, which is not "
+                                   "built here)"}))
+        sys.exit(2)
+    import torch
+
+    import mask_loss_amd
+    from mask_loss_amd import synth
+
+    cfg = synth.BY_NAME[a.config]
+    dev = torch.device("cuda:0")
+    x, z, zc, step, state = make_step(cfg, dev)
+    # timed region: K steps, no instrumentation
+    ms = time_steps(step, a.steps, a.warmup)
     # per-kernel breakdown: another K steps with the library's HIP events
     # recorded around each launch group on the launch stream (the events add
     # gaps between launches, so this pass is not the timed one)
@@ -202,7 +247,7 @@ def main():
         "prefill": e * K * LBQ,                          # gradient buffer zero-filled
         "assign": 4 * LBQ * Cp,                          # class logits
     }
-    step_bytes = e * K * (LBQ + M + LBQ) + 8 * cfg.B * Ht * Wt + 12 * LBQ * Cp
+    step_bytes = step_bytes_of(cfg, e, M)
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
     dom_bytes = bytes_alg.get(dom)
     achieved = dom_bytes / (kernels[dom]["avg_us"] * 1e-6) / 1e9 if dom_bytes else None
@@ -225,18 +270,17 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        qs = min(a.cpu_sample_queries, cfg.Q)
-        x_cpu = {  # the same inputs, image 0, first qs queries
-            "mask_logits": z.detach()[:, :1, :qs].float().cpu().numpy(),
-            "mask_targets": x["mask_targets"][:1].cpu().numpy(),
-            "cls_logits": zc.detach()[:, :1, :qs].float().cpu().numpy(),
-            "cls_targets": x["cls_targets"][:1].cpu().numpy(),
-        }
         sep = mask_loss_amd.mask_loss.pairwise_mask_loss_forward(
             z.detach(), x["mask_targets"], zc.detach(), x["cls_targets"], 1.0, 1.0, 1.0, 1.0, 0,
             1.0, 0.05, 0.0, -1.0, 0.0, -1.0, True, True)
         total = ((sep[0] + sep[1]) + sep[2]).double().cpu().numpy()
-        cpu = cpu_baseline(cfg, x_cpu, p2g.cpu().numpy(), total, qs)
+        cpu = cpu_baseline(cfg, x, z, zc, p2g.cpu().numpy(), total, a.cpu_sample_images)
+
+    others = []
+    if not a.no_other_configs:
+        for oc in synth.CONFIGS:
+            if oc.name != cfg.name:
+                others.append(other_config(oc, dev, a.other_steps, a.other_warmup))
 
     out = {
         "metric": "ms per cost+match+loss fwd/bwd step (B=16,Q=200,256²); % MFMA/HBM roofline",
@@ -259,6 +303,7 @@ def main():
         "step_roofline": step_roof,
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "other_configs": others,
     }
     print(json.dumps(out), flush=True)
 

@@ -405,7 +405,7 @@ constexpr uint32_t kGSub = kGBase - 1;          // idx = sat(m - kGSub): 0 = tin
 constexpr uint32_t kGBlock = kGN + 2;           // tiny + regular + overflow slot
 constexpr uint32_t kGBytes = 2 * kGBlock * 16;  // both signs: 90176 bytes
 constexpr int kLutThreads = 1024;
-constexpr int kLutU = 2;                        // 8-cell groups per thread per item
+constexpr int kLutU = 4;                        // 8-cell groups per thread per item
 constexpr int64_t kLutChunk = (int64_t)kLutThreads * 8 * kLutU;
 
 __device__ __forceinline__ float4 grad_terms(float z, const ElemParams& ep) {

@@ -244,8 +244,9 @@ def main():
     bytes_alg = {
         "pair_cost": e * K * LBQ + 2 * cfg.B * K,        # logits once + compact labels
         "bwd_mask": e * K * 2 * M,                       # matched rows: logits read, grads written
-        "prefill": e * K * LBQ,                          # gradient buffer zero-filled
-        "assign": 4 * LBQ * Cp,                          # class logits
+        # class logits, plus the gradient buffer zero-filled by the extra
+        # workgroups of the same launch
+        "assign": 4 * LBQ * Cp + e * K * LBQ,
     }
     step_bytes = step_bytes_of(cfg, e, M)
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"])

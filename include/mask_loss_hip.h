@@ -41,6 +41,7 @@ extern "C" {
 #endif
 
 typedef struct ihipStream_t* ml_stream_t; /* == hipStream_t */
+typedef struct ihipEvent_t* ml_event_t;   /* == hipEvent_t */
 
 enum {
   ML_OK = 0,
@@ -113,18 +114,27 @@ size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p,
 /* pred_to_gt / pred_round: (L,B,Q) int64; layer_means: (3,L) float
  * [mask, dice, cls]; separate_costs: (3,L,B,Q,GT_out) float or NULL;
  * saved: ml_saved_bytes() bytes for the backward, or NULL.
- * grad_mask_prefill: NULL, or the (L,B,Q,H,W) mask_dtype buffer that will
- * receive the mask-logit gradient.  The forward then zero-fills it on a
- * library-owned side stream while the assignment runs on `stream` (the fill
- * is joined into `stream` before the forward's last kernel), and the backward
+ * grad_mask_prefill: NULL, or the (L,B,Q,H,W) mask_dtype buffer (16-byte
+ * aligned) that will receive the mask-logit gradient.  The forward then
+ * zero-fills it with extra workgroups of the assignment launch (the
+ * assignment occupies one CU per image and leaves HBM idle), and the backward
  * called with grad_prefilled = 1 writes only the matched rows.  Not allowed
- * with force_unmatched_masks_to_empty (every row has a gradient then). */
+ * with force_unmatched_masks_to_empty (every row has a gradient then).
+ * void_found: NULL, or an int32 the device can write (device memory, or
+ * pinned host memory mapped for the device): it receives 1 if any of the
+ * B*GT_total entries of cls_targets equals params.void_class_index (a valid
+ * class index), else 0 -- the reference's check of
+ * functions/mask/matching.py:184-185, done by the forward's first kernels.
+ * void_ready: NULL, or a hipEvent_t recorded on `stream` as soon as
+ * void_found is written (before the cost contraction), so that a caller can
+ * wait for the check without waiting for the whole forward. */
 int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
                              const void* mask_logits, const int64_t* mask_targets,
                              int cls_dtype, const void* cls_logits,
                              const int64_t* cls_targets, int64_t* pred_to_gt,
                              int64_t* pred_round, float* layer_means,
                              float* separate_costs, void* saved, void* grad_mask_prefill,
+                             int32_t* void_found, ml_event_t void_ready,
                              void* workspace, size_t workspace_bytes, ml_stream_t stream);
 
 /* ---- matching backward ------------------------------------------------------
@@ -207,7 +217,7 @@ int ml_dice_loss_backward(const ml_dense_shape* s, int dtype, const float* grad_
 /* ---- input validation helper ------------------------------------------------
  * flag[0] = 1 if any of x[0..n) equals `value`, else 0 (one small kernel, no
  * synchronisation).  Replaces the device-wide comparison + reduction behind
- * the reference's void-class check (functions/mask/matching.py:177-178), so
+ * the reference's void-class check (functions/mask/matching.py:184-185), so
  * the caller can read the flag asynchronously. */
 int ml_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, ml_stream_t stream);
 

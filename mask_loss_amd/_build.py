@@ -109,7 +109,7 @@ def build_ext(force=True):
         src, "-o", EXT,
         f"-L{HERE}", "-lmask_loss_hip", "-Wl,-rpath,$ORIGIN",
         f"-L{libdir}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lc10_hip",
-        "-ltorch_hip", f"-Wl,-rpath,{libdir}",
+        "-ltorch_hip", f"-Wl,-rpath,{libdir}", "-L/opt/rocm/lib", "-lamdhip64",
     ]
     _run(cmd)
     return EXT

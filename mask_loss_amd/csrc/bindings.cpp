@@ -33,6 +33,36 @@ void ml_ok(int rc) { TORCH_CHECK(rc == ML_OK, ml_last_error()); }
 
 ml_stream_t cur_stream() { return (ml_stream_t)at::hip::getCurrentHIPStream().stream(); }
 
+// The forward's void-class check writes its answer into a pinned host word
+// (mapped for the device) and records an event right after it; one word and
+// event per host thread and device, kept for the life of the process.
+struct VoidSlot {
+  volatile int32_t* host = nullptr;
+  int32_t* dev = nullptr;
+  hipEvent_t ev = nullptr;
+};
+
+VoidSlot& void_slot() {
+  constexpr int kMaxDevices = 64;
+  static thread_local VoidSlot slots[kMaxDevices];
+  int dev = 0;
+  TORCH_CHECK(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices,
+              "no current HIP device");
+  VoidSlot& v = slots[dev];
+  if (!v.host) {
+    void* h = nullptr;
+    void* d = nullptr;
+    TORCH_CHECK(hipHostMalloc(&h, 64, hipHostMallocMapped) == hipSuccess,
+                "cannot allocate the pinned void-check word");
+    TORCH_CHECK(hipHostGetDevicePointer(&d, h, 0) == hipSuccess &&
+                    hipEventCreateWithFlags(&v.ev, hipEventDisableTiming) == hipSuccess,
+                "cannot map the void-check word");
+    v.dev = (int32_t*)d;
+    v.host = (volatile int32_t*)h;
+  }
+  return v;
+}
+
 torch::Tensor workspace(size_t bytes, const torch::Tensor& like) {
   return torch::empty({(int64_t)std::max<size_t>(bytes, 256)},
                       like.options().dtype(torch::kUInt8));
@@ -144,7 +174,8 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
                                          const torch::Tensor& cls_logits,
                                          const torch::Tensor& cls_targets, const ml_params& p,
                                          bool want_saved,
-                                         const c10::optional<torch::Tensor>& grad_prefill) {
+                                         const c10::optional<torch::Tensor>& grad_prefill,
+                                         bool check_void = false) {
   ML_CHECK_INPUT(mask_logits);
   ML_CHECK_INPUT(mask_targets);
   ML_CHECK_INPUT(cls_logits);
@@ -174,17 +205,25 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
   const size_t wsb = ml_mask_matching_workspace_size(&s, &p, mdt);
   auto ws = workspace(wsb, mask_logits);
   TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, "unsupported shape for mask_matching");
+  VoidSlot* vs = check_void ? &void_slot() : nullptr;
   ml_ok(ml_mask_matching_forward(
       &s, &p, mdt, mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt,
       cls_logits.data_ptr(), cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
       pred_round.data_ptr<int64_t>(), means.data_ptr<float>(), nullptr,
-      want_saved ? saved.data_ptr() : nullptr, prefill, ws.data_ptr(), ws.numel(), cur_stream()));
+      want_saved ? saved.data_ptr() : nullptr, prefill, vs ? vs->dev : nullptr,
+      vs ? (ml_event_t)vs->ev : nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
+  int32_t void_hit = -1;
+  if (vs) {  // waits for the preparation kernels only; the rest stays queued
+    TORCH_CHECK(hipEventSynchronize(vs->ev) == hipSuccess, "void-check event failed");
+    void_hit = *vs->host;
+  }
   // means follow the logits dtype (src/cuda/mask_matching_forward.cu:580-583);
   // the fused entry keeps them in float32
   const auto out_dt = want_saved ? torch::kFloat32 : mask_logits.scalar_type();
   std::vector<torch::Tensor> r = {pred_to_gt, pred_round, means[0].to(out_dt),
                                   means[1].to(out_dt), means[2].to(out_dt)};
   if (want_saved) r.push_back(saved);
+  if (check_void) r.push_back(torch::full({1}, void_hit, torch::dtype(torch::kInt32)));
   return r;
 }
 
@@ -224,6 +263,9 @@ std::vector<torch::Tensor> mask_matching_wrapper_order(
 // statistics, matched rows, compact labels) the fused backward uses to read
 // every matched logit once.  With grad_prefill (the tensor that will receive
 // the mask-logit gradient) the forward zero-fills it beside the assignment.
+// With check_void, a seventh output (CPU int32, one element) says whether
+// cls_targets holds void_class_index (1), not (0), or no valid index was
+// given (0); the call then waits for the forward's preparation kernels.
 std::vector<torch::Tensor> mask_matching_fused(
     const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
     const torch::Tensor& cls_logits, const torch::Tensor& cls_targets, double smooth,
@@ -231,12 +273,13 @@ std::vector<torch::Tensor> mask_matching_fused(
     double ug_min, double inf_thresh, double num_masks, bool force_cls, bool force_masks,
     int64_t topk, int64_t strategy, double mask_gamma, double mask_alpha, double cls_gamma,
     double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize,
-    const c10::optional<torch::Tensor>& grad_prefill) {
+    const c10::optional<torch::Tensor>& grad_prefill, bool check_void) {
   const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
                                   ug, ug_min, inf_thresh, num_masks, force_cls, force_masks, topk,
                                   strategy, mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
                                   use_softmax, normalize);
-  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, true, grad_prefill);
+  return matching_impl(mask_logits, mask_targets, cls_logits, cls_targets, p, true, grad_prefill,
+                       check_void);
 }
 
 // --------------------------------------------------------------------------
@@ -557,7 +600,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("topk_matches"), py::arg("strategy_id"), py::arg("mask_gamma"),
         py::arg("mask_alpha"), py::arg("cls_gamma"), py::arg("cls_alpha"),
         py::arg("void_class_index"), py::arg("use_softmax_label_loss"),
-        py::arg("normalize_uncertainty"), py::arg("grad_prefill") = py::none());
+        py::arg("normalize_uncertainty"), py::arg("grad_prefill") = py::none(),
+        py::arg("check_void") = false);
   m.def("mask_matching_backward_fused", &mask_matching_backward_fused,
         "Mask matching backward using the forward's saved state (HIP)", py::arg("g_mask"),
         py::arg("g_dice"), py::arg("g_cls"), py::arg("mask_logits"), py::arg("mask_targets"),

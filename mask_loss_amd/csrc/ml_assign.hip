@@ -566,8 +566,16 @@ __device__ void layer_pass(const LayerArgs& a) {
 // INLDS: the image's cost matrix fits in LDS (else it lives in the costT
 // workspace); a compile-time choice, so cost reads are ds_read (or global)
 // rather than flat loads.
+// Workgroups L*B .. L*B + fill_blocks - 1 zero-fill the gradient buffer:
+// the assignment keeps one CU per image busy with a serial chain and leaves
+// HBM idle, so the fill runs beside it in the same launch.
 template <int NJ, bool INLDS>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
+  if ((int64_t)blockIdx.x >= a.L * a.B) {
+    zero_fill_range(a.fill, a.fill_n16, a.fill_tail, a.fill_ntail,
+                    (int64_t)blockIdx.x - a.L * a.B, a.fill_blocks);
+    return;
+  }
   extern __shared__ __align__(16) unsigned char smem[];
   const SmemLayout L = smem_layout(a.Q, a.GT_out, INLDS);
   float* contrib = (float*)(smem + L.contrib);
@@ -580,8 +588,8 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   int* hrows = (int*)(smem + L.hrows);
   int* asg = (int*)(smem + L.asg);
 
-  // A serial, latency-bound chain: take issue priority over waves of other
-  // kernels sharing the CU (the gradient prefill runs beside this kernel).
+  // A serial, latency-bound chain: take issue priority over waves of the
+  // fill workgroups should they share the CU.
   __builtin_amdgcn_s_setprio(3);
   const int64_t lb = blockIdx.x, b = lb % a.B;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -743,8 +751,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
         greedy_wave(costL, Q, preds, (int)Q, vcols, nv, cap, p2g, thr);
       }
     }
-    if (!okh) {
-      if (lane == 0) atomicOr(a.err, 1);
+    if (!okh) {  // no finite augmenting path (invalid costs are BIG): image left unmatched
       for (int64_t q = lane; q < Q; q += 64) p2g[q] = -1;
     }
     // drop invalid, rank by (cost, q) within each column (matching.cpp:533-565)
@@ -888,7 +895,8 @@ static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
   if (sm > max_dyn) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
   {
     ProfScope ps_("assign", st);
-    hipLaunchKernelGGL((assign_kernel<NJ, INLDS>), dim3((unsigned)d.LB), dim3(256), sm, st, a);
+    hipLaunchKernelGGL((assign_kernel<NJ, INLDS>), dim3((unsigned)(d.LB + a.fill_blocks)),
+                       dim3(256), sm, st, a);
   }
   return check_launch("assign");
 }

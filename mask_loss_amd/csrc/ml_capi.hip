@@ -78,35 +78,6 @@ void prof_end(const char* name, hipStream_t st) {
   }
 }
 
-// ---- side stream for the gradient prefill --------------------------------------
-// One non-blocking stream (default priority) and a fork / join event pair per
-// device, created on first use and kept for the life of the process.  The
-// mutex keeps each record -> wait pair of one call together when several host
-// threads share a device.
-namespace {
-struct Side {
-  hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-constexpr int kMaxDevices = 64;
-std::mutex g_side_mu;
-Side g_side[kMaxDevices];
-}  // namespace
-
-static int side_stream(Side** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(ML_ELAUNCH, "prefill: no current HIP device");
-  Side& sd = g_side[dev];
-  if (!sd.s) {
-    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess)
-      return fail(ML_ELAUNCH, "prefill: cannot create the side stream");
-  }
-  *out = &sd;
-  return ML_OK;
-}
 
 constexpr size_t kMaxLds = 160 * 1024;
 
@@ -192,9 +163,8 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   };
   L.lab16 = take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2);
   L.counts8 = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0);
-  // present flags and the error word are contiguous: one fill clears them
-  L.present = take((size_t)d.B * d.GT_total * 4);
-  L.err = take(16);
+  L.pbits = take((size_t)d.B * prep_blocks(d) * kPresWords * 4);
+  L.vflag = take((size_t)d.B * 4);
   L.ncols = take((size_t)d.B * 4);
   L.colmap = take((size_t)d.B * d.nslot * 4);
   L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
@@ -203,7 +173,6 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   L.sched = take((size_t)sched_ints(pl.ntasks) * 4);
   L.partials = take((size_t)pl.float_total * 4);
   L.rowsum = take(force_masks ? (size_t)pl.nclass * cap * d.rows * 2 * 4 : 0);
-  L.flags = take((size_t)pl.nclass * cap * 4);
   L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
   L.tot = take((size_t)d.LB * ceil_div(d.Q * d.GT_out, 4) * 16);
@@ -254,8 +223,9 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                         const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
                         const void* cls_logits, const int64_t* cls_targets, int64_t* pred_to_gt,
                         int64_t* pred_round, float* layer_means, float* sep, void* saved,
-                        void* prefill, void* ws, size_t ws_bytes, hipStream_t st,
-                        bool costs_only, float* bce_out = nullptr, float* dice_out = nullptr) {
+                        void* prefill, int32_t* void_found, hipEvent_t void_ready, void* ws,
+                        size_t ws_bytes, hipStream_t st, bool costs_only,
+                        float* bce_out = nullptr, float* dice_out = nullptr) {
   if (!dtype_ok(mask_dtype) || (cls_logits && !dtype_ok(cls_dtype)))
     return fail(ML_EINVAL, "unsupported dtype");
   if (!cls_logits && !costs_only) return fail(ML_EINVAL, "matching needs class logits");
@@ -283,8 +253,16 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   // with a saved state the compact labels go straight into it (the backward reuses them)
   pa.lab16 = (uint16_t*)(saved && !d.counts_mode ? sv + SL.lab16 : w + L.lab16);
   pa.counts8 = (uint8_t*)(w + L.counts8);
-  pa.present = (int*)(w + L.present);
-  pa.fill_ints = (int64_t)((L.err + 16 - L.present) / 4);
+  pa.pbits = (uint32_t*)(w + L.pbits);
+  pa.nblk = prep_blocks(d);
+  pa.vflag = (int*)(w + L.vflag);
+  const int64_t void_idx =
+      (p->void_class_index >= 0 && p->void_class_index < d.C) ? p->void_class_index : -1;
+  if (void_found) {
+    pa.cls_targets = cls_targets;
+    pa.void_idx = cls_targets ? void_idx : -1;
+    pa.void_found = void_found;
+  }
   pa.ncols = (int*)(w + L.ncols);
   pa.colmap = (int*)(w + L.colmap);
   pa.slot_of_col = (int*)(w + L.slot_of_col);
@@ -293,6 +271,9 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.sched = (int*)(w + L.sched);
   pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = plan;
   if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
+  if (void_found && d.B == 0 && (rc = launch_fill_i32(void_found, 0, 1, st))) return rc;
+  if (void_ready && hipEventRecord(void_ready, st) != hipSuccess)
+    return fail(ML_ELAUNCH, "cannot record the void-check event");
 
   const ElemParams mask_ep = make_elem_params(p->mask_gamma, p->mask_alpha,
                                               p->uncertainty_gamma, p->uncertainty_gamma_min);
@@ -306,7 +287,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   ca.plan = plan;
   ca.partials = (float*)(w + L.partials);
   ca.rowsum = force_masks ? (float*)(w + L.rowsum) : nullptr;
-  ca.flags = (int*)(w + L.flags);
   ca.L = d.L; ca.B = d.B; ca.Q = d.Q; ca.HW = d.HW; ca.HWp = d.HWp;
   ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.rows = d.rows;
   ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;
@@ -314,7 +294,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   if (d.LB > 0 && d.rtiles > 0 && (rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
 
   const bool use_softmax = p->use_softmax_label_loss != 0;
-  int64_t void_idx = (p->void_class_index >= 0 && p->void_class_index < d.C) ? p->void_class_index : -1;
   AssignArgs aa;
   aa.cls_logits = cls_logits;
   aa.cls_dtype = cls_dtype;
@@ -342,7 +321,16 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.pred_round = pred_round;
   aa.stats = stats;
   aa.img = (float*)(w + L.img);
-  aa.err = (int*)(w + L.err);
+  // the gradient's zero fill: extra workgroups of the assignment launch
+  const size_t prefill_bytes =
+      prefill ? (size_t)(d.LB * d.Q * d.HW) * (mask_dtype == ML_F32 ? 4 : 2) : 0;
+  aa.fill = (u32x4_t*)prefill;
+  aa.fill_n16 = (int64_t)(prefill_bytes / 16);
+  aa.fill_tail = (unsigned char*)prefill + prefill_bytes / 16 * 16;
+  aa.fill_ntail = (int64_t)(prefill_bytes % 16);
+  aa.fill_blocks = prefill_bytes && !costs_only
+                       ? (int)std::min<int64_t>(kFillBlocks, std::max<int64_t>(1, ceil_div(aa.fill_n16, 256)))
+                       : 0;
   aa.L = d.L; aa.B = d.B; aa.Q = d.Q; aa.C = d.C; aa.HW = d.HW; aa.Ht = d.Ht; aa.Wt = d.Wt;
   aa.GT_total = d.GT_total; aa.GT_out = d.GT_out; aa.bg = d.bg; aa.rtiles = d.rtiles;
   aa.rows = d.rows; aa.nslot = d.nslot; aa.N2 = (float)d.N2;
@@ -377,25 +365,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.cost_in_lds = in_lds;
   if (d.LB > 0 && (rc = launch_finalize(aa, d, st))) return rc;
   if (costs_only) return ML_OK;
-  // The assignment occupies one workgroup per image and leaves HBM idle: the
-  // zero fill of the gradient buffer runs beside it on the side stream.
-  const size_t prefill_bytes =
-      prefill ? (size_t)(d.LB * d.Q * d.HW) * (mask_dtype == ML_F32 ? 4 : 2) : 0;
-  Side* sd = nullptr;
-  std::unique_lock<std::mutex> side_lock(g_side_mu, std::defer_lock);
-  if (prefill_bytes) {
-    side_lock.lock();
-    if ((rc = side_stream(&sd))) return rc;
-    if (hipEventRecord(sd->fork, st) != hipSuccess ||
-        hipStreamWaitEvent(sd->s, sd->fork, 0) != hipSuccess)
-      return fail(ML_ELAUNCH, "prefill: fork failed");
-    {
-      ProfScope ps_("prefill", sd->s);
-      if ((rc = launch_zero_fill(prefill, prefill_bytes, sd->s))) return rc;
-    }
-    if (hipEventRecord(sd->join, sd->s) != hipSuccess)
-      return fail(ML_ELAUNCH, "prefill: join record failed");
-  }
   // per-layer means and the matched-row list, after the assignment
   LayerArgs la;
   la.img = aa.img;
@@ -408,13 +377,12 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   la.force_masks = force_masks;
   la.force_cls = p->force_unmatched_class_to_background;
   la.has_void = void_idx >= 0;
-  rc = d.LB > 0 ? launch_assign(aa, d, st) : ML_OK;
-  if (prefill_bytes) {  // join even after a failed launch: the buffer is the caller's
-    if (hipStreamWaitEvent(st, sd->join, 0) != hipSuccess && rc == ML_OK)
-      rc = fail(ML_ELAUNCH, "prefill: join failed");
-    side_lock.unlock();
+  if (d.LB > 0) {
+    if ((rc = launch_assign(aa, d, st))) return rc;
+  } else if (prefill_bytes) {
+    ProfScope ps_("prefill", st);
+    if ((rc = launch_zero_fill(prefill, prefill_bytes, st))) return rc;
   }
-  if (rc) return rc;
   if (d.L > 0 && (rc = launch_layer(la, st))) return rc;
   return ML_OK;
 }
@@ -501,12 +469,14 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
                              const void* cls_logits, const int64_t* cls_targets,
                              int64_t* pred_to_gt, int64_t* pred_round, float* layer_means,
                              float* separate_costs, void* saved, void* grad_mask_prefill,
-                             void* workspace, size_t workspace_bytes, ml_stream_t stream) {
+                             int32_t* void_found, ml_event_t void_ready, void* workspace,
+                             size_t workspace_bytes, ml_stream_t stream) {
   int rc = check_params(p, s->C, true);
   if (rc) return rc;
   return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
                       cls_targets, pred_to_gt, pred_round, layer_means, separate_costs, saved,
-                      grad_mask_prefill, workspace, workspace_bytes, (hipStream_t)stream, false);
+                      grad_mask_prefill, void_found, (hipEvent_t)void_ready, workspace,
+                      workspace_bytes, (hipStream_t)stream, false);
 }
 
 int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
@@ -518,7 +488,7 @@ int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mas
   if (rc) return rc;
   return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
                       cls_targets, nullptr, nullptr, nullptr, separate_costs, nullptr, nullptr,
-                      workspace, workspace_bytes, (hipStream_t)stream, true);
+                      nullptr, nullptr, workspace, workspace_bytes, (hipStream_t)stream, true);
 }
 
 int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int dtype,
@@ -532,8 +502,8 @@ int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int 
   if (!(p->uncertainty_gamma_min >= 0.f && p->uncertainty_gamma_min <= 1.f))
     return fail(ML_EINVAL, "uncertainty_gamma_min must be in [0, 1]");
   return forward_impl(s, p, dtype, logits, targets, ML_F32, nullptr, nullptr, nullptr, nullptr,
-                      nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes,
-                      (hipStream_t)stream, true, bce_out, dice_out);
+                      nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, workspace,
+                      workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out);
 }
 
 size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,
@@ -582,7 +552,7 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   PrepArgs pa;
   pa.lab16 = (uint16_t*)(w + take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
   pa.counts8 = (uint8_t*)(w + take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
-  pa.present = nullptr;  // labels only
+  pa.pbits = nullptr;  // labels only
   pa.ncols = (int*)(w + take((size_t)d.B * 4));
   pa.colmap = (int*)(w + take((size_t)d.B * d.nslot * 4));
   pa.slot_of_col = (int*)(w + take((size_t)d.B * d.GT_out * 4));
@@ -692,7 +662,7 @@ int dense_prep(const DensePlan& P, const int64_t* targets, unsigned char* w, Den
   pa.targets = targets;
   pa.lab16 = d.counts_mode ? nullptr : (uint16_t*)w;
   pa.counts8 = d.counts_mode ? (uint8_t*)w : nullptr;
-  pa.present = nullptr;
+  pa.pbits = nullptr;
   pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
   pa.GT_total = d.C; pa.GT_out = d.C; pa.bg = d.C;
   a.lab16 = pa.lab16;

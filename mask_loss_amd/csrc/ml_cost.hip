@@ -24,8 +24,9 @@
 // planes are read from a per-workgroup LDS table built with the same float32
 // formulas (|z| in [2^-16, 64): one entry per bf16 value; |z| < 2^-16: the
 // z = 0 entry; |z| >= 64, inf and nan read a NaN marker, and a wave whose
-// sums come out NaN is redone with the formulas by a fix-up launch).  Other dtypes evaluate the formulas directly and split each
-// plane into NS bf16 terms so products keep float32 accuracy.
+// sums come out NaN redoes its K-range with the formulas).  Other dtypes
+// evaluate the formulas directly and split each plane into NS bf16 terms so
+// products keep float32 accuracy.
 #include <algorithm>
 #include <atomic>
 
@@ -233,12 +234,11 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
 // One wave's work: 16*RT query rows of task (lb, rtile) over the K-steps of
 // split ks of KS; writes the partial sums to `out` ([3][16*RT][16*NT]) and,
 // for unweighted penalties, the row sums to `rs` ([16*RT][2]).  TAB:
-// per-cell planes from the LDS table (bf16 only); returns true if the sums
-// came out NaN, i.e. some cell hit the table's overflow marker, in which case
-// the partial sums written are unusable and the wave is redone with
-// TAB = false.
+// per-cell planes from the LDS table (bf16 only); if the sums come out NaN,
+// some cell of the K-range hit the table's overflow marker, and the wave
+// redoes the range with the formulas before writing.
 template <int DT, int RT, int NT, bool CNT, bool TAB>
-__device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
+__device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
                                           int64_t ks, int64_t KS, const unsigned char* lut,
                                           float* out, float* rs_out) {
   constexpr int NS = InTraits<DT>::kSplit;
@@ -424,6 +424,29 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
 #pragma unroll
         for (int e = 0; e < 4; ++e) bad |= __builtin_isnan(acc[2][rt][nt][e]);
     bad = __ballot(bad) != 0;
+    if (bad) {  // |z| >= 64, inf or nan somewhere in the range: formulas, one step at a time
+#pragma unroll
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) acc[i][rt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int64_t st = s0; st < s1; ++st) {
+        bf16x8_t A[4][RT][NS];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          Raw8<DT> raw;
+          load_raw8<DT>(a.logits, rowoff[rt] + st * kStep, raw, vec);
+          bf16x8_t T[4][NS];
+          planes8_formula<DT, NS, false>(raw, ep, 8, false, T, ub[rt], up[rt]);
+#pragma unroll
+          for (int pl = 0; pl < 4; ++pl)
+#pragma unroll
+            for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
+        }
+        mma_step(A, *(const uint4*)(labp + st * kStep), st * kStep + g4 * 8);
+      }
+    }
   }
 
   if (has_tail) {  // last partial step: guarded loads, masked planes
@@ -490,7 +513,6 @@ __device__ __forceinline__ bool cost_wave(const CostArgs& a, int64_t lb, int64_t
       }
     }
   }
-  return bad;
 }
 
 template <int NT>
@@ -522,47 +544,7 @@ __global__ __launch_bounds__(64 * cost_waves(NT)) void cost_kernel(CostArgs a) {
   constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
   float* out = a.partials + a.plan.float_base[CI] + w * tile;
   float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + w) * (16 * RT) * 2 : nullptr;
-  const bool bad = cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs);
-  if constexpr (TAB) {
-    if ((threadIdx.x & 63) == 0) a.flags[a.plan.slot_base[CI] + w] = bad ? 1 : 0;
-  }
-}
-
-// Formula-path wave as a real call, so that the fix-up kernel's register
-// allocation is one instantiation's, not the sum of all of them.
-template <int RT, int NT>
-__device__ __noinline__ void cost_wave_formula(const CostArgs& a, int64_t w) {
-  constexpr int CI = kClassOf<NT>;
-  const int64_t KS = __builtin_amdgcn_readfirstlane(a.sched[kClasses + CI]);
-  const int64_t i = w / KS, ks = w % KS;
-  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
-  const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
-  constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
-  cost_wave<ML_BF16, RT, NT, false, false>(a, lb, rtile, ks, KS, nullptr,
-                                           a.partials + a.plan.float_base[CI] + w * tile, nullptr);
-}
-
-// Redo, with the formulas, every work item of the bf16 table path whose flag
-// is set (a cell with |z| >= 64, inf or nan in its K-range).  Grid-stride
-// over the items of every class; a flag read is the only work for clean ones.
-template <int RT>
-__global__ __launch_bounds__(64 * kWavesCost) void cost_fix_kernel(CostArgs a) {
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t step = (int64_t)gridDim.x * kWavesCost;
-#pragma unroll
-  for (int ci = 0; ci < kClasses; ++ci) {
-    if (ci >= a.plan.nclass) break;
-    const int64_t total = (int64_t)a.sched[ci] * a.sched[kClasses + ci];
-    const int64_t sb = ci == 0 ? a.plan.slot_base[0] : ci == 1 ? a.plan.slot_base[1]
-                     : ci == 2 ? a.plan.slot_base[2] : a.plan.slot_base[3];
-    for (int64_t w = (int64_t)blockIdx.x * kWavesCost + wave; w < total; w += step) {
-      if (!__builtin_amdgcn_readfirstlane(a.flags[sb + w])) continue;
-      if (ci == 0) cost_wave_formula<RT, 2>(a, w);
-      else if (ci == 1) cost_wave_formula<RT, 4>(a, w);
-      else if (ci == 2) cost_wave_formula<RT, 7>(a, w);
-      else if constexpr (RT == 1) cost_wave_formula<1, 16>(a, w);
-    }
-  }
+  cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs);
 }
 
 // ---- launch plan ---------------------------------------------------------------
@@ -646,10 +628,6 @@ static int launch_classes(const CostArgs& a, const Dims& d, bool tab, hipStream_
   if (!rc && a.plan.nclass > 2) rc = launch_one<DT, RT, 7>(a, d, tab, st);
   if constexpr (RT == 1) {
     if (!rc && a.plan.nclass > 3) rc = launch_one<DT, 1, 16>(a, d, tab, st);
-  }
-  if (!rc && tab) {
-    hipLaunchKernelGGL((cost_fix_kernel<RT>), dim3(256), dim3(64 * kWavesCost), 0, st, a);
-    rc = check_launch("pair_cost_fix");
   }
   return rc;
 }

@@ -24,7 +24,14 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 constexpr int kStep = 32;        // cells per MFMA K-step (16x16x32)
-constexpr int kWavesCost = 4;    // waves per workgroup of the cost fix-up kernel
+// Presence bits per image: make_dims admits at most 255 GT columns, so the
+// forward's GT labels are < 256.
+constexpr int kPresWords = 8;
+constexpr int kPresLabels = 32 * kPresWords;
+// Workgroups of 256 threads that zero-fill the gradient buffer beside the
+// assignment (measured on MI355X: 64 still write at the full rate while
+// leaving the other CUs to the latency-bound assignment).
+constexpr int kFillBlocks = 64;
 
 // Column-tile classes of the cost contraction: an image with G non-empty GT
 // columns (+ the ones column) is handled by the kernel instance whose tile
@@ -47,7 +54,7 @@ constexpr int64_t kCostSlots = 4096;
 // clamp(slots / n_c, 1, ks_max) for its n_c (image, row-tile) tasks, and wave
 // w of the class takes task w / KS_c, split w % KS_c (grid-stride beyond).
 // Work item w of class c owns partial tile float_base[c] + w * tile(c) and
-// global slot slot_base[c] + w (flags, unweighted row sums).
+// global slot slot_base[c] + w (unweighted row sums).
 struct CostPlan {
   int nclass;                    // classes with class_nt(c) <= padded NT
   int slots[kClasses];
@@ -125,8 +132,8 @@ inline SavedLayout saved_layout(const Dims& d) {
 
 // Byte offsets inside the caller's workspace.
 struct Layout {
-  size_t lab16, counts8, present, ncols, colmap, slot_of_col, sched, partials, rowsum, flags,
-      costT, sep, tot, rowIT, rowstat, img, layer, err, total;
+  size_t lab16, counts8, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
+      costT, sep, tot, rowIT, rowstat, img, layer, total;
 };
 Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
 // Plan slots / offsets of the cost launches (queries kernel occupancy on the
@@ -139,8 +146,18 @@ struct PrepArgs {
   const int64_t* targets;
   uint16_t* lab16;
   uint8_t* counts8;
-  int* present;          // [B][GT_total]: 1 iff the GT has pixels (forward only, else null)
-  int64_t fill_ints;     // ints cleared from `present` on (flags, error word)
+  // forward only (else null): per preparation workgroup, kPresWords words of
+  // presence bits of its GT labels, [B][nblk][kPresWords]; every word is
+  // rewritten on each call, so nothing needs clearing first
+  uint32_t* pbits = nullptr;
+  int nblk = 0;          // preparation workgroups per image (prep_blocks)
+  // void-class check (reference functions/mask/matching.py:184-185): the
+  // first workgroup of image b writes vflag[b] = any(cls_targets[b][:] == void_idx);
+  // the column pass ORs them into *void_found (device or host-mapped memory)
+  const int64_t* cls_targets = nullptr;
+  int64_t void_idx = -1;  // -1: no check
+  int* vflag = nullptr;
+  int32_t* void_found = nullptr;
   int* ncols;
   int* colmap;
   int* slot_of_col;
@@ -160,7 +177,6 @@ struct CostArgs {
   const int* sched;  // device schedule (see CostPlan)
   float* partials;   // per work item: [3][rows][16 * NT_class]
   float* rowsum;     // per work item: [rows][2] unweighted (force_masks) or null
-  int* flags;        // per work item: table-overflow flag (bf16 table path)
   CostPlan plan;
   int64_t L, B, Q, HW, HWp, rtiles, GT_total, bg, rows;
   int nslot;
@@ -204,7 +220,13 @@ struct AssignArgs {
   float* stats;          // (L,B,Q,ML_STATS) or null
   float* rowstat;        // [LB*Q][8]: S, P, mask pen, dice pen, cls pen
   float* img;            // [LB][4]: mask, dice, cls sums, matched count
-  int* err;
+  // gradient zero-fill done by extra workgroups of the assignment launch
+  // (blockIdx.x >= L*B), or fill_blocks == 0
+  u32x4_t* fill;
+  int64_t fill_n16;
+  unsigned char* fill_tail;
+  int64_t fill_ntail;
+  int fill_blocks;
   // dims / params
   int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, rtiles;
   int rows, nslot;
@@ -295,9 +317,29 @@ int launch_label_cost(const void* cls_logits, int cls_dtype, const int64_t* cls_
                       int64_t GT_out, int64_t bg, float scale, const ElemParams& ep,
                       int use_softmax, float* out, hipStream_t st);
 int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st);
+int prep_blocks(const Dims& d);
 int launch_dense(const DenseArgs& a, bool dice, bool backward, hipStream_t st);
 size_t dense_partials_bytes(int64_t L, int64_t B, int64_t C, int64_t HW, bool dice);
 int launch_zero_fill(void* p, size_t bytes, hipStream_t st);
+
+// Zero `n16` 16-byte words, then `ntail` trailing bytes, as workgroup `blk`
+// of `nblk` (256 threads each).  Streaming (non-temporal) stores: the buffer
+// is a gradient that is not read again before the backward, so it should not
+// displace the forward's working set from the L2.
+__device__ inline void zero_fill_range(u32x4_t* p, int64_t n16, unsigned char* tail,
+                                       int64_t ntail, int64_t blk, int64_t nblk) {
+  const int64_t stride = nblk * 256;
+  int64_t i = blk * 256 + threadIdx.x;
+  const u32x4_t z = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    __builtin_nontemporal_store(z, p + i);
+    __builtin_nontemporal_store(z, p + i + stride);
+    __builtin_nontemporal_store(z, p + i + 2 * stride);
+    __builtin_nontemporal_store(z, p + i + 3 * stride);
+  }
+  for (; i < n16; i += stride) __builtin_nontemporal_store(z, p + i);
+  if (blk == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
 int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, hipStream_t st);
 
 }  // namespace ml

@@ -27,30 +27,10 @@ int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st) {
   return check_launch("fill");
 }
 
-// Zero `n16` 16-byte words, then `ntail` trailing bytes.  Streaming
-// (non-temporal) stores: the buffer is a gradient that is not read again
-// before the backward, so it should not displace the forward's working set
-// from the L2.
 __global__ __launch_bounds__(256) void zero_fill_kernel(u32x4_t* p, int64_t n16,
                                                         unsigned char* tail, int64_t ntail) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const u32x4_t z = {0u, 0u, 0u, 0u};
-  for (; i + 3 * stride < n16; i += 4 * stride) {
-    __builtin_nontemporal_store(z, p + i);
-    __builtin_nontemporal_store(z, p + i + stride);
-    __builtin_nontemporal_store(z, p + i + 2 * stride);
-    __builtin_nontemporal_store(z, p + i + 3 * stride);
-  }
-  for (; i < n16; i += stride) __builtin_nontemporal_store(z, p + i);
-  if (blockIdx.x == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+  zero_fill_range(p, n16, tail, ntail, blockIdx.x, gridDim.x);
 }
-
-// 64 workgroups of 4 waves.  Measured on MI355X beside the assignment kernel
-// (375 MB): 64 workgroups still write at the full rate (72 us; 32 take 104 us)
-// while touching only a quarter of the CUs, so the latency-bound assignment
-// is slowed least (85 us vs. 77 us alone; 119 us beside 1024 workgroups).
-constexpr int64_t kFillBlocks = 64;
 
 int launch_zero_fill(void* p, size_t bytes, hipStream_t st) {
   if (bytes == 0) return ML_OK;
@@ -77,15 +57,30 @@ int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, 
   return check_launch("any_equal");
 }
 
-constexpr int kMarkMax = 8192;  // GT slots marked in LDS; more -> direct global marks
+// Presence marks of one preparation workgroup: a label bit set in LDS (lanes
+// of a wave that agree with lane 0 skip the atomic: most cells of a wave carry
+// one label); at the end the workgroup writes all kPresWords words of its
+// record, so the record never needs clearing.
+__device__ __forceinline__ void pres_clear(uint32_t* pres) {
+  if (threadIdx.x < kPresWords) pres[threadIdx.x] = 0u;
+}
+__device__ __forceinline__ void pres_mark(uint32_t* pres, int64_t lab) {
+  atomicOr(&pres[lab >> 5], 1u << (lab & 31));
+}
+__device__ __forceinline__ void pres_store(const PrepArgs& a, const uint32_t* pres, int64_t b) {
+  if (threadIdx.x < kPresWords)
+    a.pbits[(b * a.nblk + blockIdx.x) * kPresWords + threadIdx.x] = pres[threadIdx.x];
+}
 
-// Mark label `lab` present: an LDS byte, or the global flag when the GT count
-// exceeds the LDS table.  Lanes of a wave that agree with lane 0 skip the
-// store (most cells of a wave carry one label).
-__device__ __forceinline__ void mark_present(unsigned char* pres, int* present, int64_t lab,
-                                             bool lds) {
-  if (lds) pres[lab] = 1;
-  else present[lab] = 1;
+// The void check of image b's class targets (first preparation workgroup of
+// the image; every flag rewritten on each call).
+__device__ __forceinline__ void void_check(const PrepArgs& a, int64_t b) {
+  if (a.void_idx < 0 || blockIdx.x != 0) return;
+  int hit = 0;
+  for (int64_t i = threadIdx.x; i < a.GT_total; i += blockDim.x)
+    hit |= a.cls_targets[b * a.GT_total + i] == a.void_idx;
+  hit = __syncthreads_or(hit);
+  if (threadIdx.x == 0) a.vflag[b] = hit ? 1 : 0;
 }
 
 // Compacted list of the columns whose GT is non-empty, one wave per image
@@ -97,15 +92,31 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const uint64_t below = (1ull << lane) - 1ull;
+  if (a.void_found && wave == nw - 1) {  // no valid void index: 0
+    int hit = 0;
+    if (a.void_idx >= 0)
+      for (int64_t b = lane; b < a.B; b += 64) hit |= a.vflag[b];
+    hit = __any(hit);
+    if (lane == 0) *a.void_found = hit ? 1 : 0;
+  }
   for (int64_t b = wave; b < a.B; b += nw) {
+    // presence word j = OR over the image's preparation workgroups: lane
+    // (k0, j) with j = lane & 7 ORs workgroups k0, k0 + 8, ..., then the
+    // eight k0 lanes of each word combine
+    const int j = lane & (kPresWords - 1);
+    uint32_t pw = 0u;
+    const uint32_t* rec = a.pbits + b * a.nblk * kPresWords + j;
+    for (int64_t k = lane >> 3; k < a.nblk; k += 8) pw |= rec[k * kPresWords];
+    pw |= __shfl_xor(pw, 8, 64);
+    pw |= __shfl_xor(pw, 16, 64);
+    pw |= __shfl_xor(pw, 32, 64);
     int base = 0;
     for (int64_t c0 = 0; c0 < a.GT_out; c0 += 64) {
       const int64_t c = c0 + lane;
-      bool ok = false;
-      if (c < a.GT_out) {
-        const int64_t act = c + (c >= a.bg ? 1 : 0);
-        ok = a.present[b * a.GT_total + act] != 0;
-      }
+      const int64_t act = c + (c >= a.bg ? 1 : 0);
+      // lanes 0..7 hold words 0..7; every lane takes part in the shuffle
+      const uint32_t word = __shfl(pw, (int)((act >> 5) & (kPresWords - 1)), 64);
+      const bool ok = c < a.GT_out && ((word >> (act & 31)) & 1u);
       const uint64_t m = __ballot(ok);
       const int slot = base + __popcll(m & below);
       if (c < a.GT_out) {
@@ -154,16 +165,15 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
   }
 }
 
-// s == 1: each thread converts 8 consecutive cells.  grid (ceil(HWp/2048), B)
+// s == 1: each thread converts 8 consecutive cells.  grid (nblk, B)
 __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
-  __shared__ unsigned char pres[kMarkMax];
+  __shared__ uint32_t pres[kPresWords];
   const int64_t b = blockIdx.y;
   const int64_t HW = a.H * a.W;
-  const bool mark = a.present != nullptr;
-  const bool lds = a.GT_total <= kMarkMax;
-  int* present = mark ? a.present + b * a.GT_total : nullptr;
-  if (mark && lds) {
-    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) pres[i] = 0;
+  const bool mark = a.pbits != nullptr;
+  if (mark) {
+    pres_clear(pres);
+    void_check(a, b);  // ends with a barrier
     __syncthreads();
   }
   const int64_t cell0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
@@ -191,28 +201,27 @@ __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
       if (k & 1) wv[k >> 1] |= v << 16;
       else wv[k >> 1] = v;
       if (mark && valid && lab[k] != prev && !(k == 0 && lab[0] == lane0 && (threadIdx.x & 63) != 0))
-        mark_present(pres, present, lab[k], lds);
+        pres_mark(pres, lab[k]);
       prev = lab[k];
     }
     *(uint4*)(a.lab16 + b * a.HWp + cell0) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
   }
-  if (mark && lds) {
+  if (mark) {
     __syncthreads();
-    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x)
-      if (pres[i]) present[i] = 1;
+    pres_store(a, pres, b);
   }
 }
 
 // s > 1: one thread per low-res cell, counts[b][lab][cell] (single writer).
+// grid (nblk, B)
 __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
-  __shared__ unsigned char pres[kMarkMax];
+  __shared__ uint32_t pres[kPresWords];
   const int64_t b = blockIdx.y;
   const int64_t HW = a.H * a.W;
-  const bool mark = a.present != nullptr;
-  const bool lds = a.GT_total <= kMarkMax;
-  int* present = mark ? a.present + b * a.GT_total : nullptr;
-  if (mark && lds) {
-    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x) pres[i] = 0;
+  const bool mark = a.pbits != nullptr;
+  if (mark) {
+    pres_clear(pres);
+    void_check(a, b);  // ends with a barrier
     __syncthreads();
   }
   const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -226,38 +235,41 @@ __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
         if ((uint64_t)lab < (uint64_t)a.GT_total) {
           uint8_t* c = a.counts8 + (b * a.GT_total + lab) * a.HWp + cell;
           *c = (uint8_t)(*c + 1);
-          if (mark && lab != prev) mark_present(pres, present, lab, lds);
+          if (mark && lab != prev) pres_mark(pres, lab);
         }
         prev = lab;
       }
     }
   }
-  if (mark && lds) {
+  if (mark) {
     __syncthreads();
-    for (int i = threadIdx.x; i < a.GT_total; i += blockDim.x)
-      if (pres[i]) present[i] = 1;
+    pres_store(a, pres, b);
   }
 }
 
-// One workgroup: runs once every presence mark of the preparation grid is in.
+// One workgroup: runs once every presence record of the preparation grid is in.
 __global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) { columns_and_schedule(a); }
+
+// Preparation workgroups per image (the presence records' count).
+int prep_blocks(const Dims& d) {
+  return (int)(d.counts_mode ? ceil_div(d.HW, 256) : ceil_div(d.HWp, 256 * 8));
+}
 
 int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   ProfScope ps_("prep", st);
   int rc;
-  // presence flags, error word and grid tickets in one fill
-  if (a.present && (rc = launch_fill_i32(a.present, 0, a.fill_ints, st))) return rc;
+  if (a.pbits && (a.GT_total > kPresLabels || a.nblk != prep_blocks(d)))
+    return fail(ML_EINVAL, "internal: presence records do not fit the preparation grid");
+  const dim3 grid((unsigned)prep_blocks(d), (unsigned)d.B);
   if (!d.counts_mode) {
-    const dim3 grid((unsigned)ceil_div(d.HWp, 256 * 8), (unsigned)d.B);
     hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);
   } else {
     rc = launch_fill_i32((int*)a.counts8, 0, d.B * d.GT_total * d.HWp / 4, st);
     if (rc) return rc;
-    const dim3 grid((unsigned)ceil_div(d.HW, 256), (unsigned)d.B);
     hipLaunchKernelGGL(prep_counts_kernel, grid, dim3(256), 0, st, a);
   }
   if ((rc = check_launch("prep"))) return rc;
-  if (a.present) {
+  if (a.pbits) {
     hipLaunchKernelGGL(prep_columns_kernel, dim3(1), dim3(1024), 0, st, a);
     if ((rc = check_launch("prep_columns"))) return rc;
   }

@@ -92,15 +92,6 @@ class MaskMatchingFunction(Function):
             void = int(void_class_index)
             if not (0 <= void < C):
                 raise ValueError("incorrect void index")
-        # The void-class check (reference: a synchronous torch.any before any
-        # work) is started here and read at the end of forward: its flag
-        # travels to pinned host memory while the forward's kernels are
-        # queued, so the host never drains the GPU before launching them.
-        void_flag = None
-        if void != -1:
-            void_flag = mask_loss.any_equal(cls_targets, void).to("cpu", non_blocking=True)
-            void_ready = torch.cuda.Event()
-            void_ready.record()
         use_softmax = label_kind(label_loss)
         if use_softmax and force_cls and void == -1:
             raise ValueError("void_class_index must be provided when using softmax label loss "
@@ -110,10 +101,16 @@ class MaskMatchingFunction(Function):
         prefill = None
         if ctx.needs_input_grad[0] and not force_masks:
             prefill = torch.empty_like(mask_logits, memory_format=torch.contiguous_format)
-        pred_to_gt, pred_round, m, d, c, saved = mask_loss.mask_matching_fused(
+        # The void-class check (reference: a synchronous torch.any before any
+        # work) runs in the forward's first kernels; the call returns once
+        # they are done, with the rest of the forward still queued, so the
+        # host never drains the GPU before launching it.
+        check = void != -1
+        outs = mask_loss.mask_matching_fused(
             mask_logits, mask_targets, cls_logits, cls_targets, *args, inf_thresh_val,
             num_masks_val, force_cls, force_masks, K_val, STRATEGIES[strategy], mg, ma, cg, ca,
-            void, use_softmax, normalize, prefill)
+            void, use_softmax, normalize, prefill, check)
+        pred_to_gt, pred_round, m, d, c, saved = outs[:6]
         ctx.save_for_backward(mask_logits.detach(), mask_targets.detach(), cls_logits.detach(),
                               cls_targets.detach(), pred_to_gt.detach(), saved)
         # the zero-filled gradient buffer serves the first backward only (a
@@ -122,10 +119,8 @@ class MaskMatchingFunction(Function):
         ctx.bwd_args = (smooth_val, sigmoid_scale_val, dice_scale_val, cls_scale_val, bg, ug, ugm,
                         num_masks_val, force_cls, force_masks, mg, ma, cg, ca, void, use_softmax,
                         normalize)
-        if void_flag is not None:
-            void_ready.synchronize()
-            if int(void_flag[0]):
-                raise ValueError("cls_targets must not contain the void class index")
+        if check and int(outs[6][0]) == 1:
+            raise ValueError("cls_targets must not contain the void class index")
         ctx.mark_non_differentiable(pred_to_gt, pred_round)
         # no zero gradients for the integer outputs (or unused means)
         ctx.set_materialize_grads(False)

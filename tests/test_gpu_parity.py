@@ -151,13 +151,13 @@ def test_label_cost_ops(ml, softmax):
     close(got, ref, 1e-5, 1e-2)
 
 
-def matching_call(ml, x, P, M, prefill=None):
+def matching_call(ml, x, P, M, prefill=None, check_void=False):
     ss, ds, cs = P["scales"]
     return ml.mask_matching_fused(
         x["z"], x["tgt"], x["zc"], x["ct"], P["smooth"], ss, ds, cs, P["bg"], P["ug"], P["ug_min"],
         M["inf_thresh"], M["num_masks"], M["force_cls"], M["force_masks"], M["K"], M["strategy"],
         P["mask_gamma"], P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["void"],
-        P["use_softmax"], P["normalize"], prefill)
+        P["use_softmax"], P["normalize"], prefill, check_void)
 
 
 MATCH_CASES = [
@@ -315,6 +315,41 @@ def test_function_double_backward_fresh_buffer(ml):
     assert torch.equal(g1, first)
     close(g2.float().cpu().numpy(), 2.0 * first.float().cpu().numpy(), 1e-2,
           1e-2 * first.float().abs().max().item())
+
+
+@pytest.mark.parametrize("where", ["absent", "first_image", "last_image_padding"])
+def test_void_class_check(ml, where):
+    """The reference raises ValueError when cls_targets holds the void index
+    (functions/mask/matching.py:184-185).  Here the forward's preparation
+    kernels make that check and the fused binding returns it as a seventh
+    output; MaskMatchingFunction raises on it.  The forward's results do not
+    depend on the check."""
+    from mask_loss_amd.functions import MaskMatchingFunction
+    x = make_case(46, B=3, Q=24, G=5)  # classes drawn from [0, 8): void 8 absent
+    ct = x["ct"].clone()
+    if where == "first_image":
+        ct[0, 1] = 8
+    elif where == "last_image_padding":
+        ct[2, -1] = 8
+    x = dict(x, ct=ct)
+    P, M = params(dict(use_softmax=True)), mparams(dict(force_cls=True, void=8))
+    outs = matching_call(ml, x, P, M, check_void=True)
+    assert len(outs) == 7 and outs[6].device.type == "cpu"
+    assert outs[6].tolist() == [0 if where == "absent" else 1]
+    plain = matching_call(ml, x, P, M)
+    assert len(plain) == 6
+    for u, v in zip(outs[:5], plain[:5]):
+        assert torch.equal(u, v)
+    # no valid void index: the check reports 0
+    none = matching_call(ml, x, params({}), mparams(dict(void=-1)), check_void=True)
+    assert none[6].tolist() == [0]
+    args = (x["z"], x["tgt"], x["zc"], ct, 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, True, 1e30, -1.0,
+            True, False, 1, "global", 0.0, None, 0.0, None, 8, "softmax")
+    if where == "absent":
+        MaskMatchingFunction.apply(*args)
+    else:
+        with pytest.raises(ValueError, match="void class index"):
+            MaskMatchingFunction.apply(*args)
 
 
 def test_reference_wrapper_argument_order(ml):

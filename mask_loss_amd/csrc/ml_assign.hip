@@ -17,6 +17,8 @@
 //   4. pred_round ranking by (cost, query) (src/cpu/matching.cpp:533-565),
 //      per-image matched-loss sums (src/cuda/mask_matching_forward.cu:63-71)
 //      and per-query statistics for the fused backward.
+#include <type_traits>
+
 #include "ml_internal.h"
 
 namespace ml {
@@ -120,6 +122,7 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
 }
 
 __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
+  if (blockIdx.x == 0 && threadIdx.x == 0 && a.gate) *a.gate = 0;  // the assignment's fill gate
   __shared__ float sl[4][3][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -239,7 +242,9 @@ __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
     if (a.out_bce) a.out_bce[o] = bce;
     if (a.out_dice) a.out_dice[o] = dice;
     if (labels) a.sep[2 * term + o] = cls;
-    if (a.tot) a.tot[lb * a.tot_stride + q * GTo + c] = (bce + dice) + cls;  // matching.cpp:665
+    // total cost, matching.cpp:665, stored [column][query]: the assignment
+    // reads cost rows of one GT across all queries
+    if (a.tot) a.tot[lb * a.tot_stride + c * a.Q + q] = (bce + dice) + cls;
   }
   if (lane == 0 && a.rowstat) {
     float mp = 0.f, dp = 0.f;
@@ -563,15 +568,72 @@ __device__ void layer_pass(const LayerArgs& a) {
   if (threadIdx.x == 0) a.list[0] = base;
 }
 
-// INLDS: the image's cost matrix fits in LDS (else it lives in the costT
-// workspace); a compile-time choice, so cost reads are ds_read (or global)
-// rather than flat loads.
+// INLDS: the image's cost matrix fits in LDS (else it is read in place from
+// finalize's total-cost plane); a compile-time choice, so cost reads are
+// ds_read (or global) rather than flat loads.
 // Workgroups L*B .. L*B + fill_blocks - 1 zero-fill the gradient buffer:
 // the assignment keeps one CU per image busy with a serial chain and leaves
 // HBM idle, so the fill runs beside it in the same launch.
+constexpr uint64_t kGateTicks = 3000;  // 30 us of the 100 MHz real-time counter
+
+// Copy the cost rows of image b's non-empty GT columns (colmap order) from
+// finalize's plane into LDS (INLDS) and mark the valid ones (a cost that is
+// finite and below the threshold, cost_ok).  One wave per row, V floats per
+// load (V = 4 when rows start on 16-byte boundaries), R rows per wave in
+// flight; Q <= 64 * NJ, so a lane holds at most KW words of a row.
+template <int V, int NJ, bool INLDS>
+__device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int64_t b,
+                                           float* costL, int* colok) {
+  typedef typename std::conditional<V == 4, float4, float>::type word_t;
+  constexpr int KW = V == 4 ? (NJ + 3) / 4 : NJ;
+  constexpr int R = KW == 1 ? 8 : KW == 2 ? 4 : 2;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int G = __builtin_amdgcn_readfirstlane(a.ncols[b]);
+  const int* cm = a.colmap + b * a.nslot;
+  const int W = (int)(a.Q / V);  // words per row
+  const word_t* src = (const word_t*)(a.tot + lb * a.tot_stride);
+  for (int s0 = wave * R; s0 < G; s0 += 4 * R) {
+    word_t v[R][KW];
+    int col[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      col[r] = s0 + r < G ? cm[s0 + r] : -1;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        const int j = lane + 64 * k;
+        if (col[r] >= 0 && j < W) v[r][k] = src[(int64_t)col[r] * W + j];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (col[r] < 0) continue;  // wave-uniform
+      bool ok = false;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        const int j = lane + 64 * k;
+        if (j >= W) continue;
+        if constexpr (INLDS) ((word_t*)costL)[(int64_t)col[r] * W + j] = v[r][k];
+        const float* e = (const float*)&v[r][k];
+#pragma unroll
+        for (int h = 0; h < V; ++h) ok |= cost_ok((double)e[h], a.inf_thresh);
+      }
+      if (__ballot(ok) != 0ull && lane == 0) colok[col[r]] = 1;
+    }
+  }
+}
+
 template <int NJ, bool INLDS>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   if ((int64_t)blockIdx.x >= a.L * a.B) {
+    // Start once every image's cost matrix is staged (the fill's writes would
+    // otherwise stretch those reads several times), or after kGateTicks.
+    if (threadIdx.x == 0) {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      while (__hip_atomic_load(a.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.L * a.B &&
+             __builtin_amdgcn_s_memrealtime() - t0 < kGateTicks)
+        __builtin_amdgcn_s_sleep(4);
+    }
+    __syncthreads();
     zero_fill_range(a.fill, a.fill_n16, a.fill_tail, a.fill_ntail,
                     (int64_t)blockIdx.x - a.L * a.B, a.fill_blocks);
     return;
@@ -594,50 +656,21 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   const int64_t lb = blockIdx.x, b = lb % a.B;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t Q = a.Q, GTo = a.GT_out;
-  float* costL = INLDS ? (float*)(smem + L.costL) : a.costT + lb * GTo * Q;
+  float* costL = INLDS ? (float*)(smem + L.costL) : a.tot + lb * a.tot_stride;
   const int64_t term = a.L * a.B * Q * GTo;
   const float* sep = a.sep + lb * Q * GTo;
 
-  // ---- 1. total cost (bce + dice) + cls as float (src/cpu/matching.cpp:665),
-  //         transposed to [column][query]; column validity (matching.cpp:497-511)
+  // ---- 1. the image's total cost (bce + dice) + cls (src/cpu/matching.cpp:665),
+  //         [column][query] from finalize, into LDS; column validity
+  //         (matching.cpp:497-511).  Only the rows of non-empty GTs are
+  //         staged: an empty GT's costs are +inf, so its column is invalid
+  //         and its row is never read.
   for (int64_t c = tid; c <= GTo; c += 256) colok[c] = 0;
   __syncthreads();
-  {
-    // the image's (bce + dice) + cls plane from finalize: [q][c], a padded
-    // stride of whole 16-byte words; every thread issues all of its 16-byte
-    // loads before the first transposed LDS store
-    const uint32_t n = (uint32_t)(Q * GTo), n4 = (n + 3) / 4;
-    const float4* tot = (const float4*)(a.tot + lb * a.tot_stride);
-    const uint32_t gto = (uint32_t)GTo, q32 = (uint32_t)Q;
-    constexpr int U = 24;  // 24 x 256 x 16 B = 96 KB per round
-    for (uint32_t v0 = tid; v0 < n4; v0 += 256 * U) {
-      float4 v[U];
-#pragma unroll
-      for (int k = 0; k < U; ++k) {
-        const uint32_t vi = v0 + k * 256;
-        if (vi < n4) v[k] = tot[vi];
-      }
-#pragma unroll
-      for (int k = 0; k < U; ++k) {
-        const uint32_t vi = v0 + k * 256;
-        if (vi >= n4) continue;
-        uint32_t i = vi * 4, q = i / gto, c = i - q * gto;
-        const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-        for (int h = 0; h < 4; ++h, ++i) {
-          if (i < n) {
-            costL[c * q32 + q] = e[h];
-            if (cost_ok((double)e[h], a.inf_thresh)) colok[c] = 1;  // benign race: all store 1
-          }
-          if (++c == gto) {
-            c = 0;
-            ++q;
-          }
-        }
-      }
-    }
-  }
+  if ((Q & 3) == 0) stage_rows<4, NJ, INLDS>(a, lb, b, costL, colok);
+  else stage_rows<1, NJ, INLDS>(a, lb, b, costL, colok);
   __syncthreads();
+  if (tid == 0 && a.fill_blocks) __hip_atomic_fetch_add(a.gate, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- 2. assignment on wave 0
   if (wave == 0) {
@@ -664,13 +697,11 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       for (int64_t q = lane; q < Q; q += 64) preds[q] = (int)q;
       wave_sync();
       if (a.strategy == ML_GLOBAL || a.strategy == ML_PSEUDO_GREEDY) {
-        int M = 0;
+        // the assignment's rows: the valid columns, repeated K times for
+        // global (once for pseudo-greedy), at most Q of them
         const int64_t reps = a.strategy == ML_GLOBAL ? K : 1;
-        for (int64_t rep = 0; rep < reps && M < Q; ++rep)
-          for (int t = 0; t < nv && M < Q; ++t) {
-            if (lane == 0) hrows[M] = vcols[t];
-            ++M;
-          }
+        const int M = (int)min(reps * (int64_t)nv, Q);
+        for (int k = lane; k < M; k += 64) hrows[k] = vcols[k % nv];
         wave_sync();
         okh = hungarian_wave<NJ>(costL, Q, preds, (int)Q, hrows, M, thr, BIG, pp, way, u, hout);
         if (okh) {

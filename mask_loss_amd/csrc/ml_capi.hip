@@ -153,7 +153,7 @@ CostPlan bound_cost_plan(const Dims& d) {
   return p;
 }
 
-Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
+Layout make_layout(const Dims& d, bool force_masks) {
   Layout L;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -173,13 +173,13 @@ Layout make_layout(const Dims& d, bool force_masks, bool need_costT) {
   L.sched = take((size_t)sched_ints(pl.ntasks) * 4);
   L.partials = take((size_t)pl.float_total * 4);
   L.rowsum = take(force_masks ? (size_t)pl.nclass * cap * d.rows * 2 * 4 : 0);
-  L.costT = take(need_costT ? (size_t)d.LB * d.GT_out * d.Q * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
   L.tot = take((size_t)d.LB * ceil_div(d.Q * d.GT_out, 4) * 16);
   L.rowIT = take((size_t)d.LB * d.Q * d.nslot * 8);
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
   L.img = take((size_t)d.LB * 4 * 4);
   L.layer = take((size_t)d.L * ML_LAYERS * 4);
+  L.gate = take(16);
   L.total = o;
   return L;
 }
@@ -241,7 +241,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   const SavedLayout SL = saved_layout(d);
   unsigned char* sv = (unsigned char*)saved;
   float* stats = saved ? (float*)(sv + SL.stats) : nullptr;
-  const Layout L = make_layout(d, force_masks, !in_lds);
+  const Layout L = make_layout(d, force_masks);
   if (ws_bytes < L.total) return fail(ML_EWORKSPACE, "workspace too small");
   unsigned char* w = (unsigned char*)ws;
   int rc;
@@ -304,6 +304,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.plan = plan;
   aa.ncols = pa.ncols;
   aa.slot_of_col = pa.slot_of_col;
+  aa.colmap = pa.colmap;
   aa.sep = sep ? sep : (float*)(w + L.sep);
   if (cls_logits) {
     aa.out_bce = aa.sep;
@@ -313,7 +314,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
     aa.out_dice = dice_out;
   }
   aa.rowstat = (float*)(w + L.rowstat);
-  aa.costT = in_lds ? nullptr : (float*)(w + L.costT);
   aa.tot = costs_only ? nullptr : (float*)(w + L.tot);
   aa.tot_stride = ceil_div(d.Q * d.GT_out, 4) * 4;
   aa.rowIT = costs_only || !stats ? nullptr : (float*)(w + L.rowIT);
@@ -328,6 +328,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.fill_n16 = (int64_t)(prefill_bytes / 16);
   aa.fill_tail = (unsigned char*)prefill + prefill_bytes / 16 * 16;
   aa.fill_ntail = (int64_t)(prefill_bytes % 16);
+  aa.gate = (int*)(w + L.gate);
   aa.fill_blocks = prefill_bytes && !costs_only
                        ? (int)std::min<int64_t>(kFillBlocks, std::max<int64_t>(1, ceil_div(aa.fill_n16, 256)))
                        : 0;
@@ -453,7 +454,7 @@ size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p, in
   Dims d;
   std::string err;
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
-  return make_layout(d, p->force_unmatched_masks_to_empty != 0, !cost_fits_lds(d)).total;
+  return make_layout(d, p->force_unmatched_masks_to_empty != 0).total;
 }
 
 size_t ml_pairwise_mask_loss_workspace_size(const ml_shape* s, const ml_params* p,
@@ -461,7 +462,7 @@ size_t ml_pairwise_mask_loss_workspace_size(const ml_shape* s, const ml_params* 
   Dims d;
   std::string err;
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
-  return make_layout(d, false, !cost_fits_lds(d)).total;
+  return make_layout(d, false).total;
 }
 
 int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dtype,

@@ -6,6 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <string>
 
 #include "ml_common.h"
@@ -133,9 +134,9 @@ inline SavedLayout saved_layout(const Dims& d) {
 // Byte offsets inside the caller's workspace.
 struct Layout {
   size_t lab16, counts8, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
-      costT, sep, tot, rowIT, rowstat, img, layer, total;
+      sep, tot, rowIT, rowstat, img, layer, gate, total;
 };
-Layout make_layout(const Dims& d, bool force_masks, bool need_costT);
+Layout make_layout(const Dims& d, bool force_masks);
 // Plan slots / offsets of the cost launches (queries kernel occupancy on the
 // current device; the workspace bound uses kCostSlots only).
 CostPlan make_cost_plan(const Dims& d, int dtype, bool tab);
@@ -207,12 +208,12 @@ struct AssignArgs {
   CostPlan plan;
   const int* ncols;
   const int* slot_of_col;
+  const int* colmap;     // [B][nslot]: output column of each non-empty GT slot
   // outputs
   float* sep;            // (3, L, B, Q, GT_out): bce, dice, label cost
   float* out_bce;        // where finalize writes the bce / dice planes (sep's
   float* out_dice;       // first two planes, or a standalone operator's outputs, or null)
-  float* costT;          // [LB][GT_out][Q] transposed total cost (global fallback)
-  float* tot;            // [LB][tot_stride] total cost (bce + dice) + label per (q, c), or null
+  float* tot;            // [LB][tot_stride] total cost (bce + dice) + label, [c][q], or null
   int64_t tot_stride;    // Q * GT_out rounded up to whole 16-byte words
   float* rowIT;          // [LB*Q][nslot][2] summed I, T per column slot, or null
   int64_t* pred_to_gt;   // (L,B,Q) or null (costs-only mode)
@@ -227,6 +228,9 @@ struct AssignArgs {
   unsigned char* fill_tail;
   int64_t fill_ntail;
   int fill_blocks;
+  // fill start gate: finalize zeroes it, each assignment workgroup adds 1 once
+  // its cost matrix is staged, and the fill workgroups wait (bounded) for L*B
+  int* gate;
   // dims / params
   int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, rtiles;
   int rows, nslot;

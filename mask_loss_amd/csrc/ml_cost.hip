@@ -231,6 +231,24 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
   A[3] = __builtin_bit_cast(bf16x8_t, a3);
 }
 
+// Pacing of the waves of one workgroup that share a CU: the SIMD arbiter
+// issues the oldest ready wave first, so with equal work the younger waves
+// fall behind and the CU ends the launch at part occupancy.  Every few
+// K-steps a wave posts its progress in LDS and drops its issue priority while
+// it is ahead of the slowest wave of the workgroup (progress values are
+// approximate: no barrier, a stale read only delays the switch).
+constexpr int kPaceSlack = 8;  // K-steps ahead of the slowest wave before yielding
+__device__ __forceinline__ void pace(int* prog, int k) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  if (lane == 0) prog[wave] = k;
+  int v = lane < nw ? prog[lane] : 0x7FFFFFFF;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  if (__builtin_amdgcn_readfirstlane(v) + kPaceSlack < k) __builtin_amdgcn_s_setprio(0);
+  else __builtin_amdgcn_s_setprio(1);
+}
+
 // One wave's work: 16*RT query rows of task (lb, rtile) over the K-steps of
 // split ks of KS; writes the partial sums to `out` ([3][16*RT][16*NT]) and,
 // for unweighted penalties, the row sums to `rs` ([16*RT][2]).  TAB:
@@ -240,7 +258,7 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
 template <int DT, int RT, int NT, bool CNT, bool TAB>
 __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
                                           int64_t ks, int64_t KS, const unsigned char* lut,
-                                          float* out, float* rs_out) {
+                                          float* out, float* rs_out, int* prog) {
   constexpr int NS = InTraits<DT>::kSplit;
   constexpr int D = TAB ? kDepth : 2;  // K-steps of logits and labels in flight
   const int lane = threadIdx.x & 63;
@@ -390,6 +408,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
     }
     int64_t k = 0;
     for (; k + D <= nst; k += D) {
+      if (prog && (k & (2 * D - 1)) == 0) pace(prog, (int)k);
 #pragma unroll
       for (int j = 0; j < D; ++j) {
         bf16x8_t A[4][RT][NS];
@@ -523,19 +542,20 @@ constexpr int kClassOf = NT == 2 ? 0 : NT == 4 ? 1 : NT == 7 ? 2 : 3;
 // and K-split read from the device schedule.  The grid has
 // max(slots, tasks) waves, so every item has a wave.
 template <int DT, int RT, int NT, bool CNT, bool TAB>
-__global__ __launch_bounds__(64 * cost_waves(NT)) void cost_kernel(CostArgs a) {
+__global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs a) {
   constexpr int CI = kClassOf<NT>;
+  constexpr int WV = cost_waves(NT, TAB);
   __shared__ __align__(16) unsigned char lut_s[TAB ? kLutBytes : 16];
+  __shared__ int prog_s[WV];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n = __builtin_amdgcn_readfirstlane(a.sched[CI]);
   const int64_t KS = __builtin_amdgcn_readfirstlane(a.sched[kClasses + CI]);
   const int64_t total = n * KS;
-  const int64_t w0 = (int64_t)blockIdx.x * cost_waves(NT);
+  const int64_t w0 = (int64_t)blockIdx.x * WV;
   if (w0 >= total) return;  // the whole workgroup is idle
-  if constexpr (TAB) {
-    build_lut(lut_s, a.ep);
-    __syncthreads();
-  }
+  if (threadIdx.x < WV) prog_s[threadIdx.x] = 0;
+  if constexpr (TAB) build_lut(lut_s, a.ep);
+  __syncthreads();
   const int64_t w = w0 + wave;
   if (w >= total) return;
   const int64_t i = w / KS, ks = w % KS;
@@ -544,7 +564,8 @@ __global__ __launch_bounds__(64 * cost_waves(NT)) void cost_kernel(CostArgs a) {
   constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
   float* out = a.partials + a.plan.float_base[CI] + w * tile;
   float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + w) * (16 * RT) * 2 : nullptr;
-  cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs);
+  // pace the waves only where many share the workgroup's CU
+  cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs, WV >= 16 ? prog_s : nullptr);
 }
 
 // ---- launch plan ---------------------------------------------------------------
@@ -557,12 +578,12 @@ static int occ_slots() {
   int v = cache[dev].load(std::memory_order_relaxed);
   if (v == 0) {
     int nb = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_kernel<DT, RT, NT, CNT, TAB>, 64 * cost_waves(NT), 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_kernel<DT, RT, NT, CNT, TAB>, 64 * cost_waves(NT, TAB), 0) !=
             hipSuccess || nb < 1)
       nb = 1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
       cus = 256;
-    v = nb * cus * cost_waves(NT);
+    v = nb * cus * cost_waves(NT, TAB);
     cache[dev].store(v, std::memory_order_relaxed);
   }
   return v;
@@ -608,7 +629,7 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
 template <int DT, int RT, int NT>
 static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   constexpr int CI = kClassOf<NT>;
-  constexpr int WV = cost_waves(NT);
+  const int WV = cost_waves(NT, DT == ML_BF16 && tab && !d.counts_mode);
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), WV));
   if (d.counts_mode)
     hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true, false>), grid, dim3(64 * WV), 0, st, a);

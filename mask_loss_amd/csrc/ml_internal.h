@@ -39,9 +39,13 @@ constexpr int kFillBlocks = 64;
 // count NT is the smallest of {2, 4, 7, 16} that holds G + 1 columns.
 constexpr int kClasses = 4;
 __host__ __device__ inline int class_nt(int ci) { return ci == 0 ? 2 : ci == 1 ? 4 : ci == 2 ? 7 : 16; }
-// Waves per cost workgroup (all share one LDS table): 8, except for the
-// widest class, whose accumulators need more than 256 registers per lane.
-__host__ __device__ constexpr int cost_waves(int nt) { return nt >= 16 ? 4 : 8; }
+// Waves per cost workgroup (all share one LDS table): 16 for the narrowest
+// class on the table path (one workgroup per CU, at most 128 registers per
+// lane), 4 for the widest class (its accumulators need more than 256
+// registers per lane), 8 otherwise.
+__host__ __device__ constexpr int cost_waves(int nt, bool tab) {
+  return nt == 2 && tab ? 16 : nt >= 16 ? 4 : 8;
+}
 __host__ __device__ inline int class_of(int ncols_plus_one) {
   const int need = (ncols_plus_one + 15) >> 4;
   return need <= 2 ? 0 : need <= 4 ? 1 : need <= 7 ? 2 : 3;

@@ -65,6 +65,14 @@ __device__ __forceinline__ uint32_t pk_lshl3_u16(uint32_t a) {
   return r;
 }
 
+// (a & m) | (b & ~m) in one v_bfi_b32 (written out, the compiler splits it
+// into and / or / bitop3)
+__device__ __forceinline__ uint32_t bfi32(uint32_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
+
 // The four planes of one logit from the float32 formulas (+ the unweighted
 // terms of the unmatched-mask penalty).
 __device__ __forceinline__ void planes_formula(float z, const ElemParams& ep, float& neg,
@@ -217,7 +225,8 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
     const uint32_t m = u[i] & 0x7FFF7FFFu;
     const uint32_t idx =
         pk_min_u16(pk_sub_sat_u16(m, kLutSub * 0x10001u), (kLutN + 1) * 0x10001u);
-    const uint32_t addr = (u[i] & 0x80008000u) | pk_lshl3_u16(idx);
+    // sign bits (the negative block's 32 KB offset) merged in with one bitfield insert
+    const uint32_t addr = bfi32(0x80008000u, u[i], pk_lshl3_u16(idx));
     const uint2 e0 = *(const uint2*)(lut + (addr & 0xFFFFu));
     const uint2 e1 = *(const uint2*)(lut + (addr >> 16));
     a0[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x05040100u);

@@ -215,11 +215,9 @@ __device__ __forceinline__ void planes8_formula(const Raw8<DT>& r, const ElemPar
   for (int pl = 0; pl < 4; ++pl) split_pack<NS>(v[pl], A[pl]);
 }
 
-// A planes of one row's 8 bf16 cells from the LDS table.
-__device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char* lut,
-                                            bf16x8_t A[4]) {
+// Table entries of one row's 8 bf16 cells (LDS reads only; see lut_planes).
+__device__ __forceinline__ void lut_lookup8(const uint4& x, const unsigned char* lut, uint2 E[8]) {
   const uint32_t u[4] = {x.x, x.y, x.z, x.w};
-  u32x4_t a0, a1, a2, a3;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t m = u[i] & 0x7FFF7FFFu;
@@ -227,8 +225,18 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
         pk_min_u16(pk_sub_sat_u16(m, kLutSub * 0x10001u), (kLutN + 1) * 0x10001u);
     // sign bits (the negative block's 32 KB offset) merged in with one bitfield insert
     const uint32_t addr = bfi32(0x80008000u, u[i], pk_lshl3_u16(idx));
-    const uint2 e0 = *(const uint2*)(lut + (addr & 0xFFFFu));
-    const uint2 e1 = *(const uint2*)(lut + (addr >> 16));
+    E[2 * i] = *(const uint2*)(lut + (addr & 0xFFFFu));
+    E[2 * i + 1] = *(const uint2*)(lut + (addr >> 16));
+  }
+}
+
+// The four A planes from the entries of 8 cells: (neg, pos) and (wp, w) of
+// each cell regrouped into per-plane pairs of consecutive cells.
+__device__ __forceinline__ void lut_planes(const uint2 E[8], bf16x8_t A[4]) {
+  u32x4_t a0, a1, a2, a3;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint2 e0 = E[2 * i], e1 = E[2 * i + 1];
     a0[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x05040100u);
     a1[i] = __builtin_amdgcn_perm(e1.x, e0.x, 0x07060302u);
     a2[i] = __builtin_amdgcn_perm(e1.y, e0.y, 0x05040100u);
@@ -238,6 +246,14 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
   A[1] = __builtin_bit_cast(bf16x8_t, a1);
   A[2] = __builtin_bit_cast(bf16x8_t, a2);
   A[3] = __builtin_bit_cast(bf16x8_t, a3);
+}
+
+// A planes of one row's 8 bf16 cells from the LDS table.
+__device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char* lut,
+                                            bf16x8_t A[4]) {
+  uint2 E[8];
+  lut_lookup8(x, lut, E);
+  lut_planes(E, A);
 }
 
 // Pacing of the waves of one workgroup that share a CU: the SIMD arbiter
@@ -416,27 +432,61 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
       fetch_l(j, j);
     }
     int64_t k = 0;
-    for (; k + D <= nst; k += D) {
-      if (prog && (k & (2 * D - 1)) == 0) pace(prog, (int)k);
+    if constexpr (TAB) {
+      // table path, software-pipelined one step deep: the LDS reads of step
+      // k + 1 are issued before the one-hot operands and MFMAs of step k, so
+      // their latency hides behind that work
+      uint2 E[RT][8];
 #pragma unroll
-      for (int j = 0; j < D; ++j) {
+      for (int rt = 0; rt < RT; ++rt) lut_lookup8(buf[0][rt].w[0], lut, E[rt]);
+      auto step = [&](int j, int64_t kj, bool refill) {
         bf16x8_t A[4][RT][NS];
-        planes(buf[j], A);
-        // keep each refill below the last read of its slot, so that it reuses
-        // the slot's registers instead of rotating the whole pipeline
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          bf16x8_t T1[4];
+          lut_planes(E[rt], T1);
+#pragma unroll
+          for (int pl = 0; pl < 4; ++pl) A[pl][rt][0] = T1[pl];
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) lut_lookup8(buf[(j + 1) % D][rt].w[0], lut, E[rt]);
         __builtin_amdgcn_sched_barrier(0);
-        fetch_z(j, k + j + D);
-        mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+        if (refill) fetch_z(j, kj + D);
+        mma_step(A, lbuf[j], (s0 + kj) * kStep + g4 * 8);
         __builtin_amdgcn_sched_barrier(0);
-        fetch_l(j, k + j + D);
+        if (refill) fetch_l(j, kj + D);
+      };
+      for (; k + D <= nst; k += D) {
+        if (prog && (k & (2 * D - 1)) == 0) pace(prog, (int)k);
+#pragma unroll
+        for (int j = 0; j < D; ++j) step(j, k + j, true);
       }
-    }
 #pragma unroll
-    for (int j = 0; j < D - 1; ++j) {  // the last nst % D steps
-      if (k + j < nst) {
-        bf16x8_t A[4][RT][NS];
-        planes(buf[j], A);
-        mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+      for (int j = 0; j < D - 1; ++j)  // the last nst % D steps
+        if (k + j < nst) step(j, k + j, false);
+    } else {
+      for (; k + D <= nst; k += D) {
+        if (prog && (k & (2 * D - 1)) == 0) pace(prog, (int)k);
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          bf16x8_t A[4][RT][NS];
+          planes(buf[j], A);
+          // keep each refill below the last read of its slot, so that it reuses
+          // the slot's registers instead of rotating the whole pipeline
+          __builtin_amdgcn_sched_barrier(0);
+          fetch_z(j, k + j + D);
+          mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+          __builtin_amdgcn_sched_barrier(0);
+          fetch_l(j, k + j + D);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < D - 1; ++j) {  // the last nst % D steps
+        if (k + j < nst) {
+          bf16x8_t A[4][RT][NS];
+          planes(buf[j], A);
+          mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+        }
       }
     }
   }

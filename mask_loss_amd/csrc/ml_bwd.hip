@@ -312,6 +312,8 @@ __device__ __forceinline__ void cls_out(void* p, int dt, int64_t i, float v) {
 }
 
 // Class-logit gradient of one (l,b,q) row, on one wave.
+constexpr int kClsRegs = 4;  // class rows of up to 256 logits are held in registers
+
 __device__ void cls_row(const BwdArgs& a, int64_t row) {
   const int lane = threadIdx.x & 63;
   const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
@@ -336,6 +338,31 @@ __device__ void cls_row(const BwdArgs& a, int64_t row) {
   if (a.use_softmax) {
     if (matched || (a.force_cls && has_void)) {
       const int64_t tgt = matched ? y : a.void_idx;
+      if (C <= 64 * kClsRegs) {  // the row's logits stay in registers: one load
+        float zv[kClsRegs];
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kClsRegs; ++k) {
+          const int64_t c = lane + 64 * k;
+          zv[k] = c < C ? cls_in(a.cls_logits, a.cls_dtype, base + c) : -INFINITY;
+          m = fmaxf(m, zv[k]);
+        }
+        m = wave_max(m);
+        float se = 0.f;
+#pragma unroll
+        for (int k = 0; k < kClsRegs; ++k) {
+          zv[k] = lane + 64 * k < C ? __expf(zv[k] - m) : 0.f;
+          se += zv[k];
+        }
+        se = wave_sum(se);
+        const float inv = se > 0.f ? 1.f / se : 0.f;
+#pragma unroll
+        for (int k = 0; k < kClsRegs; ++k) {
+          const int64_t c = lane + 64 * k;
+          if (c < C) cls_out(a.grad_cls, a.cls_dtype, base + c, coeff * (zv[k] * inv - (c == tgt ? 1.f : 0.f)));
+        }
+        return;
+      }
       float m = -INFINITY;
       for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_in(a.cls_logits, a.cls_dtype, base + c));
       m = wave_max(m);
@@ -596,12 +623,19 @@ __global__ __launch_bounds__(kLutThreads) void bwd_mask_lut_kernel(BwdArgs a, in
       cur = nxt;
     }
   }
-  // then the class-logit gradients, one row per wave (no separate launch)
+  // then the class-logit gradients, one row per wave (no separate launch),
+  // on the workgroups that had the fewest mask items (items are dealt out
+  // round robin, so those are the last total % grid ones; all of them when
+  // the items divide evenly)
   if (a.cls_fused) {
     constexpr int kWaves = kLutThreads / 64;
     const int wave = threadIdx.x >> 6;
-    for (int64_t r0 = (int64_t)blockIdx.x * kWaves; r0 < rows; r0 += (int64_t)gridDim.x * kWaves)
-      if (r0 + wave < rows) cls_row(a, r0 + wave);
+    const int64_t G = gridDim.x, extra = total % G;
+    const int64_t nlight = extra == 0 ? G : G - extra;
+    const int64_t rank = (int64_t)blockIdx.x - (G - nlight);
+    if (rank >= 0)
+      for (int64_t r0 = rank * kWaves; r0 < rows; r0 += nlight * kWaves)
+        if (r0 + wave < rows) cls_row(a, r0 + wave);
   }
 }
 

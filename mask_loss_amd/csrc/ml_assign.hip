@@ -122,7 +122,10 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
 }
 
 __global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
-  if (blockIdx.x == 0 && threadIdx.x == 0 && a.gate) *a.gate = 0;  // the assignment's fill gate
+  if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's fill gate and finish count
+    if (a.gate) *a.gate = 0;
+    if (a.done) *a.done = 0;
+  }
   __shared__ float sl[4][3][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -879,6 +882,20 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       a.img[lb * 4 + 2] = s2;
       a.img[lb * 4 + 3] = s3;
     }
+  }
+  // ---- 4. the last image to finish runs the per-layer pass (means,
+  //         denominators, matched-row list) over every image's results:
+  //         release this workgroup's writes, count it, and acquire the others'
+  if (a.done) {
+    __shared__ int last;
+    __syncthreads();
+    if (tid == 0) {
+      __threadfence();
+      last = atomicAdd(a.done, 1) == (int)(a.L * a.B) - 1;
+      __threadfence();
+    }
+    __syncthreads();
+    if (last) layer_pass(a.layer_args);
   }
 }
 

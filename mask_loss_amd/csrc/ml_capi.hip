@@ -329,6 +329,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.fill_tail = (unsigned char*)prefill + prefill_bytes / 16 * 16;
   aa.fill_ntail = (int64_t)(prefill_bytes % 16);
   aa.gate = (int*)(w + L.gate);
+  aa.done = costs_only ? nullptr : (int*)(w + L.gate) + 1;
   aa.fill_blocks = prefill_bytes && !costs_only
                        ? (int)std::min<int64_t>(kFillBlocks, std::max<int64_t>(1, ceil_div(aa.fill_n16, 256)))
                        : 0;
@@ -378,13 +379,16 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   la.force_masks = force_masks;
   la.force_cls = p->force_unmatched_class_to_background;
   la.has_void = void_idx >= 0;
+  aa.layer_args = la;  // run by the last assignment workgroup
   if (d.LB > 0) {
     if ((rc = launch_assign(aa, d, st))) return rc;
-  } else if (prefill_bytes) {
-    ProfScope ps_("prefill", st);
-    if ((rc = launch_zero_fill(prefill, prefill_bytes, st))) return rc;
+  } else {
+    if (prefill_bytes) {
+      ProfScope ps_("prefill", st);
+      if ((rc = launch_zero_fill(prefill, prefill_bytes, st))) return rc;
+    }
+    if (d.L > 0 && (rc = launch_layer(la, st))) return rc;
   }
-  if (d.L > 0 && (rc = launch_layer(la, st))) return rc;
   return ML_OK;
 }
 

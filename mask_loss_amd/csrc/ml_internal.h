@@ -235,6 +235,10 @@ struct AssignArgs {
   // fill start gate: finalize zeroes it, each assignment workgroup adds 1 once
   // its cost matrix is staged, and the fill workgroups wait (bounded) for L*B
   int* gate;
+  // finished-image count (zeroed by finalize): the assignment workgroup that
+  // finishes last runs the per-layer pass `layer_args`, or done == null
+  int* done;
+  LayerArgs layer_args;
   // dims / params
   int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, rtiles;
   int rows, nslot;

@@ -124,10 +124,12 @@ size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p,
  * pinned host memory mapped for the device): it receives 1 if any of the
  * B*GT_total entries of cls_targets equals params.void_class_index (a valid
  * class index), else 0 -- the reference's check of
- * functions/mask/matching.py:184-185, done by the forward's first kernels.
+ * functions/mask/matching.py:184-185, done by the forward's first kernels
+ * with a system-scope store, so a host can poll a coherent pinned word
+ * (preset to another value) without waiting for the whole forward.
  * void_ready: NULL, or a hipEvent_t recorded on `stream` as soon as
- * void_found is written (before the cost contraction), so that a caller can
- * wait for the check without waiting for the whole forward. */
+ * void_found is written (before the cost contraction); recording it costs
+ * the next kernel a system-scope release, so polling is the faster wait. */
 int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
                              const void* mask_logits, const int64_t* mask_targets,
                              int cls_dtype, const void* cls_logits,

@@ -9,6 +9,8 @@
 #include <ATen/hip/HIPContext.h>
 #include <torch/extension.h>
 
+#include <chrono>
+#include <thread>
 #include <vector>
 
 #include "../../include/mask_loss_hip.h"
@@ -33,13 +35,14 @@ void ml_ok(int rc) { TORCH_CHECK(rc == ML_OK, ml_last_error()); }
 
 ml_stream_t cur_stream() { return (ml_stream_t)at::hip::getCurrentHIPStream().stream(); }
 
-// The forward's void-class check writes its answer into a pinned host word
-// (mapped for the device) and records an event right after it; one word and
-// event per host thread and device, kept for the life of the process.
+// The forward's void-class check writes its answer into a pinned, coherent
+// host word (mapped for the device) with a system-scope store; the host
+// polls the word rather than recording an event in the stream (an event's
+// system-scope release would stall the next kernel).  One word per host
+// thread and device, kept for the life of the process.
 struct VoidSlot {
   volatile int32_t* host = nullptr;
   int32_t* dev = nullptr;
-  hipEvent_t ev = nullptr;
 };
 
 VoidSlot& void_slot() {
@@ -52,15 +55,29 @@ VoidSlot& void_slot() {
   if (!v.host) {
     void* h = nullptr;
     void* d = nullptr;
-    TORCH_CHECK(hipHostMalloc(&h, 64, hipHostMallocMapped) == hipSuccess,
+    TORCH_CHECK(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess,
                 "cannot allocate the pinned void-check word");
-    TORCH_CHECK(hipHostGetDevicePointer(&d, h, 0) == hipSuccess &&
-                    hipEventCreateWithFlags(&v.ev, hipEventDisableTiming) == hipSuccess,
-                "cannot map the void-check word");
+    TORCH_CHECK(hipHostGetDevicePointer(&d, h, 0) == hipSuccess, "cannot map the void-check word");
     v.dev = (int32_t*)d;
     v.host = (volatile int32_t*)h;
   }
   return v;
+}
+
+// Wait until the device has written the word (it holds -1 until then); if
+// that takes unusually long, drain the stream, after which it is written.
+int32_t wait_void_word(const VoidSlot& v, ml_stream_t stream) {
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int32_t x = *v.host; x == -1; x = *v.host) {
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
+      TORCH_CHECK(hipStreamSynchronize((hipStream_t)stream) == hipSuccess, "void check: stream failed");
+      const int32_t y = *v.host;
+      TORCH_CHECK(y != -1, "void check: the flag was not written");
+      return y;
+    }
+    std::this_thread::yield();
+  }
+  return *v.host;
 }
 
 torch::Tensor workspace(size_t bytes, const torch::Tensor& like) {
@@ -206,17 +223,15 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
   auto ws = workspace(wsb, mask_logits);
   TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, "unsupported shape for mask_matching");
   VoidSlot* vs = check_void ? &void_slot() : nullptr;
+  if (vs) *vs->host = -1;
   ml_ok(ml_mask_matching_forward(
       &s, &p, mdt, mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt,
       cls_logits.data_ptr(), cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
       pred_round.data_ptr<int64_t>(), means.data_ptr<float>(), nullptr,
       want_saved ? saved.data_ptr() : nullptr, prefill, vs ? vs->dev : nullptr,
-      vs ? (ml_event_t)vs->ev : nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
+      nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
   int32_t void_hit = -1;
-  if (vs) {  // waits for the preparation kernels only; the rest stays queued
-    TORCH_CHECK(hipEventSynchronize(vs->ev) == hipSuccess, "void-check event failed");
-    void_hit = *vs->host;
-  }
+  if (vs) void_hit = wait_void_word(*vs, cur_stream());  // the rest of the forward stays queued
   // means follow the logits dtype (src/cuda/mask_matching_forward.cu:580-583);
   // the fused entry keeps them in float32
   const auto out_dt = want_saved ? torch::kFloat32 : mask_logits.scalar_type();

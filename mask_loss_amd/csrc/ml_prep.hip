@@ -97,7 +97,8 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
     if (a.void_idx >= 0)
       for (int64_t b = lane; b < a.B; b += 64) hit |= a.vflag[b];
     hit = __any(hit);
-    if (lane == 0) *a.void_found = hit ? 1 : 0;
+    // system scope: the word may be pinned host memory that the host polls
+    if (lane == 0) __hip_atomic_store(a.void_found, hit ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   for (int64_t b = wave; b < a.B; b += nw) {
     // presence word j = OR over the image's preparation workgroups: lane

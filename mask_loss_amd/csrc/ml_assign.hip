@@ -121,7 +121,8 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
   v2 = (a2[0] + a2[1]) + (a2[2] + a2[3]);
 }
 
-__global__ __launch_bounds__(256) void finalize_kernel(AssignArgs a) {
+// Latency-bound: at least four waves per SIMD (at most 128 registers).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void finalize_kernel(AssignArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's fill gate and finish count
     if (a.gate) *a.gate = 0;
     if (a.done) *a.done = 0;

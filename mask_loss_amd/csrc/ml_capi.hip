@@ -115,7 +115,6 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
   d.HWp = ceil_div(d.HW, kStep) * kStep;
   const int64_t need = ceil_div(d.GT_out + 1, 16);  // + ones column
   if (need <= 2) d.NT = 2;
-  else if (need <= 4) d.NT = 4;
   else if (need <= 7) d.NT = 7;
   else if (need <= 16) d.NT = 16;
   else {

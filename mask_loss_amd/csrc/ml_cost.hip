@@ -594,7 +594,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
 }
 
 template <int NT>
-constexpr int kClassOf = NT == 2 ? 0 : NT == 4 ? 1 : NT == 7 ? 2 : 3;
+constexpr int kClassOf = NT == 2 ? 0 : NT == 7 ? 1 : 2;
 
 // One launch per column-tile class: wave w of the grid takes work item w of
 // the class (item = task index * KS + split), with the class's tasks, count
@@ -661,11 +661,8 @@ static void plan_slots(CostPlan& p, bool cnt, bool tab) {
     int v = 0;
     switch (ci) {
       case 0: v = occ_slots_for<DT, RT, 2>(cnt, tab); break;
-      case 1: v = occ_slots_for<DT, RT, 4>(cnt, tab); break;
-      case 2: v = occ_slots_for<DT, RT, 7>(cnt, tab); break;
-      default:
-        if constexpr (RT == 1) v = occ_slots_for<DT, 1, 16>(cnt, tab);
-        break;
+      case 1: v = occ_slots_for<DT, RT, 7>(cnt, tab); break;
+      default: v = occ_slots_for<DT, RT, 16>(cnt, tab); break;
     }
     p.slots[ci] = (int)std::min<int64_t>(std::max(v, 8), kCostSlots);
   }
@@ -676,10 +673,7 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
   const bool cnt = d.counts_mode;
   switch (dtype) {
     case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false); break;
-    case ML_BF16:
-      if (d.RT == 2) plan_slots<ML_BF16, 2>(p, cnt, tab);
-      else plan_slots<ML_BF16, 1>(p, cnt, tab);
-      break;
+    case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab); break;
     case ML_F16: plan_slots<ML_F16, 1>(p, cnt, false); break;
   }
   return p;
@@ -704,11 +698,8 @@ static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st
 template <int DT, int RT>
 static int launch_classes(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   int rc = launch_one<DT, RT, 2>(a, d, tab, st);
-  if (!rc && a.plan.nclass > 1) rc = launch_one<DT, RT, 4>(a, d, tab, st);
-  if (!rc && a.plan.nclass > 2) rc = launch_one<DT, RT, 7>(a, d, tab, st);
-  if constexpr (RT == 1) {
-    if (!rc && a.plan.nclass > 3) rc = launch_one<DT, 1, 16>(a, d, tab, st);
-  }
+  if (!rc && a.plan.nclass > 1) rc = launch_one<DT, RT, 7>(a, d, tab, st);
+  if (!rc && a.plan.nclass > 2) rc = launch_one<DT, RT, 16>(a, d, tab, st);
   return rc;
 }
 
@@ -720,9 +711,7 @@ int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool, hipStream_t s
   const bool tab = dtype == ML_BF16 && !d.counts_mode && a.use_lut && a.rowsum == nullptr;
   switch (dtype) {
     case ML_F32: return launch_classes<ML_F32, 1>(a, d, false, st);
-    case ML_BF16:
-      return d.RT == 2 ? launch_classes<ML_BF16, 2>(a, d, tab, st)
-                       : launch_classes<ML_BF16, 1>(a, d, tab, st);
+    case ML_BF16: return launch_classes<ML_BF16, 1>(a, d, tab, st);
     case ML_F16: return launch_classes<ML_F16, 1>(a, d, false, st);
   }
   return fail(ML_EINVAL, "unsupported mask logits dtype");

@@ -36,9 +36,11 @@ constexpr int kFillBlocks = 64;
 
 // Column-tile classes of the cost contraction: an image with G non-empty GT
 // columns (+ the ones column) is handled by the kernel instance whose tile
-// count NT is the smallest of {2, 4, 7, 16} that holds G + 1 columns.
-constexpr int kClasses = 4;
-__host__ __device__ inline int class_nt(int ci) { return ci == 0 ? 2 : ci == 1 ? 4 : ci == 2 ? 7 : 16; }
+// count NT is the smallest of {2, 7, 16} that holds G + 1 columns.  Which
+// classes have images is known on the device only, and every class launch
+// costs its dispatch latency even when empty, so the classes are few.
+constexpr int kClasses = 3;
+__host__ __device__ inline int class_nt(int ci) { return ci == 0 ? 2 : ci == 1 ? 7 : 16; }
 // Waves per cost workgroup (all share one LDS table): 16 for the narrowest
 // class on the table path (one workgroup per CU, at most 128 registers per
 // lane), 4 for the widest class (its accumulators need more than 256
@@ -48,7 +50,7 @@ __host__ __device__ constexpr int cost_waves(int nt, bool tab) {
 }
 __host__ __device__ inline int class_of(int ncols_plus_one) {
   const int need = (ncols_plus_one + 15) >> 4;
-  return need <= 2 ? 0 : need <= 4 ? 1 : need <= 7 ? 2 : 3;
+  return need <= 2 ? 0 : need <= 7 ? 1 : 2;
 }
 // Upper bound of resident cost waves the workspace is sized for (256 CUs x 16).
 constexpr int64_t kCostSlots = 4096;

@@ -135,7 +135,7 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
   const int64_t nt = a.plan.ntasks;
   int* list = a.sched + 2 * kClasses;
   int* idx = list + kClasses * nt;
-  int cnt[kClasses] = {0, 0, 0, 0};
+  int cnt[kClasses] = {};
   for (int64_t t0 = 0; t0 < nt; t0 += 64) {
     const int64_t t = t0 + lane;
     int ci = -1;

@@ -460,6 +460,33 @@ __device__ void build_grad_lut(float4* lut, const ElemParams& ep) {
   }
 }
 
+// With binary targets (s == 1) a cell needs Fd and only one of Fneg / Fpos:
+// two tables of (Fneg, Fd) and (Fpos, Fd) pairs, 8 bytes per entry, picked
+// per cell by its target (half the LDS traffic of the 16-byte entries).
+// Layout: [target][sign][kGBlock] float2, 90176 bytes in all.
+__device__ void build_grad_lut2(float2* lut, const ElemParams& ep) {
+  for (uint32_t e = threadIdx.x; e < 2 * kGBlock; e += blockDim.x) {
+    const uint32_t sgn = e >= kGBlock ? 1u : 0u;
+    const uint32_t j = e - sgn * kGBlock;
+    float4 v;
+    if (j <= kGN) {
+      const uint32_t mag = j == 0 ? 0u : kGSub + j;
+      v = grad_terms(__uint_as_float(((sgn << 15) | mag) << 16), ep);
+    } else {
+      v = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), 0.f);
+    }
+    lut[e] = make_float2(v.x, v.z);
+    lut[2 * kGBlock + e] = make_float2(v.y, v.z);
+  }
+}
+
+// table indices (sign block included) of the two bf16 logits packed in `u`
+__device__ __forceinline__ uint32_t lut_index_pair(uint32_t u) {
+  const uint32_t m = u & 0x7FFF7FFFu;
+  const uint32_t idx = pk_min_u16(pk_sub_sat_u16(m, kGSub * 0x10001u), (kGN + 1) * 0x10001u);
+  return idx + ((u >> 15) & 0x00010001u) * kGBlock;  // negative block (no carry: idx < 2^15)
+}
+
 // table entries of the two bf16 logits packed in `u`
 __device__ __forceinline__ void lut_pair(uint32_t u, const float4* lut, float4& lo, float4& hi) {
   const uint32_t m = u & 0x7FFF7FFFu;
@@ -573,20 +600,27 @@ __device__ __forceinline__ void lut_compute_store(const BwdArgs& a, const LutIte
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float4 e[2];
-      lut_pair(zw[i], lut, e[0], e[1]);
+      if constexpr (CNT) {
+        float4 e[2];
+        lut_pair(zw[i], lut, e[0], e[1]);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float tk = t[2 * i + h];
-        float g;
-        if constexpr (CNT) {
-          g = cs * (e[h].y * tk + e[h].x * fmaxf(a.N2 - tk, 0.f)) + e[h].z * (c2 - c3 * tk);
-        } else {  // tk in {0, 1}, N2 = 1
-          const bool pos = tk != 0.f;
-          g = cs * (pos ? e[h].y : e[h].x) + e[h].z * (pos ? c2 - c3 : c2);
+        for (int h = 0; h < 2; ++h) {
+          const float tk = t[2 * i + h];
+          const float g = cs * (e[h].y * tk + e[h].x * fmaxf(a.N2 - tk, 0.f)) + e[h].z * (c2 - c3 * tk);
+          bad |= g != g;
+          gr[2 * i + h] = g;
         }
-        bad |= g != g;
-        gr[2 * i + h] = g;
+      } else {  // tk in {0, 1}, N2 = 1: the (Fneg, Fd) or (Fpos, Fd) table
+        const float2* lut2 = (const float2*)lut;
+        const uint32_t idx = lut_index_pair(zw[i]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bool pos = t[2 * i + h] != 0.f;
+          const float2 e = lut2[(h ? idx >> 16 : idx & 0xFFFFu) + (pos ? 2 * kGBlock : 0u)];
+          const float g = cs * e.x + e.y * (pos ? c2 - c3 : c2);
+          bad |= g != g;
+          gr[2 * i + h] = g;
+        }
       }
     }
     if (__builtin_expect(bad, 0)) {  // table overflow marker (|z| >= 64, inf, nan): formulas
@@ -606,7 +640,8 @@ __device__ __forceinline__ void lut_compute_store(const BwdArgs& a, const LutIte
 template <bool CNT>
 __global__ __launch_bounds__(kLutThreads) void bwd_mask_lut_kernel(BwdArgs a, int64_t nchunk) {
   __shared__ float4 lut[2 * kGBlock];
-  build_grad_lut(lut, a.mask_ep);
+  if constexpr (CNT) build_grad_lut(lut, a.mask_ep);
+  else build_grad_lut2((float2*)lut, a.mask_ep);
   __syncthreads();
   const int64_t rows = a.L * a.B * a.Q;
   const int64_t nrows = a.list ? min((int64_t)a.list[0], rows) : rows;

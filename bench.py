@@ -30,15 +30,15 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3_dense_headline")
     ap.add_argument("--cpu-sample-images", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the per-config lines of the other BASELINE configurations")
-    ap.add_argument("--other-steps", type=int, default=10)
-    ap.add_argument("--other-warmup", type=int, default=3)
+    ap.add_argument("--other-steps", type=int, default=50)
+    ap.add_argument("--other-warmup", type=int, default=5)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of 512 MiB (3 launches), the reference "
                          "point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")

@@ -41,6 +41,14 @@ __device__ __forceinline__ float cls_elem(const void* p, int dt, int64_t i) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
+template <int DT>
+__device__ __forceinline__ float cls_at(const void* p, int64_t i) {
+  if constexpr (DT == ML_F32) return ((const float*)p)[i];
+  const uint16_t h = ((const uint16_t*)p)[i];
+  if constexpr (DT == ML_BF16) return __uint_as_float(((uint32_t)h) << 16);
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
 // Reference float32 formulas for one label logit (mask_matching_forward.cu:195-218).
 struct ClsTerm {
   float neg, pos;
@@ -92,36 +100,52 @@ __device__ __forceinline__ bool cost_ok(double c, double thr) { return isfinite(
 // classes, and the row terms used later: normaliser S, mass P, and the
 // unmatched-query penalties (src/cuda/mask_matching_forward.cu:125-277).
 // ---------------------------------------------------------------------------
-// Sum the K-split partials k0, k0 + step, ... of slot s: four independent
-// accumulators, so twelve loads are in flight per round trip.
+// Each row is a short chain of dependent memory round trips, and the grid
+// runs in a single round, so the kernel takes as long as one chain: every
+// load that does not depend on an earlier one is issued up front (column
+// count, schedule entries of every class, class logits, the output columns'
+// slots and targets), then the K-split partials together with the class
+// logits of the targets, then the stores.
+constexpr int kFinCls = 3;      // class logits held per lane (C <= 192)
+constexpr int kFinCols = 2;     // output columns held per lane (GT_out <= 128)
+constexpr int kFinSplits = 12;  // K-splits loaded per lane and batch
+
+// Sum the K-split partials k0, k0 + step, ... of slot s in split order.  The
+// loads of a batch are unconditional (indices clamped to the last split) so
+// all of them are in flight together.
 __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0, int step,
                                            float& v0, float& v1, float& v2) {
-  float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f}, a2[4] = {0.f, 0.f, 0.f, 0.f};
-  int ks = k0;
-  for (; ks + 3 * step < rp.KS; ks += 4 * step) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+  for (int base = k0; base < rp.KS; base += kFinSplits * step) {
+    float x0[kFinSplits], x1[kFinSplits], x2[kFinSplits];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float* P = rp.p0 + (int64_t)(ks + u * step) * rp.ks_stride + s;
-      a0[u] += P[0];
-      a1[u] += P[rp.plane];
-      a2[u] += P[2 * rp.plane];
+    for (int u = 0; u < kFinSplits; ++u) {
+      const int ks = min(base + u * step, rp.KS - 1);
+      const float* P = rp.p0 + (int64_t)ks * rp.ks_stride + s;
+      x0[u] = P[0];
+      x1[u] = P[rp.plane];
+      x2[u] = P[2 * rp.plane];
+    }
+#pragma unroll
+    for (int u = 0; u < kFinSplits; ++u) {
+      if (base + u * step < rp.KS) {
+        a0 += x0[u];
+        a1 += x1[u];
+        a2 += x2[u];
+      }
     }
   }
-#pragma unroll
-  for (int u = 0; u < 3; ++u) {  // at most three splits remain
-    if (ks + u * step < rp.KS) {
-      const float* P = rp.p0 + (int64_t)(ks + u * step) * rp.ks_stride + s;
-      a0[u] += P[0];
-      a1[u] += P[rp.plane];
-      a2[u] += P[2 * rp.plane];
-    }
-  }
-  v0 = (a0[0] + a0[1]) + (a0[2] + a0[3]);
-  v1 = (a1[0] + a1[1]) + (a1[2] + a1[3]);
-  v2 = (a2[0] + a2[1]) + (a2[2] + a2[3]);
+  v0 = a0;
+  v1 = a1;
+  v2 = a2;
 }
 
 // Latency-bound: at least four waves per SIMD (at most 128 registers).
+// CDT: dtype of the class logits.  FAST (chosen on the host): class logits
+// present, 1 <= C <= 192 and 1 <= GT_out <= 128, so the row's class logits and
+// the output columns' slots and targets fit in registers and every load of
+// the first two round trips is unconditional (indices clamped into range).
+template <int CDT, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void finalize_kernel(AssignArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's fill gate and finish count
     if (a.gate) *a.gate = 0;
@@ -129,12 +153,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   }
   __shared__ float sl[4][3][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  if (row >= a.L * a.B * a.Q) return;
-  const int64_t lb = row / a.Q, q = row % a.Q, b = lb % a.B;
+  // 32-bit index arithmetic: the host checks L * B * Q < 2^31
+  const uint32_t row32 = blockIdx.x * 4u + (uint32_t)wave;
+  if (row32 >= (uint32_t)(a.L * a.B * a.Q)) return;
+  const uint32_t lb32 = row32 / (uint32_t)a.Q;
+  const int64_t row = row32, lb = lb32, q = row32 - lb32 * (uint32_t)a.Q, b = lb32 % (uint32_t)a.B;
   const int64_t GTo = a.GT_out, C = a.C;
+  const bool labels = FAST || a.cls_logits != nullptr;
+  const int64_t zb = row * C;
+  const int64_t void_idx = a.void_idx;
+  const bool has_void = void_idx >= 0;
+  const bool softmax_bg = a.use_softmax && a.force_cls && has_void;
+
+  // round trip 1: nothing here depends on another load
   const int G = a.ncols[b];
-  const RowPartials rp = row_partials(a.partials, a.sched, a.plan, lb, q, a.rows, a.rtiles, G);
+  const uint32_t rtile = (uint32_t)q / (uint32_t)a.rows;
+  const int qin = (int)((uint32_t)q - rtile * (uint32_t)a.rows);
+  const int64_t task = lb * a.rtiles + rtile;
+  const int64_t tidx = a.sched[2 * kClasses + kClasses * a.plan.ntasks + task];
+  int ksc[kClasses];
+#pragma unroll
+  for (int c = 0; c < kClasses; ++c) ksc[c] = a.sched[kClasses + c];
+  float zc[kFinCls] = {};
+  int oslot[kFinCols] = {};
+  int64_t oy[kFinCols] = {};
+  float zy[kFinCols] = {};
+  float zv = 0.f;
+  if constexpr (FAST) {
+#pragma unroll
+    for (int j = 0; j < kFinCls; ++j) zc[j] = cls_at<CDT>(a.cls_logits, zb + min((int64_t)lane + 64 * j, C - 1));
+#pragma unroll
+    for (int j = 0; j < kFinCols; ++j) {
+      const int64_t cc = min((int64_t)lane + 64 * j, GTo - 1);
+      oslot[j] = a.slot_of_col[b * GTo + cc];
+      oy[j] = a.cls_targets[b * a.GT_total + cc + (cc >= a.bg ? 1 : 0)];
+    }
+    zv = cls_at<CDT>(a.cls_logits, zb + (has_void ? void_idx : 0));
+  } else if (labels && a.use_softmax && has_void) {
+    zv = cls_at<CDT>(a.cls_logits, zb + void_idx);
+  }
+  // (softmax with forced background always has a void index: the host checks it)
+  const bool need_zv = labels && a.use_softmax && has_void;
+
+  // round trip 2: the partials (need the column class) and the targets' logits
+  const int ci = class_of(G + 1);
+  int KS = ksc[0];
+#pragma unroll
+  for (int c = 1; c < kClasses; ++c)
+    if (ci == c) KS = ksc[c];
+  const RowPartials rp = row_partials_at(a.partials, a.plan, ci, tidx, KS, qin, a.rows);
+  if constexpr (FAST) {
+#pragma unroll
+    for (int j = 0; j < kFinCols; ++j) zy[j] = cls_at<CDT>(a.cls_logits, zb + min(max(oy[j], (int64_t)0), C - 1));
+  }
   const int nsl = G + 1;  // GT columns + the ones column
   if (nsl <= 32) {
     // two lanes per slot, each summing every other K-split; fixed-order combine
@@ -158,50 +229,44 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
       sl[wave][2][s] = v2;
     }
   }
-  wave_sync();
-  if (a.rowIT) {  // summed intersection / target mass of every real slot (backward statistics)
-    float2* it = (float2*)a.rowIT + row * a.nslot;
-    for (int s = lane; s < G; s += 64) it[s] = make_float2(sl[wave][1][s], sl[wave][2][s]);
-  }
-  float S = sl[wave][2][G];
-  const float P = sl[wave][1][G];
-  if (!a.normalize) S = (float)(a.Ht * a.Wt);
-  S = fmaxf(S, kEps);
 
   // label row term and unmatched class penalty (none without class logits:
   // the standalone pairwise BCE / dice operators)
-  const bool labels = a.cls_logits != nullptr;
-  const int64_t zb = row * C;
-  const int64_t void_idx = a.void_idx;
-  const bool has_void = void_idx >= 0;
-  const bool softmax_bg = a.use_softmax && a.force_cls && has_void;
+  // f(c, z) over this lane's classes c = lane, lane + 64, ... in that order
+  auto for_cls = [&](auto&& f) {
+    if constexpr (FAST) {
+#pragma unroll
+      for (int j = 0; j < kFinCls; ++j)
+        if (lane + 64 * j < C) f((int64_t)lane + 64 * j, zc[j]);
+    } else {
+      for (int64_t c = lane; c < C; c += 64) f(c, cls_at<CDT>(a.cls_logits, zb + c));
+    }
+  };
   float rowv = 0.f, pen = 0.f;
   if (!labels) {
   } else if (a.use_softmax) {
     float m = -INFINITY;
-    for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_elem(a.cls_logits, a.cls_dtype, zb + c));
+    for_cls([&](int64_t, float z) { m = fmaxf(m, z); });
     m = wave_max(m);
     float se = 0.f;
-    for (int64_t c = lane; c < C; c += 64)
-      se += __expf(cls_elem(a.cls_logits, a.cls_dtype, zb + c) - m);
+    for_cls([&](int64_t, float z) { se += __expf(z - m); });
     se = wave_sum(se);
     rowv = __logf(fmaxf(se, 1e-20f)) + m;
-    if (a.force_cls || has_void) {
-      const float zv = cls_elem(a.cls_logits, a.cls_dtype, zb + void_idx);
+    if (need_zv) {
       // softmax CE towards void when forcing background; otherwise the
       // sigmoid BCE of the void channel (mask_matching_forward.cu:146-218)
       pen = softmax_bg ? (rowv - zv) * a.cls_scale : sig_terms(zv).cp * a.cls_scale;
     }
   } else {
     float base = 0.f, vpos = 0.f, vneg = 0.f;
-    for (int64_t c = lane; c < C; c += 64) {
-      const ClsTerm t = cls_terms(cls_elem(a.cls_logits, a.cls_dtype, zb + c), a.cls_ep);
+    for_cls([&](int64_t c, float z) {
+      const ClsTerm t = cls_terms(z, a.cls_ep);
       base += t.neg;
       if (c == void_idx) {
         vpos = t.pos;
         vneg = t.neg;
       }
-    }
+    });
     base = wave_sum(base);
     vpos = wave_sum(vpos);
     vneg = wave_sum(vneg);
@@ -215,32 +280,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
     }
     pen *= a.cls_scale;
   }
+  wave_sync();
+  if (a.rowIT) {  // summed intersection / target mass of every real slot (backward statistics)
+    float2* it = (float2*)a.rowIT + row * a.nslot;
+    for (int s = lane; s < G; s += 64) it[s] = make_float2(sl[wave][1][s], sl[wave][2][s]);
+  }
+  float S = sl[wave][2][G];
+  const float P = sl[wave][1][G];
+  if (!a.normalize) S = (float)(a.Ht * a.Wt);
+  S = fmaxf(S, kEps);
 
   // all output columns of this row
   const int64_t term = a.L * a.B * a.Q * GTo;
-  (void)term;
-  for (int64_t c = lane; c < GTo; c += 64) {
-    const int slot = a.slot_of_col[b * GTo + c];
+  auto emit = [&](int64_t c, int slot, int64_t y, float zyc) {
     float bce = INFINITY, dice = INFINITY, cls;
     if (slot >= 0) {
       bce = sl[wave][0][slot] / S * a.sigmoid_scale;
       dice = (1.f - (2.f * sl[wave][1][slot] + a.smooth) / (P + sl[wave][2][slot] + a.smooth)) *
              a.dice_scale;
     }
-    const int64_t act = c + (c >= a.bg ? 1 : 0);
-    const int64_t y = labels ? a.cls_targets[b * a.GT_total + act] : 0;
     if (!labels) {
       cls = 0.f;
     } else if (y < 0 || y >= C) {
       cls = INFINITY;
+    } else if (a.use_softmax) {
+      cls = (rowv - zyc) * a.cls_scale;
     } else {
-      const float zy = cls_elem(a.cls_logits, a.cls_dtype, zb + y);
-      if (a.use_softmax) {
-        cls = (rowv - zy) * a.cls_scale;
-      } else {
-        const ClsTerm t = cls_terms(zy, a.cls_ep);
-        cls = (rowv + (t.pos - t.neg)) * (1.f / (float)C) * a.cls_scale;
-      }
+      const ClsTerm t = cls_terms(zyc, a.cls_ep);
+      cls = (rowv + (t.pos - t.neg)) * (1.f / (float)C) * a.cls_scale;
     }
     const int64_t o = row * GTo + c;
     if (a.out_bce) a.out_bce[o] = bce;
@@ -249,6 +316,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
     // total cost, matching.cpp:665, stored [column][query]: the assignment
     // reads cost rows of one GT across all queries
     if (a.tot) a.tot[lb * a.tot_stride + c * a.Q + q] = (bce + dice) + cls;
+  };
+  if constexpr (FAST) {
+#pragma unroll
+    for (int j = 0; j < kFinCols; ++j) {
+      const int64_t c = lane + 64 * j;
+      if (c < GTo) emit(c, oslot[j], oy[j], zy[j]);
+    }
+  } else {
+    for (int64_t c = lane; c < GTo; c += 64) {
+      const int slot = a.slot_of_col[b * GTo + c];
+      const int64_t y = labels ? a.cls_targets[b * a.GT_total + c + (c >= a.bg ? 1 : 0)] : 0;
+      const float zyc = (labels && y >= 0 && y < C) ? cls_at<CDT>(a.cls_logits, zb + y) : 0.f;
+      emit(c, slot, y, zyc);
+    }
   }
   if (lane == 0 && a.rowstat) {
     float mp = 0.f, dp = 0.f;
@@ -956,8 +1037,21 @@ static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
 int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const int64_t rows = d.LB * d.Q;
   if (rows == 0) return ML_OK;
+  if (rows >= ((int64_t)1 << 31)) return fail(ML_EINVAL, "L * B * Q must be below 2^31");
   ProfScope ps_("finalize", st);
-  hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, st, a);
+  const dim3 grid((unsigned)ceil_div(rows, 4));
+  const bool fast = a.cls_logits && a.C >= 1 && a.C <= 64 * kFinCls && a.GT_out >= 1 &&
+                    a.GT_out <= 64 * kFinCols;
+  const int dt = a.cls_logits ? a.cls_dtype : ML_BF16;
+  if (fast) {
+    if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, true>), grid, dim3(256), 0, st, a);
+    else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((finalize_kernel<ML_BF16, true>), grid, dim3(256), 0, st, a);
+  } else {
+    if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, false>), grid, dim3(256), 0, st, a);
+    else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, false>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((finalize_kernel<ML_BF16, false>), grid, dim3(256), 0, st, a);
+  }
   return check_launch("finalize");
 }
 

@@ -84,22 +84,28 @@ struct RowPartials {
   int64_t ks_stride, plane, slot0;
   int KS;
 };
-__device__ inline RowPartials row_partials(const float* partials, const int* sched,
-                                           const CostPlan& plan, int64_t lb, int64_t q,
-                                           int64_t rows, int64_t rtiles, int G) {
-  const int ci = class_of(G + 1);
+// The same from values already loaded: the row's column class ci, the task's
+// index i within that class's list, the class's split count KS and the row's
+// index qin within its row tile.
+__device__ inline RowPartials row_partials_at(const float* partials, const CostPlan& plan, int ci,
+                                              int64_t i, int KS, int qin, int64_t rows) {
   const int64_t nslot_c = 16 * class_nt(ci);
-  const int64_t task = lb * rtiles + q / rows;
-  const int64_t i = sched[2 * kClasses + kClasses * plan.ntasks + task];
-  const int KS = sched[kClasses + ci];
   const int64_t tile = 3 * rows * nslot_c;
   RowPartials r;
   r.KS = KS;
   r.ks_stride = tile;
   r.plane = rows * nslot_c;
-  r.p0 = partials + plan.float_base[ci] + i * KS * tile + (q % rows) * nslot_c;
+  r.p0 = partials + plan.float_base[ci] + i * KS * tile + qin * nslot_c;
   r.slot0 = plan.slot_base[ci] + i * KS;
   return r;
+}
+__device__ inline RowPartials row_partials(const float* partials, const int* sched,
+                                           const CostPlan& plan, int64_t lb, int64_t q,
+                                           int64_t rows, int64_t rtiles, int G) {
+  const int ci = class_of(G + 1);
+  const int64_t task = lb * rtiles + q / rows;
+  const int64_t i = sched[2 * kClasses + kClasses * plan.ntasks + task];
+  return row_partials_at(partials, plan, ci, i, sched[kClasses + ci], (int)(q % rows), rows);
 }
 
 // Derived sizes of one call.

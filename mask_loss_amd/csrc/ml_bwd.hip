@@ -640,17 +640,20 @@ __device__ __forceinline__ void lut_compute_store(const BwdArgs& a, const LutIte
 template <bool CNT>
 __global__ __launch_bounds__(kLutThreads) void bwd_mask_lut_kernel(BwdArgs a, int64_t nchunk) {
   __shared__ float4 lut[2 * kGBlock];
-  if constexpr (CNT) build_grad_lut(lut, a.mask_ep);
-  else build_grad_lut2((float2*)lut, a.mask_ep);
-  __syncthreads();
   const int64_t rows = a.L * a.B * a.Q;
   const int64_t nrows = a.list ? min((int64_t)a.list[0], rows) : rows;
   const int64_t total = nrows * nchunk;
   const bool vec = a.HW % 8 == 0;
   int64_t it = blockIdx.x;
+  // the first item's loads (a chain of round trips: row list, row
+  // statistics, logits) are issued before the table is built, so their
+  // latency overlaps the build
+  LutItem cur, nxt;
+  if (it < total) lut_load<CNT>(a, it, nchunk, vec, cur);
+  if constexpr (CNT) build_grad_lut(lut, a.mask_ep);
+  else build_grad_lut2((float2*)lut, a.mask_ep);
+  __syncthreads();
   if (it < total) {
-    LutItem cur, nxt;
-    lut_load<CNT>(a, it, nchunk, vec, cur);
     for (; it < total; it += gridDim.x) {
       const int64_t it2 = it + gridDim.x;
       if (it2 < total) lut_load<CNT>(a, it2, nchunk, vec, nxt);

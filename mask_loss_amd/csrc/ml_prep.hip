@@ -83,12 +83,16 @@ __device__ __forceinline__ void void_check(const PrepArgs& a, int64_t b) {
   if (threadIdx.x == 0) a.vflag[b] = hit ? 1 : 0;
 }
 
+constexpr int kColsLds = 1024;
+
 // Compacted list of the columns whose GT is non-empty, one wave per image
 // (images w, w + nwaves, ...), then, on wave 0, the cost schedule (per
 // column-tile class: its tasks in ascending order, their count and K-split;
 // per task: its position in its class list).  Run by one workgroup after the
-// target-preparation grid.
+// target-preparation grid.  Column counts of up to kColsLds images stay in
+// LDS for the schedule pass.
 __device__ void columns_and_schedule(const PrepArgs& a) {
+  __shared__ int ncols_s[kColsLds];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const uint64_t below = (1ull << lane) - 1ull;
@@ -105,9 +109,15 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
     // (k0, j) with j = lane & 7 ORs workgroups k0, k0 + 8, ..., then the
     // eight k0 lanes of each word combine
     const int j = lane & (kPresWords - 1);
-    uint32_t pw = 0u;
     const uint32_t* rec = a.pbits + b * a.nblk * kPresWords + j;
-    for (int64_t k = lane >> 3; k < a.nblk; k += 8) pw |= rec[k * kPresWords];
+    uint32_t pq[4] = {0u, 0u, 0u, 0u};  // four records in flight per lane
+    int64_t k = lane >> 3;
+    for (; k + 24 < a.nblk; k += 32) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pq[u] |= rec[(k + 8 * u) * kPresWords];
+    }
+    for (; k < a.nblk; k += 8) pq[0] |= rec[k * kPresWords];
+    uint32_t pw = (pq[0] | pq[1]) | (pq[2] | pq[3]);
     pw |= __shfl_xor(pw, 8, 64);
     pw |= __shfl_xor(pw, 16, 64);
     pw |= __shfl_xor(pw, 32, 64);
@@ -127,7 +137,10 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
       base += __popcll(m);
     }
     for (int s = base + lane; s < a.nslot; s += 64) a.colmap[b * a.nslot + s] = -1;
-    if (lane == 0) a.ncols[b] = base;
+    if (lane == 0) {
+      a.ncols[b] = base;
+      if (b < kColsLds) ncols_s[b] = base;
+    }
   }
   if (!a.sched) return;
   __syncthreads();
@@ -139,7 +152,11 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
   for (int64_t t0 = 0; t0 < nt; t0 += 64) {
     const int64_t t = t0 + lane;
     int ci = -1;
-    if (t < nt) ci = class_of(a.ncols[(t / a.rtiles) % a.B] + 1);
+    if (t < nt) {
+      // 32-bit: the host checks L * B * row tiles < 2^31
+      const uint32_t b = ((uint32_t)t / (uint32_t)a.rtiles) % (uint32_t)a.B;
+      ci = class_of((a.B <= kColsLds ? ncols_s[b] : a.ncols[b]) + 1);
+    }
 #pragma unroll
     for (int c = 0; c < kClasses; ++c) {
       const uint64_t m = __ballot(ci == c);
@@ -261,6 +278,7 @@ int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   int rc;
   if (a.pbits && (a.GT_total > kPresLabels || a.nblk != prep_blocks(d)))
     return fail(ML_EINVAL, "internal: presence records do not fit the preparation grid");
+  if (a.sched && a.plan.ntasks >= ((int64_t)1 << 31)) return fail(ML_EINVAL, "too many row tiles");
   const dim3 grid((unsigned)prep_blocks(d), (unsigned)d.B);
   if (!d.counts_mode) {
     hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);

@@ -67,7 +67,7 @@ struct SmemLayout {
   size_t contrib, colok, vcols, preds, p, way, u, hrows, asg, costL, total;
 };
 
-__host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, bool cost_in_lds) {
+__host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, int64_t lds_rows) {
   SmemLayout s;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -85,7 +85,7 @@ __host__ __device__ inline SmemLayout smem_layout(int64_t Q, int64_t GTo, bool c
   s.hrows = take((Q + 1) * 4);
   s.asg = take((Q + 1) * 4);
   s.costL = o;
-  if (cost_in_lds) take(GTo * Q * 4);
+  if (lds_rows > 0) take(lds_rows * Q * 4);
   s.total = o;
   return s;
 }
@@ -418,8 +418,34 @@ __device__ __forceinline__ double rl_d(const double (&x)[NJ], int t, int l) {
   return r;
 }
 
-template <int NJ>
-__device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds, int n,
+// Cost rows of one image, [column][query] with row stride ldq: rows c < nl
+// in LDS, the others read in place from finalize's total-cost plane (L2).
+// CM, a compile-time choice so that each read is a ds_read or a global load:
+// kCostLds (every row in LDS), kCostGlobal (none), kCostSplit (the first nl).
+enum { kCostGlobal = 0, kCostLds = 1, kCostSplit = 2 };
+typedef __attribute__((address_space(3))) const float lds_f32;     // LDS
+typedef __attribute__((address_space(1))) const float global_f32;  // device memory
+template <int CM>
+struct CostRows {
+  // address-space qualified, so that a row read is a ds_read or a global load
+  // and never a flat load through a pointer chosen at run time
+  const lds_f32* lds;
+  const global_f32* glb;
+  int64_t ldq;
+  int64_t nl;
+  __device__ __forceinline__ bool in_lds(int64_t c) const {
+    return CM == kCostLds || (CM == kCostSplit && c < nl);
+  }
+  // one element (per-lane column): split mode reads the plane in place, where
+  // every row is (the LDS rows are copies), so no read goes through a flat
+  // pointer
+  __device__ __forceinline__ float at(int64_t c, int64_t q) const {
+    return CM == kCostLds ? lds[c * ldq + q] : glb[c * ldq + q];
+  }
+};
+
+template <int NJ, int CM>
+__device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n,
                                const int* hrows, int M, double thr, double BIG, int* p, int* way,
                                double* u, int* asg) {
   (void)p;
@@ -458,10 +484,16 @@ __device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds,
     double ui0 = ucur;
     int col = colcur;
     for (;;) {
-      const float* crow = cost + (int64_t)col * ldq;
       float rawf[NJ];  // all reads issued together (predj is in range for every lane)
+      if (cost.in_lds(col)) {  // wave-uniform
+        const lds_f32* crow = cost.lds + (int64_t)col * cost.ldq;
 #pragma unroll
-      for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+        for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+      } else {
+        const global_f32* crow = cost.glb + (int64_t)col * cost.ldq;
+#pragma unroll
+        for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+      }
       double lmin = INFINITY;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
@@ -556,7 +588,8 @@ __device__ bool hungarian_wave(const float* cost, int64_t ldq, const int* preds,
 
 // Greedy over preds[0..n) with per-column capacities (src/cpu/matching.cpp:193-229).
 // Column order = vcols[0..nv); ties -> earlier column (strict '<').
-__device__ void greedy_wave(const float* cost, int64_t ldq, const int* preds, int n,
+template <int CM>
+__device__ void greedy_wave(const CostRows<CM>& cost, const int* preds, int n,
                             const int* vcols, int nv, int* cap, int* p2g, double thr) {
   const int lane = threadIdx.x & 63;
   for (int k = 0; k < n; ++k) {
@@ -567,7 +600,7 @@ __device__ void greedy_wave(const float* cost, int64_t ldq, const int* preds, in
     for (int t = lane; t < nv; t += 64) {
       const int c = vcols[t];
       if (cap[c] <= 0) continue;
-      const double cv = (double)cost[(int64_t)c * ldq + q];
+      const double cv = (double)cost.at(c, q);
       if (!cost_ok(cv, thr)) continue;
       if (cv < best) {
         best = cv;
@@ -653,22 +686,22 @@ __device__ void layer_pass(const LayerArgs& a) {
   if (threadIdx.x == 0) a.list[0] = base;
 }
 
-// INLDS: the image's cost matrix fits in LDS (else it is read in place from
-// finalize's total-cost plane); a compile-time choice, so cost reads are
-// ds_read (or global) rather than flat loads.
+// CM: where the image's cost rows live (CostRows): all in LDS when the
+// matrix fits, else the first lds_rows columns' rows in LDS and the rest read
+// in place from finalize's total-cost plane.
 // Workgroups L*B .. L*B + fill_blocks - 1 zero-fill the gradient buffer:
 // the assignment keeps one CU per image busy with a serial chain and leaves
 // HBM idle, so the fill runs beside it in the same launch.
 constexpr uint64_t kGateTicks = 3000;  // 30 us of the 100 MHz real-time counter
 
 // Copy the cost rows of image b's non-empty GT columns (colmap order) from
-// finalize's plane into LDS (INLDS) and mark the valid ones (a cost that is
+// finalize's plane into LDS (those CM keeps there) and mark the valid ones (a cost that is
 // finite and below the threshold, cost_ok).  One wave per row, V floats per
 // load (V = 4 when rows start on 16-byte boundaries), R rows per wave in
 // flight; Q <= 64 * NJ, so a lane holds at most KW words of a row.
-template <int V, int NJ, bool INLDS>
+template <int V, int NJ, int CM>
 __device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int64_t b,
-                                           float* costL, int* colok) {
+                                           float* costL, int64_t lds_rows, int* colok) {
   typedef typename std::conditional<V == 4, float4, float>::type word_t;
   constexpr int KW = V == 4 ? (NJ + 3) / 4 : NJ;
   constexpr int R = KW == 1 ? 8 : KW == 2 ? 4 : 2;
@@ -697,7 +730,8 @@ __device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int6
       for (int k = 0; k < KW; ++k) {
         const int j = lane + 64 * k;
         if (j >= W) continue;
-        if constexpr (INLDS) ((word_t*)costL)[(int64_t)col[r] * W + j] = v[r][k];
+        if (CM == kCostLds || (CM == kCostSplit && col[r] < lds_rows))
+          ((word_t*)costL)[(int64_t)col[r] * W + j] = v[r][k];
         const float* e = (const float*)&v[r][k];
 #pragma unroll
         for (int h = 0; h < V; ++h) ok |= cost_ok((double)e[h], a.inf_thresh);
@@ -707,7 +741,7 @@ __device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int6
   }
 }
 
-template <int NJ, bool INLDS>
+template <int NJ, int CM>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   if ((int64_t)blockIdx.x >= a.L * a.B) {
     // Start once every image's cost matrix is staged (the fill's writes would
@@ -724,7 +758,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
     return;
   }
   extern __shared__ __align__(16) unsigned char smem[];
-  const SmemLayout L = smem_layout(a.Q, a.GT_out, INLDS);
+  const SmemLayout L = smem_layout(a.Q, a.GT_out, CM == kCostGlobal ? 0 : a.lds_rows);
   float* contrib = (float*)(smem + L.contrib);
   int* colok = (int*)(smem + L.colok);
   int* vcols = (int*)(smem + L.vcols);
@@ -741,7 +775,12 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   const int64_t lb = blockIdx.x, b = lb % a.B;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t Q = a.Q, GTo = a.GT_out;
-  float* costL = INLDS ? (float*)(smem + L.costL) : a.tot + lb * a.tot_stride;
+  float* costL = (float*)(smem + L.costL);
+  CostRows<CM> crows;
+  crows.lds = (const lds_f32*)costL;
+  crows.glb = (const global_f32*)(a.tot + lb * a.tot_stride);
+  crows.ldq = Q;
+  crows.nl = a.lds_rows;
   const int64_t term = a.L * a.B * Q * GTo;
   const float* sep = a.sep + lb * Q * GTo;
 
@@ -752,8 +791,8 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   //         and its row is never read.
   for (int64_t c = tid; c <= GTo; c += 256) colok[c] = 0;
   __syncthreads();
-  if ((Q & 3) == 0) stage_rows<4, NJ, INLDS>(a, lb, b, costL, colok);
-  else stage_rows<1, NJ, INLDS>(a, lb, b, costL, colok);
+  if ((Q & 3) == 0) stage_rows<4, NJ, CM>(a, lb, b, costL, a.lds_rows, colok);
+  else stage_rows<1, NJ, CM>(a, lb, b, costL, a.lds_rows, colok);
   __syncthreads();
   if (tid == 0 && a.fill_blocks) __hip_atomic_fetch_add(a.gate, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
@@ -788,13 +827,13 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
         const int M = (int)min(reps * (int64_t)nv, Q);
         for (int k = lane; k < M; k += 64) hrows[k] = vcols[k % nv];
         wave_sync();
-        okh = hungarian_wave<NJ>(costL, Q, preds, (int)Q, hrows, M, thr, BIG, pp, way, u, hout);
+        okh = hungarian_wave<NJ>(crows, preds, (int)Q, hrows, M, thr, BIG, pp, way, u, hout);
         if (okh) {
           for (int64_t q = lane; q < Q; q += 64) {
             const int r = hout[q];
             if (r >= 0) {
               const int c = hrows[r];
-              if (cost_ok((double)costL[c * Q + q], thr)) p2g[q] = c;
+              if (cost_ok((double)crows.at(c, q), thr)) p2g[q] = c;
             }
           }
           wave_sync();
@@ -812,7 +851,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
               nr += __popcll(m);
             }
             wave_sync();
-            if (nr > 0) greedy_wave(costL, Q, preds, nr, vcols, nv, cap, p2g, thr);
+            if (nr > 0) greedy_wave(crows, preds, nr, vcols, nv, cap, p2g, thr);
           }
         }
       } else if (a.strategy == ML_ROUND) {
@@ -827,7 +866,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
           if (M == 0 || nrem == 0) break;
           if (M > nrem) M = nrem;
           wave_sync();
-          okh = hungarian_wave<NJ>(costL, Q, preds, nrem, hrows, M, thr, BIG, pp, way, u, hout);
+          okh = hungarian_wave<NJ>(crows, preds, nrem, hrows, M, thr, BIG, pp, way, u, hout);
           if (!okh) break;
           // apply in query order and compact the remaining queries (order kept)
           int nn = 0;
@@ -840,7 +879,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
               const int r = hout[k];
               if (r >= 0) {
                 const int c = hrows[r];
-                if (!cost_ok((double)costL[c * Q + q], thr)) keep = true;
+                if (!cost_ok((double)crows.at(c, q), thr)) keep = true;
                 else p2g[q] = c;
               } else {
                 keep = true;
@@ -864,7 +903,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
           if (nrem == 0) break;
         }
       } else if (a.strategy == ML_GREEDY) {
-        greedy_wave(costL, Q, preds, (int)Q, vcols, nv, cap, p2g, thr);
+        greedy_wave(crows, preds, (int)Q, vcols, nv, cap, p2g, thr);
       }
     }
     if (!okh) {  // no finite augmenting path (invalid costs are BIG): image left unmatched
@@ -873,7 +912,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
     // drop invalid, rank by (cost, q) within each column (matching.cpp:533-565)
     for (int64_t q = lane; q < Q; q += 64) {
       const int c = p2g[q];
-      if (c >= 0 && !cost_ok((double)costL[c * Q + q], thr)) p2g[q] = -1;
+      if (c >= 0 && !cost_ok((double)crows.at(c, q), thr)) p2g[q] = -1;
     }
     wave_sync();
     // compact the matched queries; rank each among those of its column
@@ -893,11 +932,11 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       if (c >= 0) {
         int64_t rank = 0;
         if (K > 1) {
-          const float cq = costL[c * Q + q];
+          const float cq = crows.at(c, q);
           for (int k = 0; k < nm; ++k) {
             const int q2 = mq[k];
             if (q2 == q || p2g[q2] != c) continue;
-            const float c2 = costL[c * Q + q2];
+            const float c2 = crows.at(c, q2);
             if (c2 < cq || (c2 == cq && q2 < q)) ++rank;
           }
         }
@@ -1004,20 +1043,20 @@ __global__ void layer_from_p2g_kernel(const int64_t* p2g, float* layer, int64_t 
   }
 }
 
-size_t assign_smem_bytes(int64_t Q, int64_t GTo, bool cost_in_lds) {
-  return smem_layout(Q, GTo, cost_in_lds).total;
+size_t assign_smem_bytes(int64_t Q, int64_t GTo, int64_t lds_rows) {
+  return smem_layout(Q, GTo, lds_rows).total;
 }
 
-template <int NJ, bool INLDS>
+template <int NJ, int CM>
 static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
-  const size_t sm = smem_layout(a.Q, a.GT_out, INLDS).total;
+  const size_t sm = smem_layout(a.Q, a.GT_out, CM == kCostGlobal ? 0 : a.lds_rows).total;
   static size_t max_dyn = 0;  // 160 KB of LDS less the kernel's static part
   if (max_dyn == 0) {
     hipFuncAttributes fa;
-    if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ, INLDS>) != hipSuccess)
+    if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ, CM>) != hipSuccess)
       return fail(ML_ELAUNCH, "assign: cannot query the kernel attributes");
     const size_t dyn = 160 * 1024 - fa.sharedSizeBytes;
-    if (hipFuncSetAttribute((const void*)assign_kernel<NJ, INLDS>,
+    if (hipFuncSetAttribute((const void*)assign_kernel<NJ, CM>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
       return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
     max_dyn = dyn;
@@ -1025,14 +1064,16 @@ static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
   if (sm > max_dyn) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
   {
     ProfScope ps_("assign", st);
-    hipLaunchKernelGGL((assign_kernel<NJ, INLDS>), dim3((unsigned)(d.LB + a.fill_blocks)),
+    hipLaunchKernelGGL((assign_kernel<NJ, CM>), dim3((unsigned)(d.LB + a.fill_blocks)),
                        dim3(256), sm, st, a);
   }
   return check_launch("assign");
 }
 template <int NJ>
 static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
-  return a.cost_in_lds ? launch_nj_l<NJ, true>(a, d, st) : launch_nj_l<NJ, false>(a, d, st);
+  if (a.lds_rows >= a.GT_out) return launch_nj_l<NJ, kCostLds>(a, d, st);
+  if (a.lds_rows > 0) return launch_nj_l<NJ, kCostSplit>(a, d, st);
+  return launch_nj_l<NJ, kCostGlobal>(a, d, st);
 }
 int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const int64_t rows = d.LB * d.Q;
@@ -1057,9 +1098,14 @@ int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
 
 int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const int64_t nj = ceil_div(a.Q, 64);
+  // one instance per column count up to 6 per lane: the Dijkstra step's work
+  // is proportional to NJ
   if (nj <= 1) return launch_nj<1>(a, d, st);
   if (nj <= 2) return launch_nj<2>(a, d, st);
+  if (nj <= 3) return launch_nj<3>(a, d, st);
   if (nj <= 4) return launch_nj<4>(a, d, st);
+  if (nj <= 5) return launch_nj<5>(a, d, st);
+  if (nj <= 6) return launch_nj<6>(a, d, st);
   if (nj <= 8) return launch_nj<8>(a, d, st);
   if (nj <= 16) return launch_nj<16>(a, d, st);
   return fail(ML_EUNSUPPORTED, "more than 1024 queries per image are not supported");

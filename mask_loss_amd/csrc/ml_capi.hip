@@ -28,7 +28,7 @@ int check_launch(const char* what) {
   return ML_OK;
 }
 
-size_t assign_smem_bytes(int64_t Q, int64_t GTo, bool cost_in_lds);
+size_t assign_smem_bytes(int64_t Q, int64_t GTo, int64_t lds_rows);
 
 // ---- instrumentation ----------------------------------------------------------
 namespace {
@@ -183,9 +183,17 @@ Layout make_layout(const Dims& d, bool force_masks) {
   return L;
 }
 
-static bool cost_fits_lds(const Dims& d) {
-  // 1 KB stays free for the assignment kernel's static LDS
-  return assign_smem_bytes(d.Q, d.GT_out, true) <= kMaxLds - 1024;
+// Cost rows (by column) the assignment keeps in LDS: all GT_out of them when
+// they fit, else as many as fit (the others are read in place from L2).
+// 1 KB stays free for the assignment kernel's static LDS.
+static int64_t cost_lds_rows(const Dims& d) {
+  const size_t budget = kMaxLds - 1024;
+  if (assign_smem_bytes(d.Q, d.GT_out, d.GT_out) <= budget) return d.GT_out;
+  const size_t base = assign_smem_bytes(d.Q, d.GT_out, 0);
+  if (d.Q <= 0 || base + 16 > budget) return 0;
+  int64_t n = (int64_t)((budget - base - 16) / ((size_t)d.Q * 4));
+  while (n > 0 && assign_smem_bytes(d.Q, d.GT_out, n) > budget) --n;
+  return n;
 }
 
 static int check_focal(float gamma, float alpha, const char* who) {
@@ -236,7 +244,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
     return fail(ML_EINVAL, "gradient prefill needs a saved state and unforced unmatched masks");
   if (((uintptr_t)prefill & 15) || ((uintptr_t)saved & 255))
     return fail(ML_EINVAL, "the prefill buffer must be 16-byte and the saved state 256-byte aligned");
-  const bool in_lds = cost_fits_lds(d);
+  const int64_t lds_rows = cost_lds_rows(d);
   const SavedLayout SL = saved_layout(d);
   unsigned char* sv = (unsigned char*)saved;
   float* stats = saved ? (float*)(sv + SL.stats) : nullptr;
@@ -363,7 +371,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.topk = p->topk_matches;
   aa.strategy = (int)p->strategy_id;
   aa.costs_only = costs_only;
-  aa.cost_in_lds = in_lds;
+  aa.lds_rows = lds_rows;
   if (d.LB > 0 && (rc = launch_finalize(aa, d, st))) return rc;
   if (costs_only) return ML_OK;
   // per-layer means and the matched-row list, after the assignment

@@ -261,7 +261,7 @@ struct AssignArgs {
   int64_t topk;
   int strategy;
   int costs_only;
-  int cost_in_lds;
+  int64_t lds_rows;  // cost rows (columns 0 .. lds_rows - 1) the assignment keeps in LDS
 };
 
 

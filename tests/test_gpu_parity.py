@@ -178,6 +178,12 @@ MATCH_CASES = [
          m=dict(force_masks=True, force_cls=True)),
     dict(name="empty_image", kw=dict(empty_image=True), p={}, m=dict(force_cls=True, void=8)),
     dict(name="q_tail_1024", kw=dict(Q=130, H=8, W=8, G=20), p={}, m={}),
+    # cost matrices too large for LDS (300 x 250 floats): the first columns'
+    # rows in LDS, the others read in place
+    dict(name="split_lds_global", kw=dict(Q=300, H=8, W=8, G=250), p={}, m={}),
+    dict(name="split_lds_round_K2", kw=dict(Q=300, H=8, W=8, G=160), p={}, m=dict(K=2, strategy=1)),
+    dict(name="split_lds_pseudo_greedy_K2", kw=dict(Q=300, H=8, W=8, G=200), p={},
+         m=dict(K=2, strategy=3)),
 ]
 
 

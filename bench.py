@@ -195,6 +195,64 @@ def other_config(cfg, dev, steps, warmup):
             "roofline_frac": round(t_roof / (ms * 1e3), 4), "steps": steps, "warmup": warmup}
 
 
+def point_front_end(dev, steps, warmup):
+    """Point-sampling front end at configuration 2's shape: mask logits
+    (1, 8, 100, 128, 128) float32 ~ N(0, 2), label maps (8, 512, 512) from the
+    configuration's recipe, 12,544 points per image (torch.rand).  Times the
+    bilinear point gather alone (HIP events on the launch stream) and one
+    matcher front end: the point-sampled pairwise sigmoid-CE and dice costs
+    (two calls, each sampling the logits and reading targets.max() back, as
+    the reference's functions do)."""
+    import dataclasses
+    import numpy as np
+    import torch
+    from mask_loss_amd import synth
+    from mask_loss_amd.functions import (pairwise_dice_loss_sampling_py,
+                                         pairwise_sigmoid_cross_entropy_loss_sampling_py)
+    ml = mask_loss_amd_module()
+    cfg2 = [c for c in synth.CONFIGS if c.name == "cfg2_point_sampled"][0]
+    cfg = dataclasses.replace(cfg2, H=128, W=128, scale=4)
+    rng = np.random.Generator(np.random.PCG64(cfg.seed))
+    labels, cls_t, _ = synth.make_targets(cfg, rng)
+    t = torch.from_numpy(np.ascontiguousarray(labels)).to(dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    z = torch.randn(cfg.L, cfg.B, cfg.Q, cfg.H, cfg.W, device=dev, generator=g) * cfg.sigma
+    P = 12544
+    coords = torch.rand(cfg.B, P, 2, device=dev, generator=g)
+    # the gather alone
+    for _ in range(warmup):
+        ml.point_sample_masks(z, coords, False)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ml.point_sample_masks(z, coords, False)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    gather_bytes = 4 * cfg.L * cfg.B * cfg.Q * (cfg.H * cfg.W + P)  # planes read once, samples written
+
+    def both():
+        pairwise_sigmoid_cross_entropy_loss_sampling_py(z, t, background_index=0, point_coords=coords)
+        pairwise_dice_loss_sampling_py(z, t, smooth=1.0, background_index=0, point_coords=coords)
+
+    ms = time_steps(both, steps, warmup)
+    return {"workload": "cfg2_point_sampling_front_end", "L": cfg.L, "B": cfg.B, "Q": cfg.Q,
+            "H": cfg.H, "W": cfg.W, "Ht": cfg.H * cfg.scale, "Wt": cfg.W * cfg.scale, "points": P,
+            "dtype": "float32", "ms_per_call": round(ms, 4),
+            "images_per_s": round(cfg.B / (ms * 1e-3), 1),
+            "point_sample": {"avg_us": round(us, 2), "algorithmic_bytes": gather_bytes,
+                             "achieved_GBs": round(gather_bytes / (us * 1e-6) / 1e9, 1),
+                             "frac_of_hbm_peak": round(gather_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+            "steps": steps, "warmup": warmup}
+
+
+def mask_loss_amd_module():
+    import mask_loss_amd
+    return mask_loss_amd.mask_loss
+
+
 def main():
     a = parse()
     if a.copy_calibration:
@@ -282,6 +340,7 @@ def main():
         for oc in synth.CONFIGS:
             if oc.name != cfg.name:
                 others.append(other_config(oc, dev, a.other_steps, a.other_warmup))
+        others.append(point_front_end(dev, a.other_steps, a.other_warmup))
 
     out = {
         "metric": "ms per cost+match+loss fwd/bwd step (B=16,Q=200,256²); % MFMA/HBM roofline",

@@ -29,6 +29,12 @@
  *                                   (bound at src/bindings.cpp:157-158)
  *   ml_dice_loss_forward/backward   src/cuda/dice_loss.cu:159-289
  *                                   (bound at src/bindings.cpp:160-161)
+ *   ml_point_sample                 functions/utils.py:12-20 (point_sample)
+ *   ml_point_labels                 functions/sigmoid/pw_sigmoid_ce.py:497-502
+ *   ml_pairwise_sigmoid_dice_points_forward
+ *                                   functions/sigmoid/pw_sigmoid_ce.py:407-550 and
+ *                                   functions/dice/pw_dice_loss.py:174-268
+ *                                   (the *_sampling_py costs, for given points)
  */
 #ifndef MASK_LOSS_HIP_H
 #define MASK_LOSS_HIP_H
@@ -183,6 +189,45 @@ int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int 
                                      const void* logits, const int64_t* targets,
                                      float* bce_out, float* dice_out, void* workspace,
                                      size_t workspace_bytes, ml_stream_t stream);
+
+/* ---- point-sampling front end (Mask2Former-style matching on sampled points)
+ * ml_point_sample: out[n][c][p] = bilinear sample of input plane (n, c) at
+ *   coords[n % coords_batch][p] = (x, y) in [0, 1], i.e. grid_sample(input,
+ *   2 * coords - 1, mode bilinear, zero padding, align_corners); input
+ *   (N,C,H,W) and out (N,C,P) in `dtype`, coords float (coords_batch,P,2).
+ *   Replaces point_sample, functions/utils.py:12-20 (F.grid_sample), as
+ *   called at functions/sigmoid/pw_sigmoid_ce.py:489-495 and
+ *   functions/dice/pw_dice_loss.py:235-239 (coords shared by every (L, C)
+ *   map of an image: N = L*B, C = queries, coords_batch = B).
+ * ml_point_labels: labels[b][p] = targets[b][iy][ix] with
+ *   ix = clamp(long(x * (Wt-1)), 0, Wt-1) in float32 (NaN -> 0), likewise iy;
+ *   targets (B,Ht,Wt) int64, labels (B,P) int64.  Replaces the nearest-label
+ *   lookup of functions/sigmoid/pw_sigmoid_ce.py:497-502 and
+ *   functions/dice/pw_dice_loss.py:242-245.
+ * ml_pairwise_sigmoid_dice_points_forward: the pairwise sigmoid-BCE / dice
+ *   costs of ml_pairwise_sigmoid_dice_forward over P sampled points:
+ *   point_logits (L,B,C,1,P) in `dtype` (ml_point_sample's output), with
+ *   s->H = s->Ht = 1, s->W = s->Wt = P, s->Q = C, s->GT_total = the label
+ *   slots (the reference: max of the full map + 1); the labels under
+ *   `coords` (B,P,2) in the full map targets (B,Hs,Ws) are the binary
+ *   targets, and a GT is present (finite costs) iff it has a pixel anywhere in
+ *   the full map.  With uncertainty_gamma = 0 and normalize_uncertainty = 0
+ *   this is the reference's pairwise_sigmoid_cross_entropy_loss_sampling_py
+ *   (functions/sigmoid/pw_sigmoid_ce.py:407-550) and
+ *   pairwise_dice_loss_sampling_py (functions/dice/pw_dice_loss.py:174-268)
+ *   for given points.  Workspace from ml_pairwise_points_workspace_size. */
+int ml_point_sample(int dtype, const void* input, const float* coords, int64_t N, int64_t C,
+                    int64_t H, int64_t W, int64_t P, int64_t coords_batch, int align_corners,
+                    void* out, ml_stream_t stream);
+int ml_point_labels(const int64_t* targets, const float* coords, int64_t B, int64_t Ht,
+                    int64_t Wt, int64_t P, int64_t* labels, ml_stream_t stream);
+size_t ml_pairwise_points_workspace_size(const ml_shape* s, const ml_params* p, int dtype,
+                                         int64_t Hs, int64_t Ws);
+int ml_pairwise_sigmoid_dice_points_forward(const ml_shape* s, const ml_params* p, int dtype,
+                                            const void* point_logits, const int64_t* targets,
+                                            int64_t Hs, int64_t Ws, const float* coords,
+                                            float* bce_out, float* dice_out, void* workspace,
+                                            size_t workspace_bytes, ml_stream_t stream);
 
 /* ---- non-pairwise sigmoid-CE and dice losses over dense class logits --------
  * logits (L,B,C,H,W) in `dtype`, targets (B,Ht,Wt) int64 class labels

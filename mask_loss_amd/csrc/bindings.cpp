@@ -422,6 +422,136 @@ torch::Tensor forward_pw_softmax_label_loss(const torch::Tensor& logits,
 }
 
 // --------------------------------------------------------------------------
+// point-sampling front end (functions/utils.py:12-20, the *_sampling_py
+// costs of functions/sigmoid/pw_sigmoid_ce.py:407-550 and
+// functions/dice/pw_dice_loss.py:174-268 for given points)
+// --------------------------------------------------------------------------
+void check_coords(const torch::Tensor& coords, const torch::Tensor& like) {
+  ML_CHECK_INPUT(coords);
+  TORCH_CHECK(coords.scalar_type() == torch::kFloat32, "point coordinates must be float32");
+  TORCH_CHECK(coords.size(-1) == 2, "point coordinates must end in a dimension of size 2 (x, y)");
+  TORCH_CHECK(coords.device() == like.device(), "all tensors must be on the same device");
+}
+
+// (N, C, H, W) planes at (N, P, 2) or (N, Hg, Wg, 2) points -> (N, C, P) or (N, C, Hg, Wg)
+torch::Tensor point_sample(const torch::Tensor& input, const torch::Tensor& coords,
+                           bool align_corners) {
+  ML_CHECK_INPUT(input);
+  check_coords(coords, input);
+  TORCH_CHECK(input.dim() == 4, "point_sample: input must be (N,C,H,W)");
+  TORCH_CHECK(coords.dim() == 3 || coords.dim() == 4, "point_sample: coords must be (N,P,2) or (N,Hg,Wg,2)");
+  TORCH_CHECK(coords.size(0) == input.size(0), "point_sample: batch size mismatch between input and coords");
+  const int64_t N = input.size(0), C = input.size(1), H = input.size(2), W = input.size(3);
+  const int64_t P = coords.dim() == 3 ? coords.size(1) : coords.size(1) * coords.size(2);
+  TORCH_CHECK(H > 0 && W > 0, "point_sample: input must have positive spatial size");
+  auto out = torch::empty({N, C, P}, input.options());
+  ml_ok(ml_point_sample(dtype_code(input, "input"), input.data_ptr(), coords.data_ptr<float>(), N, C,
+                        H, W, P, std::max<int64_t>(N, 1), align_corners ? 1 : 0, out.data_ptr(),
+                        cur_stream()));
+  if (coords.dim() == 4) return out.view({N, C, coords.size(1), coords.size(2)});
+  return out;
+}
+
+// (L, B, Q, H, W) logits at one (B, P, 2) point set per image -> (L, B, Q, P)
+torch::Tensor point_sample_masks(const torch::Tensor& logits, const torch::Tensor& coords,
+                                 bool align_corners) {
+  ML_CHECK_INPUT(logits);
+  check_coords(coords, logits);
+  TORCH_CHECK(logits.dim() == 5, "logits must be (L,B,Q,H,W)");
+  TORCH_CHECK(coords.dim() == 3 && coords.size(0) == logits.size(1),
+              "point coordinates must be (B,P,2) with the logits' batch size");
+  const int64_t L = logits.size(0), B = logits.size(1), Q = logits.size(2);
+  const int64_t H = logits.size(3), W = logits.size(4), P = coords.size(1);
+  TORCH_CHECK(H > 0 && W > 0, "mask_logits must have positive spatial size");
+  auto out = torch::empty({L, B, Q, P}, logits.options());
+  ml_ok(ml_point_sample(dtype_code(logits, "logits"), logits.data_ptr(), coords.data_ptr<float>(),
+                        L * B, Q, H, W, P, std::max<int64_t>(B, 1), align_corners ? 1 : 0,
+                        out.data_ptr(), cur_stream()));
+  return out;
+}
+
+torch::Tensor point_labels(const torch::Tensor& targets, const torch::Tensor& coords) {
+  ML_CHECK_INPUT(targets);
+  check_coords(coords, targets);
+  TORCH_CHECK(targets.dim() == 3, "targets must be (B,H_t,W_t)");
+  TORCH_CHECK(targets.scalar_type() == torch::kLong, "targets must be int64");
+  TORCH_CHECK(coords.dim() == 3 && coords.size(0) == targets.size(0),
+              "point coordinates must be (B,P,2) with the targets' batch size");
+  const int64_t B = targets.size(0), P = coords.size(1);
+  TORCH_CHECK(targets.size(1) > 0 && targets.size(2) > 0, "targets must have positive spatial size");
+  auto out = torch::empty({B, P}, targets.options());
+  ml_ok(ml_point_labels(targets.data_ptr<int64_t>(), coords.data_ptr<float>(), B, targets.size(1),
+                        targets.size(2), P, out.data_ptr<int64_t>(), cur_stream()));
+  return out;
+}
+
+// GT_total = max of the full label map + 1, read back to the host as the
+// reference does (pw_sigmoid_ce.py:466-467, pw_dice_loss.py:209-210).
+torch::Tensor pairwise_points_impl(const torch::Tensor& logits, const torch::Tensor& targets,
+                                   const torch::Tensor& coords, const ml_params& p, bool dice,
+                                   bool align_corners) {
+  ML_CHECK_INPUT(logits);
+  ML_CHECK_INPUT(targets);
+  check_coords(coords, logits);
+  TORCH_CHECK(logits.dim() == 5, "logits must be (L,B,C,H,W)");
+  TORCH_CHECK(targets.dim() == 3, "targets must be (B,H_t,W_t)");
+  TORCH_CHECK(targets.scalar_type() == torch::kLong, "targets must be int64");
+  TORCH_CHECK(targets.size(0) == logits.size(1), "Batch size mismatch between logits and targets");
+  TORCH_CHECK(targets.device() == logits.device(), "all tensors must be on the same device");
+  TORCH_CHECK(coords.dim() == 3 && coords.size(0) == logits.size(1),
+              "point coordinates must be (B,P,2) with the logits' batch size");
+  TORCH_CHECK(coords.size(1) > 0, "num_points must be > 0");
+  TORCH_CHECK(targets.size(1) > 0 && targets.size(2) > 0, "targets must have positive spatial size");
+  const int64_t gt_total =
+      targets.numel() > 0 ? std::max<int64_t>(targets.max().item<int64_t>() + 1, 0) : 0;
+  const int64_t L = logits.size(0), B = logits.size(1), C = logits.size(2), P = coords.size(1);
+  auto f32 = logits.options().dtype(torch::kFloat32);
+  const int64_t GT_out = gt_out_of(gt_total, p.background_index);
+  if (GT_out == 0) return torch::zeros({L, B, C, 0}, f32);
+  auto pts = point_sample_masks(logits, coords, align_corners);  // (L, B, C, P)
+  ml_shape s;
+  s.L = L;
+  s.B = B;
+  s.Q = C;
+  s.H = 1;
+  s.W = P;
+  s.Ht = 1;
+  s.Wt = P;
+  s.C = 0;
+  s.GT_total = gt_total;
+  auto out = torch::empty({L, B, C, GT_out}, f32);
+  const int dt = dtype_code(logits, "logits");
+  const size_t wsb = ml_pairwise_points_workspace_size(&s, &p, dt, targets.size(1), targets.size(2));
+  TORCH_CHECK(wsb > 0 || B == 0, ml_last_error());
+  auto ws = workspace(wsb, logits);
+  ml_ok(ml_pairwise_sigmoid_dice_points_forward(
+      &s, &p, dt, pts.data_ptr(), targets.data_ptr<int64_t>(), targets.size(1), targets.size(2),
+      coords.data_ptr<float>(), dice ? nullptr : out.data_ptr<float>(),
+      dice ? out.data_ptr<float>() : nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
+  return out;
+}
+
+// focal BCE over the points, mean over the points (no uncertainty weights)
+torch::Tensor forward_pw_sigmoid_ce_loss_sampling(const torch::Tensor& logits,
+                                                  const torch::Tensor& targets,
+                                                  const torch::Tensor& coords,
+                                                  int64_t background_index, double scale,
+                                                  double gamma, double alpha, bool align_corners) {
+  ml_params p = make_params(1.0, scale, 1.0, 1.0, background_index, 0.0, 0.0, 1e30, -1.0, false,
+                            false, 1, 0, gamma, alpha, 0.0, -1.0, -1, false, false);
+  return pairwise_points_impl(logits, targets, coords, p, false, align_corners);
+}
+
+torch::Tensor forward_pw_dice_loss_sampling(const torch::Tensor& logits, const torch::Tensor& targets,
+                                            const torch::Tensor& coords, double smooth,
+                                            int64_t background_index, double scale,
+                                            bool align_corners) {
+  ml_params p = make_params(smooth, 1.0, scale, 1.0, background_index, 0.0, 0.0, 1e30, -1.0, false,
+                            false, 1, 0, 0.0, -1.0, 0.0, -1.0, -1, false, false);
+  return pairwise_points_impl(logits, targets, coords, p, true, align_corners);
+}
+
+// --------------------------------------------------------------------------
 // standalone pairwise sigmoid CE / dice  (src/bindings.cpp:159,162)
 // --------------------------------------------------------------------------
 // GT_total = targets.max() + 1, read back to the host as the reference does
@@ -640,6 +770,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_dice_loss", &forward_dice_loss, "Dice loss forward (HIP)");
   m.def("backward_dice_loss", &backward_dice_loss, "Dice loss backward (HIP)");
   m.def("forward_pw_dice_loss", &forward_pw_dice_loss, "Pairwise dice loss forward (HIP)");
+  m.def("point_sample", &point_sample, "Bilinear point sampling, grid_sample semantics (HIP)");
+  m.def("point_sample_masks", &point_sample_masks,
+        "Bilinear point sampling of (L,B,Q,H,W) logits at (B,P,2) points (HIP)");
+  m.def("point_labels", &point_labels, "Labels under (B,P,2) points, floor mapping (HIP)");
+  m.def("forward_pw_sigmoid_ce_loss_sampling", &forward_pw_sigmoid_ce_loss_sampling,
+        "Pairwise sigmoid CE over sampled points (HIP)");
+  m.def("forward_pw_dice_loss_sampling", &forward_pw_dice_loss_sampling,
+        "Pairwise dice loss over sampled points (HIP)");
   m.def("any_equal", &any_equal, "Device flag: any element equal to value (HIP)");
   m.attr("__backend__") = "hip-gfx950";
 }

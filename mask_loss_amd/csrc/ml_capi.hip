@@ -232,7 +232,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                         int64_t* pred_round, float* layer_means, float* sep, void* saved,
                         void* prefill, int32_t* void_found, hipEvent_t void_ready, void* ws,
                         size_t ws_bytes, hipStream_t st, bool costs_only,
-                        float* bce_out = nullptr, float* dice_out = nullptr) {
+                        float* bce_out = nullptr, float* dice_out = nullptr,
+                        const float* pt_coords = nullptr, int64_t pt_Hs = 0, int64_t pt_Ws = 0) {
   if (!dtype_ok(mask_dtype) || (cls_logits && !dtype_ok(cls_dtype)))
     return fail(ML_EINVAL, "unsupported dtype");
   if (!cls_logits && !costs_only) return fail(ML_EINVAL, "matching needs class logits");
@@ -249,7 +250,11 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   unsigned char* sv = (unsigned char*)saved;
   float* stats = saved ? (float*)(sv + SL.stats) : nullptr;
   const Layout L = make_layout(d, force_masks);
-  if (ws_bytes < L.total) return fail(ML_EWORKSPACE, "workspace too small");
+  // point-sampling front end: presence records of the full label map after the layout
+  const size_t pt_pbits = align256(L.total);
+  const int pt_nblk = pt_coords ? prep_blocks_map(pt_Hs, pt_Ws) : 0;
+  const size_t need = pt_coords ? pt_pbits + (size_t)d.B * pt_nblk * kPresWords * 4 : L.total;
+  if (ws_bytes < need) return fail(ML_EWORKSPACE, "workspace too small");
   unsigned char* w = (unsigned char*)ws;
   int rc;
 
@@ -277,7 +282,13 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
   pa.sched = (int*)(w + L.sched);
   pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = plan;
-  if (d.B > 0 && (rc = launch_prep(pa, d, st))) return rc;
+  if (pt_coords) {
+    pa.pbits = (uint32_t*)(w + pt_pbits);
+    pa.nblk = pt_nblk;
+    if (d.B > 0 && (rc = launch_prep_points(pa, d, pt_Hs, pt_Ws, pt_coords, st))) return rc;
+  } else if (d.B > 0 && (rc = launch_prep(pa, d, st))) {
+    return rc;
+  }
   if (void_found && d.B == 0 && (rc = launch_fill_i32(void_found, 0, 1, st))) return rc;
   if (void_ready && hipEventRecord(void_ready, st) != hipSuccess)
     return fail(ML_ELAUNCH, "cannot record the void-check event");
@@ -516,6 +527,57 @@ int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int 
   return forward_impl(s, p, dtype, logits, targets, ML_F32, nullptr, nullptr, nullptr, nullptr,
                       nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, workspace,
                       workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out);
+}
+
+// ---- point-sampling front end ------------------------------------------------
+int ml_point_sample(int dtype, const void* input, const float* coords, int64_t N, int64_t C,
+                    int64_t H, int64_t W, int64_t P, int64_t coords_batch, int align_corners,
+                    void* out, ml_stream_t stream) {
+  if (N < 0 || C < 0 || H <= 0 || W <= 0 || P < 0 || coords_batch <= 0)
+    return fail(ML_EINVAL, "point_sample: invalid shape");
+  if (!dtype_ok(dtype)) return fail(ML_EINVAL, "unsupported dtype");
+  return launch_point_sample(dtype, input, coords, N, C, H, W, P, coords_batch, align_corners, out,
+                             (hipStream_t)stream);
+}
+
+int ml_point_labels(const int64_t* targets, const float* coords, int64_t B, int64_t Ht, int64_t Wt,
+                    int64_t P, int64_t* labels, ml_stream_t stream) {
+  if (B < 0 || Ht <= 0 || Wt <= 0 || P < 0) return fail(ML_EINVAL, "point labels: invalid shape");
+  return launch_point_labels(targets, coords, B, Ht, Wt, P, INT64_MAX, labels, nullptr, 0,
+                             (hipStream_t)stream);
+}
+
+// The sampled-cost shape: s->H = 1, s->W = s->Wt = P (points), s->Ht = 1.
+static bool points_shape_ok(const ml_shape* s, int64_t Hs, int64_t Ws) {
+  return s->H == 1 && s->Ht == 1 && s->W == s->Wt && s->W > 0 && Hs > 0 && Ws > 0;
+}
+
+size_t ml_pairwise_points_workspace_size(const ml_shape* s, const ml_params* p, int dtype,
+                                         int64_t Hs, int64_t Ws) {
+  if (!points_shape_ok(s, Hs, Ws)) return 0;
+  Dims d;
+  std::string err;
+  if (!make_dims(s, p->background_index, dtype, d, err)) return 0;
+  return align256(make_layout(d, false).total) + (size_t)d.B * prep_blocks_map(Hs, Ws) * kPresWords * 4;
+}
+
+int ml_pairwise_sigmoid_dice_points_forward(const ml_shape* s, const ml_params* p, int dtype,
+                                            const void* point_logits, const int64_t* targets,
+                                            int64_t Hs, int64_t Ws, const float* coords,
+                                            float* bce_out, float* dice_out, void* workspace,
+                                            size_t workspace_bytes, ml_stream_t stream) {
+  if (!points_shape_ok(s, Hs, Ws))
+    return fail(ML_EINVAL, "sampled costs: the shape must be (L,B,C,1,P) with a (1,P) target row");
+  if (!coords) return fail(ML_EINVAL, "sampled costs: point coordinates are required");
+  int rc = check_focal(p->mask_gamma, p->mask_alpha, "pairwise sigmoid");
+  if (rc) return rc;
+  if (!(p->uncertainty_gamma >= 0.f))
+    return fail(ML_EINVAL, "uncertainty_gamma must be non-negative");
+  if (!(p->uncertainty_gamma_min >= 0.f && p->uncertainty_gamma_min <= 1.f))
+    return fail(ML_EINVAL, "uncertainty_gamma_min must be in [0, 1]");
+  return forward_impl(s, p, dtype, point_logits, targets, ML_F32, nullptr, nullptr, nullptr,
+                      nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, workspace,
+                      workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out, coords, Hs, Ws);
 }
 
 size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,

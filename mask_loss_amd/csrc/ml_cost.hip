@@ -279,11 +279,13 @@ __device__ __forceinline__ void pace(int* prog, int k) {
 // for unweighted penalties, the row sums to `rs` ([16*RT][2]).  TAB:
 // per-cell planes from the LDS table (bf16 only); if the sums come out NaN,
 // some cell of the K-range hit the table's overflow marker, and the wave
-// redoes the range with the formulas before writing.
-template <int DT, int RT, int NT, bool CNT, bool TAB>
+// redoes the range with the formulas before writing.  `setup` (the
+// workgroup's table build and barrier) is called exactly once on every path,
+// after the first D K-steps of loads are issued, so their latency overlaps it.
+template <int DT, int RT, int NT, bool CNT, bool TAB, class Setup>
 __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
                                           int64_t ks, int64_t KS, const unsigned char* lut,
-                                          float* out, float* rs_out, int* prog) {
+                                          float* out, float* rs_out, int* prog, Setup&& setup) {
   constexpr int NS = InTraits<DT>::kSplit;
   constexpr int D = TAB ? kDepth : 2;  // K-steps of logits and labels in flight
   const int lane = threadIdx.x & 63;
@@ -431,6 +433,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
       fetch_z(j, j);
       fetch_l(j, j);
     }
+    setup();
     int64_t k = 0;
     if constexpr (TAB) {
       // table path, software-pipelined one step deep: the LDS reads of step
@@ -489,6 +492,8 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
         }
       }
     }
+  } else {
+    setup();
   }
 
   bool bad = false;
@@ -613,10 +618,16 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
   const int64_t w0 = (int64_t)blockIdx.x * WV;
   if (w0 >= total) return;  // the whole workgroup is idle
   if (threadIdx.x < WV) prog_s[threadIdx.x] = 0;
-  if constexpr (TAB) build_lut(lut_s, a.ep);
-  __syncthreads();
+  // table build + barrier: once per wave, after its first loads are in flight
+  auto setup = [&]() {
+    if constexpr (TAB) build_lut(lut_s, a.ep);
+    __syncthreads();
+  };
   const int64_t w = w0 + wave;
-  if (w >= total) return;
+  if (w >= total) {
+    setup();
+    return;
+  }
   const int64_t i = w / KS, ks = w % KS;
   const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
@@ -624,7 +635,8 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
   float* out = a.partials + a.plan.float_base[CI] + w * tile;
   float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + w) * (16 * RT) * 2 : nullptr;
   // pace the waves only where many share the workgroup's CU
-  cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs, WV >= 16 ? prog_s : nullptr);
+  cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs, WV >= 16 ? prog_s : nullptr,
+                                  setup);
 }
 
 // ---- launch plan ---------------------------------------------------------------

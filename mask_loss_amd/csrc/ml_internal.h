@@ -338,6 +338,16 @@ int launch_label_cost(const void* cls_logits, int cls_dtype, const int64_t* cls_
                       int use_softmax, float* out, hipStream_t st);
 int launch_fill_i32(int* p, int v, int64_t n, hipStream_t st);
 int prep_blocks(const Dims& d);
+// point-sampling front end (ml_points.hip, ml_prep.hip)
+int prep_blocks_map(int64_t Hs, int64_t Ws);
+int launch_prep_points(const PrepArgs& a, const Dims& d, int64_t Hs, int64_t Ws, const float* coords,
+                       hipStream_t st);
+int launch_point_sample(int dtype, const void* in, const float* coords, int64_t N, int64_t C,
+                        int64_t H, int64_t W, int64_t P, int64_t cb, int align, void* out,
+                        hipStream_t st);
+int launch_point_labels(const int64_t* targets, const float* coords, int64_t B, int64_t Ht,
+                        int64_t Wt, int64_t P, int64_t GT_total, int64_t* out64, uint16_t* out16,
+                        int64_t HWp, hipStream_t st);
 int launch_dense(const DenseArgs& a, bool dice, bool backward, hipStream_t st);
 size_t dense_partials_bytes(int64_t L, int64_t B, int64_t C, int64_t HW, bool dice);
 int launch_zero_fill(void* p, size_t bytes, hipStream_t st);

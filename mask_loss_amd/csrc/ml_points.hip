@@ -1,0 +1,283 @@
+// Point-sampling front end (Mask2Former-style matching on sampled points).
+//
+// * point_sample_kernel: bilinear sampling of (N, C, H, W) planes at P points
+//   per batch entry, the reference's point_sample (functions/utils.py:12-20):
+//   torch.nn.functional.grid_sample with grid = 2 * coords - 1, mode
+//   bilinear, zero padding, align_corners as given.  Batch entry n reads the
+//   coordinates of entry n % coords_batch, so (L, B, Q, H, W) mask logits
+//   sample with one (B, P, 2) point set per image (N = L * B, C = Q), as the
+//   reference's pairwise sampling costs do (functions/sigmoid/pw_sigmoid_ce.py:
+//   489-495, functions/dice/pw_dice_loss.py:235-239).
+// * point_labels_kernel: the label under each point with the reference's
+//   floor mapping ix = clamp(long(x * (W_t - 1)), 0, W_t - 1)
+//   (pw_sigmoid_ce.py:497-502, pw_dice_loss.py:242-245), as int64 and/or as
+//   the u16 compact label row the cost contraction reads (labels outside
+//   [0, GT_total) -> no label).
+//
+// Planes of up to 64 KB are staged in LDS (point_sample_lds_kernel: each
+// plane read from HBM once with coalesced loads, the corners gathered from
+// LDS); larger planes gather their corners straight from memory
+// (point_sample_kernel).  The samples are written along the point index.
+#include <algorithm>
+#include <type_traits>
+
+#include "ml_internal.h"
+
+namespace ml {
+
+template <int DT>
+__device__ __forceinline__ float ld_val(const void* base, int64_t i) {
+  if constexpr (DT == ML_F32) return ((const float*)base)[i];
+  else if constexpr (DT == ML_BF16) return bf16_lo((uint32_t)((const uint16_t*)base)[i]);
+  else return (float)__builtin_bit_cast(_Float16, ((const uint16_t*)base)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void st_val(void* base, int64_t i, float v) {
+  if constexpr (DT == ML_F32) ((float*)base)[i] = v;
+  else if constexpr (DT == ML_BF16) ((uint16_t*)base)[i] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xFFFFu);
+  else ((uint16_t*)base)[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Source index of one grid coordinate g in [-1, 1] along a side of `size`
+// cells (grid_sample's unnormalisation; written without contraction).
+__device__ __forceinline__ float unnormalize(float g, int64_t size, bool align) {
+  const float fs = (float)size;
+  if (align) return __fmul_rn(__fmul_rn(__fadd_rn(g, 1.f), 0.5f), fs - 1.f);
+  return __fmul_rn(__fadd_rn(__fmul_rn(__fadd_rn(g, 1.f), fs), -1.f), 0.5f);
+}
+
+constexpr int kPsThreads = 256;
+constexpr int kPsChan = 8;  // channels per workgroup (grid z)
+
+// grid (ceil(P / 256), N, ceil(C / kPsChan))
+template <int DT>
+__global__ __launch_bounds__(kPsThreads) void point_sample_kernel(const void* in, const float* coords,
+                                                                   int64_t N, int64_t C, int64_t H,
+                                                                   int64_t W, int64_t P, int64_t cb,
+                                                                   int align, void* out) {
+  const int64_t p = (int64_t)blockIdx.x * kPsThreads + threadIdx.x;
+  const int64_t n = blockIdx.y;
+  if (p >= P) return;
+  const float* cp = coords + ((n % cb) * P + p) * 2;
+  const float gx = __fadd_rn(__fmul_rn(2.f, cp[0]), -1.f);
+  const float gy = __fadd_rn(__fmul_rn(2.f, cp[1]), -1.f);
+  const float ix = unnormalize(gx, W, align != 0);
+  const float iy = unnormalize(gy, H, align != 0);
+  float x0f = floorf(ix), y0f = floorf(iy);
+  // corners outside [0, W) x [0, H) read zero; non-finite or far-away
+  // coordinates leave every corner outside (no float -> int overflow)
+  const bool xin = x0f >= -1.f && x0f <= (float)(W - 1);
+  const bool yin = y0f >= -1.f && y0f <= (float)(H - 1);
+  if (!xin) x0f = -2.f;
+  if (!yin) y0f = -2.f;
+  const int64_t x0 = (int64_t)x0f, y0 = (int64_t)y0f;
+  const float x1f = x0f + 1.f, y1f = y0f + 1.f;
+  // weights in grid_sample's form: nw = (x_se - ix) * (y_se - iy), ...
+  const float w_nw = (x1f - ix) * (y1f - iy);
+  const float w_ne = (ix - x0f) * (y1f - iy);
+  const float w_sw = (x1f - ix) * (iy - y0f);
+  const float w_se = (ix - x0f) * (iy - y0f);
+  const bool ok_x0 = xin && x0 >= 0, ok_x1 = xin && x0 + 1 < W;
+  const bool ok_y0 = yin && y0 >= 0, ok_y1 = yin && y0 + 1 < H;
+  const bool k_nw = ok_x0 && ok_y0, k_ne = ok_x1 && ok_y0;
+  const bool k_sw = ok_x0 && ok_y1, k_se = ok_x1 && ok_y1;
+  const int64_t o_nw = y0 * W + x0;
+  const int64_t HW = H * W;
+  const int64_t c0 = (int64_t)blockIdx.z * kPsChan;
+  const int64_t c1 = min(C, c0 + kPsChan);
+  for (int64_t c = c0; c < c1; ++c) {
+    const int64_t base = (n * C + c) * HW + o_nw;
+    // the four corner loads of a channel are independent of the previous
+    // channel's, so consecutive iterations overlap
+    const float v_nw = k_nw ? ld_val<DT>(in, base) : 0.f;
+    const float v_ne = k_ne ? ld_val<DT>(in, base + 1) : 0.f;
+    const float v_sw = k_sw ? ld_val<DT>(in, base + W) : 0.f;
+    const float v_se = k_se ? ld_val<DT>(in, base + W + 1) : 0.f;
+    float acc = 0.f;
+    if (k_nw) acc += v_nw * w_nw;
+    if (k_ne) acc += v_ne * w_ne;
+    if (k_sw) acc += v_sw * w_sw;
+    if (k_se) acc += v_se * w_se;
+    st_val<DT>(out, (n * C + c) * P + p, acc);
+  }
+}
+
+// LDS-staged form for planes that fit: a workgroup reads CPW planes of one
+// batch entry into LDS with coalesced 16-byte loads (each plane from HBM
+// once), then gathers every point's four corners from LDS and writes the
+// samples along the point index.  The corner weights of a point are formed
+// once for its CPW planes.  grid (N * ceil(C / CPW)), dynamic LDS
+// CPW * H * W elements.
+constexpr int kPsLdsThreads = 512;
+constexpr size_t kPsLdsBytes = 64 * 1024;
+
+template <int DT, int CPW>
+__global__ __launch_bounds__(kPsLdsThreads) void point_sample_lds_kernel(
+    const void* in, const float* coords, int64_t N, int64_t C, int64_t H, int64_t W, int64_t P,
+    int64_t cb, int align, void* out) {
+  extern __shared__ __align__(16) unsigned char lds_raw[];
+  using E = typename std::conditional<DT == ML_F32, float, uint16_t>::type;
+  E* plane = (E*)lds_raw;
+  const int64_t ngrp = ceil_div(C, (int64_t)CPW);
+  const int64_t n = blockIdx.x / ngrp;
+  const int64_t c0 = (blockIdx.x % ngrp) * CPW;
+  const int ncp = (int)min((int64_t)CPW, C - c0);
+  const int64_t HW = H * W;
+  // planes c0 .. c0 + ncp - 1 of entry n are contiguous in the input
+  const E* src = (const E*)in + (n * C + c0) * HW;
+  const int64_t total = (int64_t)ncp * HW;
+  constexpr int kPer16 = 16 / sizeof(E);
+  if (((uintptr_t)src & 15) == 0) {
+    const int64_t n16 = total / kPer16;
+    for (int64_t i = threadIdx.x; i < n16; i += kPsLdsThreads) ((uint4*)plane)[i] = ((const uint4*)src)[i];
+    for (int64_t i = n16 * kPer16 + threadIdx.x; i < total; i += kPsLdsThreads) plane[i] = src[i];
+  } else {
+    for (int64_t i = threadIdx.x; i < total; i += kPsLdsThreads) plane[i] = src[i];
+  }
+  __syncthreads();
+  const float* cbase = coords + (n % cb) * P * 2;
+  const bool al = align != 0;
+  for (int64_t p = threadIdx.x; p < P; p += kPsLdsThreads) {
+    const float2 cp = *(const float2*)(cbase + p * 2);
+    const float gx = __fadd_rn(__fmul_rn(2.f, cp.x), -1.f);
+    const float gy = __fadd_rn(__fmul_rn(2.f, cp.y), -1.f);
+    const float ix = unnormalize(gx, W, al);
+    const float iy = unnormalize(gy, H, al);
+    float x0f = floorf(ix), y0f = floorf(iy);
+    const bool xin = x0f >= -1.f && x0f <= (float)(W - 1);
+    const bool yin = y0f >= -1.f && y0f <= (float)(H - 1);
+    if (!xin) x0f = -2.f;
+    if (!yin) y0f = -2.f;
+    const int x0 = (int)x0f, y0 = (int)y0f;
+    const float x1f = x0f + 1.f, y1f = y0f + 1.f;
+    const float w_nw = (x1f - ix) * (y1f - iy);
+    const float w_ne = (ix - x0f) * (y1f - iy);
+    const float w_sw = (x1f - ix) * (iy - y0f);
+    const float w_se = (ix - x0f) * (iy - y0f);
+    const bool ok_x0 = xin && x0 >= 0, ok_x1 = xin && x0 + 1 < W;
+    const bool ok_y0 = yin && y0 >= 0, ok_y1 = yin && y0 + 1 < H;
+    const bool k_nw = ok_x0 && ok_y0, k_ne = ok_x1 && ok_y0;
+    const bool k_sw = ok_x0 && ok_y1, k_se = ok_x1 && ok_y1;
+    // LDS indices, clamped into the plane for corners outside it (their
+    // values are then discarded, not multiplied)
+    const int i_nw = k_nw ? y0 * (int)W + x0 : 0;
+    const int i_ne = k_ne ? y0 * (int)W + x0 + 1 : 0;
+    const int i_sw = k_sw ? (y0 + 1) * (int)W + x0 : 0;
+    const int i_se = k_se ? (y0 + 1) * (int)W + x0 + 1 : 0;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      if (j < ncp) {
+        const E* pl = plane + (int64_t)j * HW;
+        const float v_nw = ld_val<DT>(pl, i_nw), v_ne = ld_val<DT>(pl, i_ne);
+        const float v_sw = ld_val<DT>(pl, i_sw), v_se = ld_val<DT>(pl, i_se);
+        float acc = 0.f;
+        if (k_nw) acc += v_nw * w_nw;
+        if (k_ne) acc += v_ne * w_ne;
+        if (k_sw) acc += v_sw * w_sw;
+        if (k_se) acc += v_se * w_se;
+        st_val<DT>(out, (n * C + c0 + j) * P + p, acc);
+      }
+    }
+  }
+}
+
+template <int DT>
+static int launch_point_sample_lds(const void* in, const float* coords, int64_t N, int64_t C,
+                                   int64_t H, int64_t W, int64_t P, int64_t cb, int align,
+                                   void* out, hipStream_t st) {
+  const size_t eb = DT == ML_F32 ? 4 : 2;
+  const size_t plane = (size_t)H * W * eb;
+  const int64_t fit = (int64_t)(kPsLdsBytes / plane);
+  const int cpw = (int)std::min<int64_t>({4, fit, C});
+  const int64_t blocks = N * ceil_div(C, (int64_t)cpw);
+  if (blocks > INT32_MAX) return fail(ML_EINVAL, "point_sample: too many planes");
+  const size_t lds = (size_t)cpw * plane;
+  const dim3 grid((unsigned)blocks), blk(kPsLdsThreads);
+  switch (cpw) {
+    case 1: hipLaunchKernelGGL((point_sample_lds_kernel<DT, 1>), grid, blk, lds, st, in, coords, N, C, H, W, P, cb, align, out); break;
+    case 2: hipLaunchKernelGGL((point_sample_lds_kernel<DT, 2>), grid, blk, lds, st, in, coords, N, C, H, W, P, cb, align, out); break;
+    case 3: hipLaunchKernelGGL((point_sample_lds_kernel<DT, 3>), grid, blk, lds, st, in, coords, N, C, H, W, P, cb, align, out); break;
+    default: hipLaunchKernelGGL((point_sample_lds_kernel<DT, 4>), grid, blk, lds, st, in, coords, N, C, H, W, P, cb, align, out); break;
+  }
+  return check_launch("point_sample");
+}
+
+int launch_point_sample(int dtype, const void* in, const float* coords, int64_t N, int64_t C,
+                        int64_t H, int64_t W, int64_t P, int64_t cb, int align, void* out,
+                        hipStream_t st) {
+  if (N == 0 || C == 0 || P == 0) return ML_OK;
+  ProfScope ps_("point_sample", st);
+  // planes that fit the workgroup's LDS budget are staged there; larger ones
+  // gather straight from memory
+  const size_t eb = dtype == ML_F32 ? 4 : 2;
+  if ((size_t)H * W * eb <= kPsLdsBytes) {
+    switch (dtype) {
+      case ML_F32: return launch_point_sample_lds<ML_F32>(in, coords, N, C, H, W, P, cb, align, out, st);
+      case ML_BF16: return launch_point_sample_lds<ML_BF16>(in, coords, N, C, H, W, P, cb, align, out, st);
+      default: return launch_point_sample_lds<ML_F16>(in, coords, N, C, H, W, P, cb, align, out, st);
+    }
+  }
+  const int64_t gz = ceil_div(C, kPsChan);
+  if (N > 65535 || gz > 65535) return fail(ML_EINVAL, "point_sample: batch or channel count too large");
+  const dim3 grid((unsigned)ceil_div(P, kPsThreads), (unsigned)N, (unsigned)gz);
+  switch (dtype) {
+    case ML_F32:
+      hipLaunchKernelGGL(point_sample_kernel<ML_F32>, grid, dim3(kPsThreads), 0, st, in, coords, N, C,
+                         H, W, P, cb, align, out);
+      break;
+    case ML_BF16:
+      hipLaunchKernelGGL(point_sample_kernel<ML_BF16>, grid, dim3(kPsThreads), 0, st, in, coords, N,
+                         C, H, W, P, cb, align, out);
+      break;
+    case ML_F16:
+      hipLaunchKernelGGL(point_sample_kernel<ML_F16>, grid, dim3(kPsThreads), 0, st, in, coords, N, C,
+                         H, W, P, cb, align, out);
+      break;
+    default: return fail(ML_EINVAL, "point_sample: unsupported dtype");
+  }
+  return check_launch("point_sample");
+}
+
+// Index of the cell under coordinate x in [0, 1] along a side of `size`
+// cells: long(x * (size - 1)) in float32, truncated toward zero, clamped to
+// [0, size - 1]; NaN maps to 0.
+__device__ __forceinline__ int64_t point_cell(float x, int64_t size) {
+  const float f = __fmul_rn(x, (float)(size - 1));
+  if (!(f > 0.f)) return 0;  // also NaN
+  if (f >= (float)(size - 1)) return size - 1;
+  return (int64_t)f;
+}
+
+// grid (ceil(HWp / 256), B): point p < P writes its label; the padding points
+// [P, HWp) of the u16 row get no label.
+__global__ __launch_bounds__(256) void point_labels_kernel(const int64_t* targets, const float* coords,
+                                                           int64_t Ht, int64_t Wt, int64_t P,
+                                                           int64_t GT_total, int64_t* out64,
+                                                           uint16_t* out16, int64_t HWp) {
+  const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (p < P) {
+    const float* cp = coords + (b * P + p) * 2;
+    const int64_t ix = point_cell(cp[0], Wt), iy = point_cell(cp[1], Ht);
+    const int64_t lab = targets[(b * Ht + iy) * Wt + ix];
+    if (out64) out64[b * P + p] = lab;
+    if (out16)
+      out16[b * HWp + p] = (uint64_t)lab < (uint64_t)GT_total ? (uint16_t)lab : (uint16_t)kNoLabel;
+  } else if (out16 && p < HWp) {
+    out16[b * HWp + p] = (uint16_t)kNoLabel;
+  }
+}
+
+int launch_point_labels(const int64_t* targets, const float* coords, int64_t B, int64_t Ht,
+                        int64_t Wt, int64_t P, int64_t GT_total, int64_t* out64, uint16_t* out16,
+                        int64_t HWp, hipStream_t st) {
+  const int64_t n = out16 ? HWp : P;
+  if (B == 0 || n == 0) return ML_OK;
+  if (B > 65535) return fail(ML_EINVAL, "point labels: too many images");
+  hipLaunchKernelGGL(point_labels_kernel, dim3((unsigned)ceil_div(n, 256), (unsigned)B), dim3(256), 0,
+                     st, targets, coords, Ht, Wt, P, GT_total, out64, out16, HWp);
+  return check_launch("point_labels");
+}
+
+}  // namespace ml

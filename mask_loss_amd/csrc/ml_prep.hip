@@ -222,7 +222,9 @@ __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
         pres_mark(pres, lab[k]);
       prev = lab[k];
     }
-    *(uint4*)(a.lab16 + b * a.HWp + cell0) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    // no label output: a presence-only pass (the point-sampling front end
+    // takes presence from the full label map and labels at the points)
+    if (a.lab16) *(uint4*)(a.lab16 + b * a.HWp + cell0) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
   }
   if (mark) {
     __syncthreads();
@@ -293,6 +295,39 @@ int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
     if ((rc = check_launch("prep_columns"))) return rc;
   }
   return ML_OK;
+}
+
+// Preparation workgroups per image of the presence-only pass over a full
+// (Hs, Ws) label map.
+int prep_blocks_map(int64_t Hs, int64_t Ws) { return (int)ceil_div(ceil_div(Hs * Ws, kStep) * kStep, 256 * 8); }
+
+// Point-sampling front end: GT presence from the full (Hs, Ws) label map (the
+// reference's per-image torch.unique of the whole map,
+// functions/sigmoid/pw_sigmoid_ce.py:476-484), the u16 labels of the cost
+// contraction from the labels under the points (`coords`, (B, P, 2) with
+// P = d.HW), then the column pass and schedule.  `a.pbits` holds
+// [B][prep_blocks_map(Hs, Ws)][kPresWords] words and `a.nblk` that count.
+int launch_prep_points(const PrepArgs& a, const Dims& d, int64_t Hs, int64_t Ws, const float* coords,
+                       hipStream_t st) {
+  ProfScope ps_("prep", st);
+  if (d.counts_mode || d.H != 1 || !a.pbits || !a.lab16)
+    return fail(ML_EINVAL, "internal: point preparation needs a 1 x P grid of labels");
+  if (a.GT_total > kPresLabels || a.nblk != prep_blocks_map(Hs, Ws))
+    return fail(ML_EINVAL, "internal: presence records do not fit the preparation grid");
+  if (a.sched && a.plan.ntasks >= ((int64_t)1 << 31)) return fail(ML_EINVAL, "too many row tiles");
+  if (d.B > 65535) return fail(ML_EINVAL, "too many images");
+  PrepArgs m = a;
+  m.lab16 = nullptr;
+  m.H = Hs;
+  m.W = Ws;
+  m.HWp = ceil_div(Hs * Ws, kStep) * kStep;
+  hipLaunchKernelGGL(prep_labels_kernel, dim3((unsigned)a.nblk, (unsigned)d.B), dim3(256), 0, st, m);
+  int rc = check_launch("prep");
+  if (rc) return rc;
+  rc = launch_point_labels(a.targets, coords, d.B, Hs, Ws, d.HW, a.GT_total, nullptr, a.lab16, d.HWp, st);
+  if (rc) return rc;
+  hipLaunchKernelGGL(prep_columns_kernel, dim3(1), dim3(1024), 0, st, a);
+  return check_launch("prep_columns");
 }
 
 }  // namespace ml

@@ -32,7 +32,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="cfg3_dense_headline")
+    ap.add_argument("--config", default="cfg3_dense_headline",
+                    help="workload of the main line; cfg2_point_sampling_front_end runs only the "
+                         "point-sampling front end")
     ap.add_argument("--cpu-sample-images", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
@@ -268,6 +270,9 @@ def main():
     import mask_loss_amd
     from mask_loss_amd import synth
 
+    if a.config == "cfg2_point_sampling_front_end":  # the front end alone (for profiling)
+        print(json.dumps(point_front_end(torch.device("cuda:0"), a.steps, a.warmup)), flush=True)
+        return
     cfg = synth.BY_NAME[a.config]
     dev = torch.device("cuda:0")
     x, z, zc, step, state = make_step(cfg, dev)

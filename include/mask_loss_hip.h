@@ -29,7 +29,8 @@
  *                                   (bound at src/bindings.cpp:157-158)
  *   ml_dice_loss_forward/backward   src/cuda/dice_loss.cu:159-289
  *                                   (bound at src/bindings.cpp:160-161)
- *   ml_point_sample                 functions/utils.py:12-20 (point_sample)
+ *   ml_point_sample(_backward)      functions/utils.py:12-20 (point_sample, through
+ *                                   F.grid_sample and its input gradient)
  *   ml_point_labels                 functions/sigmoid/pw_sigmoid_ce.py:497-502
  *   ml_pairwise_sigmoid_dice_points_forward
  *                                   functions/sigmoid/pw_sigmoid_ce.py:407-550 and
@@ -219,6 +220,20 @@ int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int 
 int ml_point_sample(int dtype, const void* input, const float* coords, int64_t N, int64_t C,
                     int64_t H, int64_t W, int64_t P, int64_t coords_batch, int align_corners,
                     void* out, ml_stream_t stream);
+/* ml_point_sample_backward: grad_input (N,C,H,W) = the gradient of
+ *   ml_point_sample with respect to its input, for grad_out (N,C,P), both in
+ *   `dtype`: each sample's gradient added to its four corner cells with its
+ *   bilinear weights (grid_sample's input gradient, functions/utils.py:17;
+ *   float atomics, so the last bits depend on their order, as with the
+ *   reference's CUDA grid_sample backward).  Every cell of grad_input is
+ *   written.  Workspace: ml_point_sample_backward_workspace_size bytes (0 when
+ *   a plane's float accumulators fit 64 KB of LDS). */
+size_t ml_point_sample_backward_workspace_size(int dtype, int64_t N, int64_t C, int64_t H,
+                                               int64_t W);
+int ml_point_sample_backward(int dtype, const void* grad_out, const float* coords, int64_t N,
+                             int64_t C, int64_t H, int64_t W, int64_t P, int64_t coords_batch,
+                             int align_corners, void* grad_input, float* workspace,
+                             size_t workspace_bytes, ml_stream_t stream);
 int ml_point_labels(const int64_t* targets, const float* coords, int64_t B, int64_t Ht,
                     int64_t Wt, int64_t P, int64_t* labels, ml_stream_t stream);
 size_t ml_pairwise_points_workspace_size(const ml_shape* s, const ml_params* p, int dtype,

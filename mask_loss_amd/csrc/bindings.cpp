@@ -452,6 +452,29 @@ torch::Tensor point_sample(const torch::Tensor& input, const torch::Tensor& coor
   return out;
 }
 
+// gradient of point_sample with respect to its (N, C, H, W) input
+torch::Tensor point_sample_backward(const torch::Tensor& grad_out, const torch::Tensor& coords,
+                                    int64_t H, int64_t W, bool align_corners) {
+  ML_CHECK_INPUT(grad_out);
+  check_coords(coords, grad_out);
+  TORCH_CHECK(grad_out.dim() == 3 || grad_out.dim() == 4, "point_sample backward: grad must be (N,C,P) or (N,C,Hg,Wg)");
+  TORCH_CHECK(coords.dim() == grad_out.dim() && coords.size(0) == grad_out.size(0),
+              "point_sample backward: coords do not match the gradient");
+  const int64_t N = grad_out.size(0), C = grad_out.size(1);
+  const int64_t P = grad_out.dim() == 3 ? grad_out.size(2) : grad_out.size(2) * grad_out.size(3);
+  const int64_t Pc = coords.dim() == 3 ? coords.size(1) : coords.size(1) * coords.size(2);
+  TORCH_CHECK(P == Pc, "point_sample backward: coords do not match the gradient");
+  TORCH_CHECK(H > 0 && W > 0, "point_sample backward: input must have positive spatial size");
+  const int dt = dtype_code(grad_out, "grad");
+  auto gin = torch::empty({N, C, H, W}, grad_out.options());
+  const size_t wsb = ml_point_sample_backward_workspace_size(dt, N, C, H, W);
+  auto ws = workspace(wsb, grad_out);
+  ml_ok(ml_point_sample_backward(dt, grad_out.data_ptr(), coords.data_ptr<float>(), N, C, H, W, P,
+                                 std::max<int64_t>(N, 1), align_corners ? 1 : 0, gin.data_ptr(),
+                                 wsb ? (float*)ws.data_ptr() : nullptr, wsb, cur_stream()));
+  return gin;
+}
+
 // (L, B, Q, H, W) logits at one (B, P, 2) point set per image -> (L, B, Q, P)
 torch::Tensor point_sample_masks(const torch::Tensor& logits, const torch::Tensor& coords,
                                  bool align_corners) {
@@ -771,6 +794,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("backward_dice_loss", &backward_dice_loss, "Dice loss backward (HIP)");
   m.def("forward_pw_dice_loss", &forward_pw_dice_loss, "Pairwise dice loss forward (HIP)");
   m.def("point_sample", &point_sample, "Bilinear point sampling, grid_sample semantics (HIP)");
+  m.def("point_sample_backward", &point_sample_backward,
+        "Gradient of point_sample with respect to its input (HIP)");
   m.def("point_sample_masks", &point_sample_masks,
         "Bilinear point sampling of (L,B,Q,H,W) logits at (B,P,2) points (HIP)");
   m.def("point_labels", &point_labels, "Labels under (B,P,2) points, floor mapping (HIP)");

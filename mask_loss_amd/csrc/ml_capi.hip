@@ -540,6 +540,24 @@ int ml_point_sample(int dtype, const void* input, const float* coords, int64_t N
                              (hipStream_t)stream);
 }
 
+size_t ml_point_sample_backward_workspace_size(int dtype, int64_t N, int64_t C, int64_t H, int64_t W) {
+  if (N < 0 || C < 0 || H <= 0 || W <= 0 || !dtype_ok(dtype)) return 0;
+  return point_sample_bwd_workspace(dtype, N, C, H, W);
+}
+
+int ml_point_sample_backward(int dtype, const void* grad_out, const float* coords, int64_t N,
+                             int64_t C, int64_t H, int64_t W, int64_t P, int64_t coords_batch,
+                             int align_corners, void* grad_input, float* workspace,
+                             size_t workspace_bytes, ml_stream_t stream) {
+  if (N < 0 || C < 0 || H <= 0 || W <= 0 || P < 0 || coords_batch <= 0)
+    return fail(ML_EINVAL, "point_sample backward: invalid shape");
+  if (!dtype_ok(dtype)) return fail(ML_EINVAL, "unsupported dtype");
+  if (workspace_bytes < point_sample_bwd_workspace(dtype, N, C, H, W))
+    return fail(ML_EWORKSPACE, "workspace too small");
+  return launch_point_sample_backward(dtype, grad_out, coords, N, C, H, W, P, coords_batch,
+                                      align_corners, grad_input, workspace, (hipStream_t)stream);
+}
+
 int ml_point_labels(const int64_t* targets, const float* coords, int64_t B, int64_t Ht, int64_t Wt,
                     int64_t P, int64_t* labels, ml_stream_t stream) {
   if (B < 0 || Ht <= 0 || Wt <= 0 || P < 0) return fail(ML_EINVAL, "point labels: invalid shape");

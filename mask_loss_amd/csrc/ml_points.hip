@@ -239,6 +239,152 @@ int launch_point_sample(int dtype, const void* in, const float* coords, int64_t 
   return check_launch("point_sample");
 }
 
+// ---- gradient with respect to the sampled planes --------------------------------
+// grid_sample's input gradient: every sample's gradient is added to its four
+// corner cells with its bilinear weights (corners outside the plane take
+// nothing).  The additions are float atomics (LDS or global), so the last
+// bits depend on their order, as with the reference's CUDA grid_sample
+// backward, which also adds with atomics.
+struct Corners {
+  int64_t i[4];
+  float w[4];
+  bool k[4];
+};
+
+__device__ __forceinline__ Corners corners_of(const float* cp, int64_t H, int64_t W, bool al) {
+  Corners c;
+  const float gx = __fadd_rn(__fmul_rn(2.f, cp[0]), -1.f);
+  const float gy = __fadd_rn(__fmul_rn(2.f, cp[1]), -1.f);
+  const float ix = unnormalize(gx, W, al);
+  const float iy = unnormalize(gy, H, al);
+  float x0f = floorf(ix), y0f = floorf(iy);
+  const bool xin = x0f >= -1.f && x0f <= (float)(W - 1);
+  const bool yin = y0f >= -1.f && y0f <= (float)(H - 1);
+  if (!xin) x0f = -2.f;
+  if (!yin) y0f = -2.f;
+  const int64_t x0 = (int64_t)x0f, y0 = (int64_t)y0f;
+  const float x1f = x0f + 1.f, y1f = y0f + 1.f;
+  c.w[0] = (x1f - ix) * (y1f - iy);  // nw
+  c.w[1] = (ix - x0f) * (y1f - iy);  // ne
+  c.w[2] = (x1f - ix) * (iy - y0f);  // sw
+  c.w[3] = (ix - x0f) * (iy - y0f);  // se
+  const bool ok_x0 = xin && x0 >= 0, ok_x1 = xin && x0 + 1 < W;
+  const bool ok_y0 = yin && y0 >= 0, ok_y1 = yin && y0 + 1 < H;
+  c.k[0] = ok_x0 && ok_y0;
+  c.k[1] = ok_x1 && ok_y0;
+  c.k[2] = ok_x0 && ok_y1;
+  c.k[3] = ok_x1 && ok_y1;
+  c.i[0] = y0 * W + x0;
+  c.i[1] = c.i[0] + 1;
+  c.i[2] = c.i[0] + W;
+  c.i[3] = c.i[2] + 1;
+  return c;
+}
+
+constexpr int kPsBwdThreads = 512;
+constexpr size_t kPsBwdLdsBytes = 64 * 1024;  // float accumulators of one plane
+
+// One workgroup per plane: accumulate in LDS, then write the plane's
+// gradient in the input dtype (every cell, so no clearing is needed).
+template <int DT>
+__global__ __launch_bounds__(kPsBwdThreads) void point_sample_bwd_lds_kernel(
+    const void* gout, const float* coords, int64_t C, int64_t H, int64_t W, int64_t P, int64_t cb,
+    int align, void* gin) {
+  extern __shared__ __align__(16) float accs[];
+  const int64_t plane = blockIdx.x;
+  const int64_t n = plane / C;
+  const int64_t HW = H * W;
+  for (int64_t i = threadIdx.x; i < HW; i += kPsBwdThreads) accs[i] = 0.f;
+  __syncthreads();
+  const float* cbase = coords + (n % cb) * P * 2;
+  const bool al = align != 0;
+  for (int64_t p = threadIdx.x; p < P; p += kPsBwdThreads) {
+    const float g = ld_val<DT>(gout, plane * P + p);
+    const Corners c = corners_of(cbase + p * 2, H, W, al);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (c.k[q]) atomicAdd(&accs[c.i[q]], c.w[q] * g);
+  }
+  __syncthreads();
+  for (int64_t i = threadIdx.x; i < HW; i += kPsBwdThreads) st_val<DT>(gin, plane * HW + i, accs[i]);
+}
+
+// Planes too large for LDS: float atomics into a zeroed float buffer, then a
+// conversion pass.  grid (ceil(P / 256), N, ceil(C / kPsChan))
+template <int DT>
+__global__ __launch_bounds__(kPsThreads) void point_sample_bwd_global_kernel(
+    const void* gout, const float* coords, int64_t N, int64_t C, int64_t H, int64_t W, int64_t P,
+    int64_t cb, int align, float* acc) {
+  const int64_t p = (int64_t)blockIdx.x * kPsThreads + threadIdx.x;
+  const int64_t n = blockIdx.y;
+  if (p >= P) return;
+  const Corners c = corners_of(coords + ((n % cb) * P + p) * 2, H, W, align != 0);
+  const int64_t c0 = (int64_t)blockIdx.z * kPsChan;
+  const int64_t c1 = min(C, c0 + kPsChan);
+  for (int64_t ch = c0; ch < c1; ++ch) {
+    const float g = ld_val<DT>(gout, (n * C + ch) * P + p);
+    float* a = acc + (n * C + ch) * H * W;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (c.k[q]) unsafeAtomicAdd(&a[c.i[q]], c.w[q] * g);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void f32_to_dtype_kernel(const float* src, void* dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    st_val<DT>(dst, i, src[i]);
+}
+
+size_t point_sample_bwd_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W) {
+  (void)dtype;
+  if ((size_t)H * W * 4 <= kPsBwdLdsBytes) return 0;
+  return (size_t)N * C * H * W * 4;
+}
+
+template <int DT>
+static int launch_bwd_dt(const void* gout, const float* coords, int64_t N, int64_t C, int64_t H,
+                         int64_t W, int64_t P, int64_t cb, int align, void* gin, float* acc,
+                         hipStream_t st) {
+  const int64_t planes = N * C;
+  if ((size_t)H * W * 4 <= kPsBwdLdsBytes) {
+    if (planes > INT32_MAX) return fail(ML_EINVAL, "point_sample backward: too many planes");
+    hipLaunchKernelGGL(point_sample_bwd_lds_kernel<DT>, dim3((unsigned)planes), dim3(kPsBwdThreads),
+                       (size_t)H * W * 4, st, gout, coords, C, H, W, P, cb, align, gin);
+    return check_launch("point_sample_backward");
+  }
+  if (!acc) return fail(ML_EWORKSPACE, "point_sample backward: a float workspace is required");
+  const int64_t total = planes * H * W;
+  int rc = launch_zero_fill(acc, (size_t)total * 4, st);
+  if (rc) return rc;
+  const int64_t gz = ceil_div(C, kPsChan);
+  if (N > 65535 || gz > 65535) return fail(ML_EINVAL, "point_sample: batch or channel count too large");
+  if (P > 0) {
+    hipLaunchKernelGGL(point_sample_bwd_global_kernel<DT>,
+                       dim3((unsigned)ceil_div(P, kPsThreads), (unsigned)N, (unsigned)gz),
+                       dim3(kPsThreads), 0, st, gout, coords, N, C, H, W, P, cb, align, acc);
+    if ((rc = check_launch("point_sample_backward"))) return rc;
+  }
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 8192);
+  hipLaunchKernelGGL(f32_to_dtype_kernel<DT>, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0,
+                     st, acc, gin, total);
+  return check_launch("point_sample_backward");
+}
+
+int launch_point_sample_backward(int dtype, const void* gout, const float* coords, int64_t N,
+                                 int64_t C, int64_t H, int64_t W, int64_t P, int64_t cb, int align,
+                                 void* gin, float* acc, hipStream_t st) {
+  if (N == 0 || C == 0) return ML_OK;
+  ProfScope ps_("point_sample_backward", st);
+  switch (dtype) {
+    case ML_F32: return launch_bwd_dt<ML_F32>(gout, coords, N, C, H, W, P, cb, align, gin, acc, st);
+    case ML_BF16: return launch_bwd_dt<ML_BF16>(gout, coords, N, C, H, W, P, cb, align, gin, acc, st);
+    case ML_F16: return launch_bwd_dt<ML_F16>(gout, coords, N, C, H, W, P, cb, align, gin, acc, st);
+  }
+  return fail(ML_EINVAL, "point_sample backward: unsupported dtype");
+}
+
 // Index of the cell under coordinate x in [0, 1] along a side of `size`
 // cells: long(x * (size - 1)) in float32, truncated toward zero, clamped to
 // [0, size - 1]; NaN maps to 0.

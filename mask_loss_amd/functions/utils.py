@@ -3,8 +3,8 @@
 
 * ``point_sample``: bilinear sampling with ``torch.nn.functional.grid_sample``
   semantics at coordinates in [0, 1] (grid = 2 * coords - 1), zero padding
-  (functions/utils.py:12-20).  Forward only; the sampled values are used by
-  the matching costs, which take no gradient.
+  (functions/utils.py:12-20), differentiable with respect to the sampled
+  input (grid_sample's input gradient; the coordinates take no gradient).
 * ``calculate_uncertainty``: -|logit| (functions/utils.py:6-9).
 * ``get_uncertain_point_coords_with_randomness``: oversampled random points,
   the most uncertain ``importance_sample_ratio * num_points`` of them, plus
@@ -14,9 +14,29 @@
 from __future__ import annotations
 
 import torch
+from torch.autograd import Function
 
 import mask_loss_amd  # noqa: F401  (registers the `mask_loss` extension)
 import mask_loss
+
+
+class PointSampleFunction(Function):
+    """Bilinear point sampling with its input gradient (HIP forward and
+    backward); coordinates are constants."""
+
+    @staticmethod
+    def forward(ctx, input, coords, align_corners):
+        ctx.save_for_backward(coords)
+        ctx.hw = (input.shape[-2], input.shape[-1])
+        ctx.align = bool(align_corners)
+        return mask_loss.point_sample(input, coords, ctx.align)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        (coords,) = ctx.saved_tensors
+        g = mask_loss.point_sample_backward(grad_out.contiguous(), coords, ctx.hw[0], ctx.hw[1],
+                                            ctx.align)
+        return g, None, None
 
 
 def calculate_uncertainty(logits):
@@ -28,7 +48,8 @@ def point_sample(input, point_coords, **kwargs):
     """``input`` (N, C, H, W); ``point_coords`` (N, P, 2) -> (N, C, P), or
     (N, Hg, Wg, 2) -> (N, C, Hg, Wg).  Keyword arguments as grid_sample's:
     ``align_corners`` (default False); only mode="bilinear" and
-    padding_mode="zeros" (grid_sample's defaults) are provided."""
+    padding_mode="zeros" (grid_sample's defaults) are provided.  The result
+    carries the gradient with respect to ``input``."""
     align = bool(kwargs.pop("align_corners", False) or False)
     mode = kwargs.pop("mode", "bilinear")
     padding = kwargs.pop("padding_mode", "zeros")
@@ -36,9 +57,11 @@ def point_sample(input, point_coords, **kwargs):
         raise NotImplementedError("point_sample: only mode='bilinear', padding_mode='zeros'")
     if kwargs:
         raise TypeError(f"point_sample: unexpected arguments {sorted(kwargs)}")
+    if point_coords.requires_grad and torch.is_grad_enabled():
+        raise NotImplementedError("point_sample: no gradient with respect to the coordinates")
+    coords = point_coords.detach().to(dtype=torch.float32).contiguous()
     if input.requires_grad and torch.is_grad_enabled():
-        raise NotImplementedError("point_sample: no gradient with respect to the sampled input")
-    coords = point_coords.to(dtype=torch.float32).contiguous()
+        return PointSampleFunction.apply(input.contiguous(), coords, align)
     return mask_loss.point_sample(input.contiguous(), coords, align)
 
 

@@ -12,7 +12,8 @@ the interpolation and the costs are float64.
 Pinning (tests/test_oracle_points.py): ``grid_sample_bilinear`` against
 ``torch.nn.functional.grid_sample`` on the CPU (float64 inputs and
 coordinates with ``index_dtype=float64``, float32 ones otherwise), including
-zero padding outside the plane; ``point_cells`` against the reference's own
+zero padding outside the plane; ``point_sample_backward`` against torch's
+autograd gradient of the same grid_sample call; ``point_cells`` against the reference's own
 torch expression ``clamp(long(x * (W_t - 1)))`` evaluated by torch;
 ``pairwise_sigmoid_ce_sampling`` / ``pairwise_dice_sampling`` against the
 closed forms at z == 0 (BCE = ln 2 * scale for every present class, dice =
@@ -81,6 +82,38 @@ def point_sample(inp, coords, align_corners=False, index_dtype=np.float32):
     if grid.ndim == 3:
         return grid_sample_bilinear(inp, grid[:, :, None, :], align_corners, index_dtype)[..., 0]
     return grid_sample_bilinear(inp, grid, align_corners, index_dtype)
+
+
+def point_sample_backward(grad_out, coords, H, W, align_corners=False, index_dtype=np.float32):
+    """Gradient of point_sample with respect to its (N, C, H, W) input
+    (grid_sample's input gradient): every sample's gradient added to its four
+    corner cells with the bilinear weights; grad_out (N, C, P) with coords
+    (N, P, 2), or (N, C, Hg, Wg) with coords (N, Hg, Wg, 2).  float64 sums."""
+    g = np.asarray(grad_out, dtype=np.float64)
+    N, C = g.shape[:2]
+    g = g.reshape(N, C, -1)
+    dt = index_dtype
+    c = np.asarray(coords).astype(dt).reshape(N, -1, 2)
+    grid = dt(2.0) * c - dt(1.0)
+    ix = _unnormalize(grid[..., 0], W, align_corners, dt)
+    iy = _unnormalize(grid[..., 1], H, align_corners, dt)
+    with np.errstate(invalid="ignore"):
+        x0 = np.floor(ix)
+        y0 = np.floor(iy)
+    x1 = x0 + dt(1.0)
+    y1 = y0 + dt(1.0)
+    corners = ((x0, y0, (x1 - ix) * (y1 - iy)), (x1, y0, (ix - x0) * (y1 - iy)),
+               (x0, y1, (x1 - ix) * (iy - y0)), (x1, y1, (ix - x0) * (iy - y0)))
+    out = np.zeros((N, C, H * W), dtype=np.float64)
+    for cx, cy, wgt in corners:
+        with np.errstate(invalid="ignore"):
+            ok = np.isfinite(cx) & np.isfinite(cy) & (cx >= 0) & (cx <= W - 1) & (cy >= 0) & (cy <= H - 1)
+        idx = (np.where(ok, cy, 0).astype(np.int64) * W + np.where(ok, cx, 0).astype(np.int64))
+        w64 = np.where(ok, wgt.astype(np.float64), 0.0)
+        for n in range(N):
+            for ch in range(C):
+                np.add.at(out[n, ch], idx[n], w64[n] * g[n, ch])
+    return out.reshape(N, C, H, W)
 
 
 def point_cells(x, size):

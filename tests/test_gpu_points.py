@@ -207,3 +207,73 @@ def test_validation(ml):
     # background only: no GT columns
     out = ml.forward_pw_sigmoid_ce_loss_sampling(z, t, c, 0, 1.0, 0.0, -1.0, False)
     assert out.shape == (1, 2, 3, 0)
+
+
+@pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("H,W", [(9, 13), (130, 140)])
+def test_point_sample_backward(ml, dt, H, W):
+    # (9, 13): float accumulators in LDS; (130, 140): 72.8 KB of float
+    # accumulators, so the global-atomics path with its workspace
+    rng = np.random.default_rng(31 + H)
+    c = coords_with_edges(rng, 3, 777)
+    g64, g = as_dtype(rng.normal(0, 1, size=(3, 5, 777)), dt)
+    got = ml.point_sample_backward(g, torch.from_numpy(c).cuda(), H, W, False)
+    assert got.dtype == TDT[dt] and got.shape == (3, 5, H, W)
+    ref = PO.point_sample_backward(g64, c, H, W, False)
+    # float32 atomics in any order: a few ulps of the cell's largest partial sum
+    close(got.double().cpu().numpy(), ref, SAMPLE_RTOL[dt], np.abs(ref).max())
+
+
+def test_point_sample_autograd_4d_grid(ml):
+    from mask_loss_amd.functions import point_sample
+    rng = np.random.default_rng(4)
+    x64, x = as_dtype(rng.normal(0, 2, size=(2, 3, 11, 6)), "float32")
+    x.requires_grad_(True)
+    c = rng.uniform(-0.1, 1.1, size=(2, 4, 5, 2)).astype(np.float32)
+    out = point_sample(x, torch.from_numpy(c).cuda(), align_corners=True)
+    g = rng.normal(size=out.shape)
+    out.backward(torch.from_numpy(g).float().cuda())
+    ref = PO.point_sample_backward(g, c, 11, 6, True)
+    close(x.grad.double().cpu().numpy(), ref, 1e-5, np.abs(ref).max())
+    with pytest.raises(NotImplementedError, match="coordinates"):
+        point_sample(x, torch.from_numpy(c).cuda().requires_grad_(True))
+
+
+def test_point_sampled_matching_step_gradient_reaches_dense_logits(ml):
+    """Mask2Former-style step: dense logits sampled at the points, the fused
+    cost -> assignment -> loss on the 1 x P map of sampled logits and point
+    labels, backward through the sampling to the dense logits."""
+    from mask_loss_amd.functions import MaskMatchingFunction, point_sample
+    from oracle import mask_oracle as O
+    rng = np.random.default_rng(9)
+    B, Q, h, w, P, C = 2, 24, 16, 12, 600, 7
+    z = rng.normal(0, 2, size=(1, B, Q, h, w)).astype(np.float32)
+    t = np.zeros((B, 64, 48), np.int64)
+    for b in range(B):
+        for g in range(1, 6):
+            y0, x0 = rng.integers(0, 40), rng.integers(0, 30)
+            t[b, y0:y0 + 20, x0:x0 + 16] = g
+    cls_t = np.full((B, 6), -1, np.int64)
+    cls_t[:, 1:] = rng.integers(0, C - 1, size=(B, 5))
+    zc = rng.normal(0, 1, size=(1, B, Q, C)).astype(np.float32)
+    c = rng.uniform(0, 1, size=(B, P, 2)).astype(np.float32)
+    zt = torch.from_numpy(z).cuda().requires_grad_(True)
+    ct = torch.from_numpy(c).cuda()
+    lab = ml.point_labels(torch.from_numpy(t).cuda(), ct).view(B, 1, P)
+    zs = point_sample(zt.view(B, Q, h, w), ct).view(1, B, Q, 1, P)
+    zct = torch.from_numpy(zc).cuda()
+    ctt = torch.from_numpy(cls_t).cuda()
+    p2g, pr, m, d, cl = MaskMatchingFunction.apply(
+        zs, lab, zct, ctt, 1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, True, 1e30, -1.0, True, False, 1,
+        "global", 0.0, None, 0.0, None, C - 1, "softmax")
+    (m.sum() + d.sum() + cl.sum()).backward()
+    assert int((p2g >= 0).sum()) > 0
+    # oracle: the same chain in float64 with the GPU's assignment
+    zs64 = PO.point_sample(z[0].astype(np.float64), c)[None, :, :, None, :]
+    lab64 = PO.point_labels(t, c)[:, None, :]
+    gzs, _ = O.matching_backward(np.ones(1), np.ones(1), np.ones(1), zs64, lab64,
+                                 zc.astype(np.float64), cls_t, p2g.cpu().numpy(),
+                                 background_index=0, force_cls=True, void_class_index=C - 1,
+                                 use_softmax=True)
+    ref = PO.point_sample_backward(gzs[0, :, :, 0, :], c, h, w)[None]
+    close(zt.grad.double().cpu().numpy(), ref, 1e-5, np.abs(ref).max())

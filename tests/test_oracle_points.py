@@ -4,6 +4,8 @@
   CPU (a library routine, the function the reference's point_sample calls,
   functions/utils.py:17), float64 with float64 indices to 1e-12 and float32
   to float32 rounding, inside and outside the plane, both align_corners.
+* point_sample_backward: torch's autograd gradient of the same grid_sample
+  call (float64, both align_corners, points outside the plane).
 * point_cells / point_labels: the reference's own expression
   clamp(long(x * (W_t - 1)), 0, W_t - 1) evaluated by torch in float32,
   including the borders and coordinates outside [0, 1].
@@ -48,6 +50,21 @@ def test_grid_sample_matches_torch_float32_and_4d_grid(align):
                         padding_mode="zeros", align_corners=align).numpy()
     assert got.shape == ref.shape == (2, 3, 6, 7)
     np.testing.assert_allclose(got, ref, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("align", [False, True])
+def test_point_sample_backward_matches_torch_autograd(align):
+    rng = np.random.default_rng(17 + align)
+    H, W = 7, 9
+    inp = torch.from_numpy(rng.normal(size=(2, 3, H, W))).requires_grad_(True)
+    c = _coords(rng, 2, 150, -0.2, 1.2).astype(np.float64)
+    c[0, :3] = [[0, 0], [1, 1], [0.5, 0.25]]
+    out = F.grid_sample(inp, torch.from_numpy(2.0 * c - 1.0)[:, :, None, :], mode="bilinear",
+                        padding_mode="zeros", align_corners=align)[..., 0]
+    g = rng.normal(size=out.shape)
+    out.backward(torch.from_numpy(g))
+    got = PO.point_sample_backward(g, c, H, W, align, index_dtype=np.float64)
+    np.testing.assert_allclose(got, inp.grad.numpy(), rtol=1e-12, atol=1e-12)
 
 
 def test_grid_sample_exact_at_cell_centres():

@@ -204,7 +204,9 @@ def point_front_end(dev, steps, warmup):
     bilinear point gather alone (HIP events on the launch stream) and one
     matcher front end: the point-sampled pairwise sigmoid-CE and dice costs
     (two calls, each sampling the logits and reading targets.max() back, as
-    the reference's functions do)."""
+    the reference's functions do); then configuration 2's Mask2Former-style
+    step on the same points: sampling with its gradient, then the fused
+    cost -> assignment -> loss forward and backward."""
     import dataclasses
     import numpy as np
     import torch
@@ -240,6 +242,29 @@ def point_front_end(dev, steps, warmup):
         pairwise_dice_loss_sampling_py(z, t, smooth=1.0, background_index=0, point_coords=coords)
 
     ms = time_steps(both, steps, warmup)
+
+    # the Mask2Former-style step of configuration 2 on these points: sampled
+    # logits and point labels into the fused cost -> assignment -> loss, with
+    # the backward through the sampling to the dense logits
+    from mask_loss_amd.functions import MaskMatchingFunction, point_sample
+    zd = z.clone().requires_grad_(True)
+    lab = ml.point_labels(t, coords).view(cfg.B, 1, P)
+    zc = torch.randn(cfg.L, cfg.B, cfg.Q, cfg.C + 1, device=dev, generator=g).requires_grad_(True)
+    ct = torch.from_numpy(np.ascontiguousarray(cls_t)).to(dev)
+    ones = [torch.ones(cfg.L, device=dev) for _ in range(3)]
+
+    def match_step():
+        zd.grad = None
+        zc.grad = None
+        zs = point_sample(zd.view(cfg.L * cfg.B, cfg.Q, cfg.H, cfg.W),
+                          coords.repeat(cfg.L, 1, 1)).view(cfg.L, cfg.B, cfg.Q, 1, P)
+        out = MaskMatchingFunction.apply(*synth.call_args(
+            cfg, dict(mask_logits=zs, mask_targets=lab, cls_logits=zc, cls_targets=ct)))
+        torch.autograd.backward(out[2:], ones)
+        match_step.p2g = out[0]
+
+    ms_match = time_steps(match_step, steps, warmup)
+    matched = int((match_step.p2g >= 0).sum().item())
     return {"workload": "cfg2_point_sampling_front_end", "L": cfg.L, "B": cfg.B, "Q": cfg.Q,
             "H": cfg.H, "W": cfg.W, "Ht": cfg.H * cfg.scale, "Wt": cfg.W * cfg.scale, "points": P,
             "dtype": "float32", "ms_per_call": round(ms, 4),
@@ -247,6 +272,11 @@ def point_front_end(dev, steps, warmup):
             "point_sample": {"avg_us": round(us, 2), "algorithmic_bytes": gather_bytes,
                              "achieved_GBs": round(gather_bytes / (us * 1e-6) / 1e9, 1),
                              "frac_of_hbm_peak": round(gather_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+            "matching_step": {"what": "point_sample (autograd) + MaskMatchingFunction fwd/bwd on the "
+                                      "sampled 1 x P map, gradient to the dense logits",
+                              "ms_per_step": round(ms_match, 4),
+                              "images_per_s": round(cfg.B / (ms_match * 1e-3), 1),
+                              "matched": matched},
             "steps": steps, "warmup": warmup}
 
 

@@ -282,6 +282,7 @@ __device__ __forceinline__ Corners corners_of(const float* cp, int64_t H, int64_
 }
 
 constexpr int kPsBwdThreads = 512;
+constexpr int kPsBwdBatch = 8;
 constexpr size_t kPsBwdLdsBytes = 64 * 1024;  // float accumulators of one plane
 
 // One workgroup per plane: accumulate in LDS, then write the plane's
@@ -298,12 +299,28 @@ __global__ __launch_bounds__(kPsBwdThreads) void point_sample_bwd_lds_kernel(
   __syncthreads();
   const float* cbase = coords + (n % cb) * P * 2;
   const bool al = align != 0;
-  for (int64_t p = threadIdx.x; p < P; p += kPsBwdThreads) {
-    const float g = ld_val<DT>(gout, plane * P + p);
-    const Corners c = corners_of(cbase + p * 2, H, W, al);
+  // kPsBwdBatch points per thread per round: their gradient and coordinate
+  // loads are issued together; samples with a zero gradient add nothing (the
+  // rows of unmatched queries are all zero)
+  for (int64_t p0 = 0; p0 < P; p0 += (int64_t)kPsBwdThreads * kPsBwdBatch) {
+    float g[kPsBwdBatch];
+    float2 cp[kPsBwdBatch];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      if (c.k[q]) atomicAdd(&accs[c.i[q]], c.w[q] * g);
+    for (int u = 0; u < kPsBwdBatch; ++u) {
+      const int64_t p = p0 + (int64_t)u * kPsBwdThreads + threadIdx.x;
+      g[u] = p < P ? ld_val<DT>(gout, plane * P + p) : 0.f;
+      cp[u] = p < P ? *(const float2*)(cbase + p * 2) : make_float2(0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kPsBwdBatch; ++u) {
+      if (g[u] != 0.f) {
+        const float c2[2] = {cp[u].x, cp[u].y};
+        const Corners c = corners_of(c2, H, W, al);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (c.k[q]) atomicAdd(&accs[c.i[q]], c.w[q] * g[u]);
+      }
+    }
   }
   __syncthreads();
   for (int64_t i = threadIdx.x; i < HW; i += kPsBwdThreads) st_val<DT>(gin, plane * HW + i, accs[i]);

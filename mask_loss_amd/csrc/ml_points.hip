@@ -244,7 +244,14 @@ int launch_point_sample(int dtype, const void* in, const float* coords, int64_t 
 // corner cells with its bilinear weights (corners outside the plane take
 // nothing).  The additions are float atomics (LDS or global), so the last
 // bits depend on their order, as with the reference's CUDA grid_sample
-// backward, which also adds with atomics.
+// backward, which also adds with atomics.  The atomics bound both forms: on
+// 800 planes of 128 x 128 with 12,544 points and 20% of the rows nonzero, the
+// LDS form takes 146 us against 38 us with plain (racy) adds, and global
+// float atomics into a float buffer take 1.9 ms; samples with a zero
+// gradient are skipped in both.  A deterministic form (the corner entries
+// sorted by cell once per image with a radix sort, then a fixed-order sum per
+// cell) measured 148 us with all-zero gradients and 200 us at 20% nonzero
+// rows: the sort's 18 launches alone take about 110 us.
 struct Corners {
   int64_t i[4];
   float w[4];
@@ -340,6 +347,7 @@ __global__ __launch_bounds__(kPsThreads) void point_sample_bwd_global_kernel(
   const int64_t c1 = min(C, c0 + kPsChan);
   for (int64_t ch = c0; ch < c1; ++ch) {
     const float g = ld_val<DT>(gout, (n * C + ch) * P + p);
+    if (g == 0.f) continue;  // rows of unmatched queries are all zero
     float* a = acc + (n * C + ch) * H * W;
 #pragma unroll
     for (int q = 0; q < 4; ++q)

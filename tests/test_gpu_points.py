@@ -210,17 +210,21 @@ def test_validation(ml):
 
 
 @pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
-@pytest.mark.parametrize("H,W", [(9, 13), (130, 140)])
-def test_point_sample_backward(ml, dt, H, W):
-    # (9, 13): float accumulators in LDS; (130, 140): 72.8 KB of float
-    # accumulators, so the global-atomics path with its workspace
-    rng = np.random.default_rng(31 + H)
-    c = coords_with_edges(rng, 3, 777)
-    g64, g = as_dtype(rng.normal(0, 1, size=(3, 5, 777)), dt)
+@pytest.mark.parametrize("H,W,P", [(9, 13, 777), (130, 140, 777), (9, 13, 17000), (130, 140, 17000)])
+def test_point_sample_backward(ml, dt, H, W, P):
+    # float atomics in LDS for the (9, 13) plane and into a float workspace
+    # for the 72.8 KB (130, 140) plane; P = 17000 gives up to a few hundred
+    # samples per cell of the small plane
+    rng = np.random.default_rng(31 + H + P)
+    c = coords_with_edges(rng, 3, P)
+    g64, g = as_dtype(rng.normal(0, 1, size=(3, 5, P)), dt)
+    g64[1, 2] = 0.0  # an all-zero row (an unmatched query)
+    g[1, 2] = 0
     got = ml.point_sample_backward(g, torch.from_numpy(c).cuda(), H, W, False)
     assert got.dtype == TDT[dt] and got.shape == (3, 5, H, W)
     ref = PO.point_sample_backward(g64, c, H, W, False)
-    # float32 atomics in any order: a few ulps of the cell's largest partial sum
+    assert (got[1, 2] == 0).all()
+    # float32 sums in another order: a few ulps of the cell's largest partial sum
     close(got.double().cpu().numpy(), ref, SAMPLE_RTOL[dt], np.abs(ref).max())
 
 

@@ -115,6 +115,56 @@ def test_dense_workspace_query():
     assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 4, 4, 64, 64)), 1, 0, 0) == 0  # s = 16
 
 
+def test_point_sampling_queries_and_host_tensors_rejected():
+    """The front end's size queries accept only the (L,B,C,1,P) sampled shape
+    and valid planes; its operators reject host tensors (no CPU path)."""
+    import torch
+    if not os.path.exists(LIB):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(LIB)
+
+    class Shape(ctypes.Structure):
+        _fields_ = [(k, ctypes.c_int64) for k in ["L", "B", "Q", "H", "W", "Ht", "Wt", "C", "GT_total"]]
+
+    class Params(ctypes.Structure):
+        _fields_ = [("smooth", ctypes.c_float), ("sigmoid_scale", ctypes.c_float),
+                    ("dice_scale", ctypes.c_float), ("cls_scale", ctypes.c_float),
+                    ("background_index", ctypes.c_int64), ("uncertainty_gamma", ctypes.c_float),
+                    ("uncertainty_gamma_min", ctypes.c_float), ("inf_thresh", ctypes.c_double),
+                    ("num_masks", ctypes.c_double), ("force_cls", ctypes.c_int32),
+                    ("force_masks", ctypes.c_int32), ("topk", ctypes.c_int64),
+                    ("strategy", ctypes.c_int64), ("mask_gamma", ctypes.c_float),
+                    ("mask_alpha", ctypes.c_float), ("cls_gamma", ctypes.c_float),
+                    ("cls_alpha", ctypes.c_float), ("void", ctypes.c_int64),
+                    ("softmax", ctypes.c_int32), ("normalize", ctypes.c_int32)]
+
+    q = lib.ml_pairwise_points_workspace_size
+    q.restype = ctypes.c_size_t
+    q.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    p = Params(1, 1, 1, 1, 0, 0, 0, 1e30, -1, 0, 0, 1, 0, 0, -1, 0, -1, -1, 0, 0)
+    good = Shape(1, 8, 100, 1, 12544, 1, 12544, 0, 51)
+    assert q(ctypes.byref(good), ctypes.byref(p), 0, 512, 512) > 0
+    assert q(ctypes.byref(Shape(1, 8, 100, 2, 12544, 2, 12544, 0, 51)), ctypes.byref(p), 0, 512, 512) == 0
+    assert q(ctypes.byref(good), ctypes.byref(p), 0, 0, 512) == 0
+    b = lib.ml_point_sample_backward_workspace_size
+    b.restype = ctypes.c_size_t
+    b.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
+    assert b(0, 8, 100, 128, 128) == 0                 # float accumulators fit LDS
+    assert b(0, 2, 3, 130, 140) == 2 * 3 * 130 * 140 * 4  # float workspace
+    assert b(7, 2, 3, 130, 140) == 0                   # unknown dtype
+    import mask_loss_amd
+    ml = mask_loss_amd.mask_loss
+    x = torch.zeros(2, 3, 4, 4)
+    c = torch.zeros(2, 5, 2)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.point_sample(x, c, False)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.point_labels(torch.zeros(2, 4, 4, dtype=torch.long), c)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        ml.forward_pw_dice_loss_sampling(torch.zeros(1, 2, 3, 4, 4), torch.zeros(2, 8, 8, dtype=torch.long),
+                                         c, 1.0, -1, 1.0, False)
+
+
 def test_function_validation_errors():
     import torch
     from mask_loss_amd.functions import MaskMatchingFunction

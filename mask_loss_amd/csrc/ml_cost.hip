@@ -263,13 +263,22 @@ __device__ __forceinline__ void planes8_lut(const uint4& x, const unsigned char*
 // it is ahead of the slowest wave of the workgroup (progress values are
 // approximate: no barrier, a stale read only delays the switch).
 constexpr int kPaceSlack = 8;  // K-steps ahead of the slowest wave before yielding
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+// The workgroup has at most 16 waves, so lanes 0..15 (one DPP row) hold every
+// wave's progress and four DPP swaps within the row give their minimum, with
+// no LDS traffic.
 __device__ __forceinline__ void pace(int* prog, int k) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
   if (lane == 0) prog[wave] = k;
   int v = lane < nw ? prog[lane] : 0x7FFFFFFF;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  v = min(v, dpp_i<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = min(v, dpp_i<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = min(v, dpp_i<0x141>(v));  // row_half_mirror
+  v = min(v, dpp_i<0x140>(v));  // row_mirror
   if (__builtin_amdgcn_readfirstlane(v) + kPaceSlack < k) __builtin_amdgcn_s_setprio(0);
   else __builtin_amdgcn_s_setprio(1);
 }
@@ -396,7 +405,9 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
   // first and then refilled with step k + j + D (clamped to the last step, so
   // the loads are unconditional and the wait counts stay exact).  Every
   // branch here is wave-uniform.
-  const int64_t nst = s1 - s0;
+  // step counters in 32 bits: their compares stay scalar (a wave has at most
+  // HW / 32 < 2^31 steps)
+  const int nst = (int)(s1 - s0);
   auto planes = [&](const Raw8<DT> (&raw)[RT], bf16x8_t (&A)[4][RT][NS]) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -419,12 +430,12 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
     Raw8<DT> buf[D][RT];
     uint4 lbuf[D];
     // slot j <- step s0 + min(k, nst - 1): logits, labels
-    auto fetch_z = [&](int j, int64_t k) {
+    auto fetch_z = [&](int j, int k) {
       const int64_t st = s0 + (k < nst ? k : nst - 1);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) load_raw8<DT>(a.logits, rowoff[rt] + st * kStep, buf[j][rt], vec);
     };
-    auto fetch_l = [&](int j, int64_t k) {
+    auto fetch_l = [&](int j, int k) {
       const int64_t st = s0 + (k < nst ? k : nst - 1);
       lbuf[j] = *(const uint4*)(labp + st * kStep);
     };
@@ -434,7 +445,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
       fetch_l(j, j);
     }
     setup();
-    int64_t k = 0;
+    int k = 0;
     if constexpr (TAB) {
       // table path, software-pipelined one step deep: the LDS reads of step
       // k + 1 are issued before the one-hot operands and MFMAs of step k, so
@@ -442,7 +453,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
       uint2 E[RT][8];
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) lut_lookup8(buf[0][rt].w[0], lut, E[rt]);
-      auto step = [&](int j, int64_t kj, bool refill) {
+      auto step = [&](int j, int kj, bool refill) {
         bf16x8_t A[4][RT][NS];
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -460,7 +471,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
         if (refill) fetch_l(j, kj + D);
       };
       for (; k + D <= nst; k += D) {
-        if (prog && (k & (2 * D - 1)) == 0) pace(prog, (int)k);
+        if (prog && (k & (2 * D - 1)) == 0) pace(prog, k);
 #pragma unroll
         for (int j = 0; j < D; ++j) step(j, k + j, true);
       }
@@ -469,7 +480,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
         if (k + j < nst) step(j, k + j, false);
     } else {
       for (; k + D <= nst; k += D) {
-        if (prog && (k & (2 * D - 1)) == 0) pace(prog, (int)k);
+        if (prog && (k & (2 * D - 1)) == 0) pace(prog, k);
 #pragma unroll
         for (int j = 0; j < D; ++j) {
           bf16x8_t A[4][RT][NS];

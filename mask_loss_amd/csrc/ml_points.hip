@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kPsThreads) void point_sample_kernel(const void* in
 // samples along the point index.  The corner weights of a point are formed
 // once for its CPW planes.  grid (N * ceil(C / CPW)), dynamic LDS
 // CPW * H * W elements.
-constexpr int kPsLdsThreads = 512;
+constexpr int kPsLdsThreads = 1024;
 constexpr size_t kPsLdsBytes = 64 * 1024;
 
 template <int DT, int CPW>

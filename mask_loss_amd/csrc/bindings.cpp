@@ -220,16 +220,24 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
     prefill = g.data_ptr();
   }
   const size_t wsb = ml_mask_matching_workspace_size(&s, &p, mdt);
+  TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, ml_last_error());
   auto ws = workspace(wsb, mask_logits);
-  TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, "unsupported shape for mask_matching");
   VoidSlot* vs = check_void ? &void_slot() : nullptr;
   if (vs) *vs->host = -1;
-  ml_ok(ml_mask_matching_forward(
+  const int rc = ml_mask_matching_forward(
       &s, &p, mdt, mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt,
       cls_logits.data_ptr(), cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
       pred_round.data_ptr<int64_t>(), means.data_ptr<float>(), nullptr,
       want_saved ? saved.data_ptr() : nullptr, prefill, vs ? vs->dev : nullptr,
-      nullptr, ws.data_ptr(), ws.numel(), cur_stream()));
+      nullptr, ws.data_ptr(), ws.numel(), cur_stream());
+  if (rc != ML_OK) {
+    // a failure after the first launch leaves kernels queued that may still
+    // write this thread's void word: let them finish before the next call
+    // re-arms it
+    const std::string msg = ml_last_error();
+    if (vs) (void)hipStreamSynchronize((hipStream_t)cur_stream());
+    TORCH_CHECK(false, msg);
+  }
   int32_t void_hit = -1;
   if (vs) void_hit = wait_void_word(*vs, cur_stream());  // the rest of the forward stays queued
   // means follow the logits dtype (src/cuda/mask_matching_forward.cu:580-583);

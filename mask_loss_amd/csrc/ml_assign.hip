@@ -17,6 +17,8 @@
 //   4. pred_round ranking by (cost, query) (src/cpu/matching.cpp:533-565),
 //      per-image matched-loss sums (src/cuda/mask_matching_forward.cu:63-71)
 //      and per-query statistics for the fused backward.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "ml_internal.h"
@@ -1050,18 +1052,30 @@ size_t assign_smem_bytes(int64_t Q, int64_t GTo, int64_t lds_rows) {
 template <int NJ, int CM>
 static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const size_t sm = smem_layout(a.Q, a.GT_out, CM == kCostGlobal ? 0 : a.lds_rows).total;
-  static size_t max_dyn = 0;  // 160 KB of LDS less the kernel's static part
-  if (max_dyn == 0) {
-    hipFuncAttributes fa;
-    if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ, CM>) != hipSuccess)
-      return fail(ML_ELAUNCH, "assign: cannot query the kernel attributes");
-    const size_t dyn = 160 * 1024 - fa.sharedSizeBytes;
-    if (hipFuncSetAttribute((const void*)assign_kernel<NJ, CM>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
-      return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
-    max_dyn = dyn;
+  // 160 KB of LDS less the kernel's static part, raised once per device (the
+  // attribute is set with that device current); the lock makes the first
+  // call of several host threads safe
+  constexpr int kMaxDev = 64;
+  static std::atomic<size_t> max_dyn[kMaxDev];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
+    return fail(ML_ELAUNCH, "assign: no current device (or more than 64)");
+  if (max_dyn[dev].load(std::memory_order_acquire) == 0) {
+    std::lock_guard<std::mutex> g(mu);
+    if (max_dyn[dev].load(std::memory_order_relaxed) == 0) {
+      hipFuncAttributes fa;
+      if (hipFuncGetAttributes(&fa, (const void*)assign_kernel<NJ, CM>) != hipSuccess)
+        return fail(ML_ELAUNCH, "assign: cannot query the kernel attributes");
+      const size_t dyn = 160 * 1024 - fa.sharedSizeBytes;
+      if (hipFuncSetAttribute((const void*)assign_kernel<NJ, CM>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
+        return fail(ML_ELAUNCH, "assign: cannot raise the LDS limit");
+      max_dyn[dev].store(dyn, std::memory_order_release);
+    }
   }
-  if (sm > max_dyn) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
+  const size_t max_dyn_dev = max_dyn[dev].load(std::memory_order_acquire);
+  if (sm > max_dyn_dev) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
   {
     ProfScope ps_("assign", st);
     hipLaunchKernelGGL((assign_kernel<NJ, CM>), dim3((unsigned)(d.LB + a.fill_blocks)),

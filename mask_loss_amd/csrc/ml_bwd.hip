@@ -96,7 +96,7 @@ __device__ __forceinline__ void load8_any(const void* base, int dt, int64_t i, i
 // target count of label `act` for 8 cells starting at cell0
 __device__ __forceinline__ void target8(const BwdArgs& a, int64_t b, int64_t act, int64_t cell0,
                                         float t[8]) {
-  if (a.counts8 == nullptr) {
+  if (a.counts == nullptr) {
     const uint4 lv = *(const uint4*)(a.lab16 + b * a.HWp + cell0);
     const uint32_t w[4] = {lv.x, lv.y, lv.z, lv.w};
 #pragma unroll
@@ -105,10 +105,7 @@ __device__ __forceinline__ void target8(const BwdArgs& a, int64_t b, int64_t act
       t[2 * k + 1] = (int64_t)(w[k] >> 16) == act ? 1.f : 0.f;
     }
   } else {
-    const uint2 cv = *(const uint2*)(a.counts8 + (b * a.GT_total + act) * a.HWp + cell0);
-    const uint32_t w[2] = {cv.x, cv.y};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) t[k] = (float)((w[k >> 2] >> ((k & 3) * 8)) & 0xFF);
+    counts8_f(a.counts, a.cw, (b * a.GT_total + act) * a.HWp + cell0, t);
   }
 }
 
@@ -503,7 +500,7 @@ struct LutItem {
   int64_t out;           // pred_to_gt of the row
   float S, P, I, T, mc, dc;
   uint4 z[kLutU];        // 8 bf16 logits per group
-  uint4 lab[kLutU];      // 8 u16 labels (s == 1) or 8 u8 counts in .x/.y (s > 1)
+  uint4 lab[kLutU];      // 8 u16 labels (s == 1), 8 u8 counts in .x/.y or 8 u16 counts (s > 1)
 };
 
 template <bool CNT>
@@ -548,8 +545,13 @@ __device__ __forceinline__ void lut_load(const BwdArgs& a, int64_t it, int64_t n
         m.z[u] = make_uint4(w[0], w[1], w[2], w[3]);
       }
       if constexpr (CNT) {
-        const uint2 cv = *(const uint2*)(a.counts8 + (b * a.GT_total + actc) * a.HWp + c);
-        m.lab[u] = make_uint4(cv.x, cv.y, 0, 0);
+        const int64_t e = (b * a.GT_total + actc) * a.HWp + c;
+        if (a.cw == 1) {
+          const uint2 cv = *(const uint2*)(a.counts + e);
+          m.lab[u] = make_uint4(cv.x, cv.y, 0, 0);
+        } else {
+          m.lab[u] = *(const uint4*)(a.counts + 2 * e);
+        }
       } else {
         m.lab[u] = *(const uint4*)(a.lab16 + b * a.HWp + c);
       }
@@ -586,8 +588,12 @@ __device__ __forceinline__ void lut_compute_store(const BwdArgs& a, const LutIte
     float t[8];
     if constexpr (CNT) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
-        t[k] = matched ? (float)(((k < 4 ? m.lab[u].x : m.lab[u].y) >> ((k & 3) * 8)) & 0xFFu) : 0.f;
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t lw[4] = {m.lab[u].x, m.lab[u].y, m.lab[u].z, m.lab[u].w};
+        const uint32_t n = a.cw == 1 ? (lw[k >> 2] >> ((k & 3) * 8)) & 0xFFu
+                                     : (lw[k >> 1] >> ((k & 1) * 16)) & 0xFFFFu;
+        t[k] = matched ? (float)n : 0.f;
+      }
     } else {
       const uint32_t lw[4] = {m.lab[u].x, m.lab[u].y, m.lab[u].z, m.lab[u].w};
 #pragma unroll

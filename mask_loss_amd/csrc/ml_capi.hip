@@ -98,8 +98,8 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
     return false;
   }
   d.s = d.Ht / d.H;
-  if (d.s > 15) {
-    err = "target/logit scale factor above 15 overflows the per-cell uint8 counts";
+  if (d.s > 255) {
+    err = "target/logit scale factors above 255 are not supported (per-cell counts are 16-bit)";
     return false;
   }
   if (d.GT_total > 65535) {
@@ -129,6 +129,7 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
   const int64_t nsteps = ceil_div(d.HW, kStep);
   d.ks_max = nsteps / 8 > 1 ? nsteps / 8 : 1;
   d.counts_mode = d.s > 1;
+  d.cw = d.s >= 16 ? 2 : 1;  // u8 counts overflow at s*s >= 256
   return true;
 }
 
@@ -161,7 +162,7 @@ Layout make_layout(const Dims& d, bool force_masks) {
     return r;
   };
   L.lab16 = take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2);
-  L.counts8 = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0);
+  L.counts = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp * d.cw : 0);
   L.pbits = take((size_t)d.B * prep_blocks(d) * kPresWords * 4);
   L.vflag = take((size_t)d.B * 4);
   L.ncols = take((size_t)d.B * 4);
@@ -181,6 +182,22 @@ Layout make_layout(const Dims& d, bool force_masks) {
   L.gate = take(16);
   L.total = o;
   return L;
+}
+
+// Shapes the assignment launch supports, checked before anything is queued:
+// one wave holds a cost row of at most 1024 queries in registers (16 per
+// lane), and the workgroup's per-query arrays must fit the LDS without any
+// cost row.
+static bool check_assign_dims(const Dims& d, std::string& err) {
+  if (d.Q > 1024) {
+    err = "more than 1024 queries per image are not supported by the assignment";
+    return false;
+  }
+  if (assign_smem_bytes(d.Q, d.GT_out, 0) > kMaxLds - 1024) {
+    err = "assign: the per-query arrays exceed the LDS budget";
+    return false;
+  }
+  return true;
 }
 
 // Cost rows (by column) the assignment keeps in LDS: all GT_out of them when
@@ -240,6 +257,7 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   Dims d;
   std::string err;
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
+  if (!costs_only && !check_assign_dims(d, err)) return fail(ML_EUNSUPPORTED, err);
   const bool force_masks = !costs_only && p->force_unmatched_masks_to_empty;
   if (prefill && (force_masks || costs_only || !saved))
     return fail(ML_EINVAL, "gradient prefill needs a saved state and unforced unmatched masks");
@@ -264,7 +282,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.targets = mask_targets;
   // with a saved state the compact labels go straight into it (the backward reuses them)
   pa.lab16 = (uint16_t*)(saved && !d.counts_mode ? sv + SL.lab16 : w + L.lab16);
-  pa.counts8 = (uint8_t*)(w + L.counts8);
+  pa.counts = (uint8_t*)(w + L.counts);
+  pa.cw = d.cw;
   pa.pbits = (uint32_t*)(w + L.pbits);
   pa.nblk = prep_blocks(d);
   pa.vflag = (int*)(w + L.vflag);
@@ -298,7 +317,8 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   CostArgs ca;
   ca.logits = mask_logits;
   ca.lab16 = pa.lab16;
-  ca.counts8 = d.counts_mode ? pa.counts8 : nullptr;
+  ca.counts = d.counts_mode ? pa.counts : nullptr;
+  ca.cw = d.cw;
   ca.ncols = pa.ncols;
   ca.colmap = pa.colmap;
   ca.sched = pa.sched;
@@ -468,14 +488,15 @@ int ml_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, ml_s
 size_t ml_saved_bytes(const ml_shape* s, const ml_params* p, int mask_dtype) {
   Dims d;
   std::string err;
-  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(0, err);
   return saved_layout(d).total;
 }
 
 size_t ml_mask_matching_workspace_size(const ml_shape* s, const ml_params* p, int mask_dtype) {
   Dims d;
   std::string err;
-  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err) || !check_assign_dims(d, err))
+    return fail(0, err);
   return make_layout(d, p->force_unmatched_masks_to_empty != 0).total;
 }
 
@@ -483,7 +504,7 @@ size_t ml_pairwise_mask_loss_workspace_size(const ml_shape* s, const ml_params* 
                                             int mask_dtype) {
   Dims d;
   std::string err;
-  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(0, err);
   return make_layout(d, false).total;
 }
 
@@ -605,7 +626,7 @@ size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_para
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return 0;
   size_t o = 0;
   o = align256(o + (d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
-  o = align256(o + (d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
+  o = align256(o + (d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp * d.cw : 0));
   o = align256(o + (size_t)d.B * 4);                // ncols
   o = align256(o + (size_t)d.B * d.nslot * 4);      // colmap
   o = align256(o + (size_t)d.B * d.GT_out * 4);     // slot_of_col
@@ -643,7 +664,8 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   };
   PrepArgs pa;
   pa.lab16 = (uint16_t*)(w + take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2));
-  pa.counts8 = (uint8_t*)(w + take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp : 0));
+  pa.counts = (uint8_t*)(w + take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp * d.cw : 0));
+  pa.cw = d.cw;
   pa.pbits = nullptr;  // labels only
   pa.ncols = (int*)(w + take((size_t)d.B * 4));
   pa.colmap = (int*)(w + take((size_t)d.B * d.nslot * 4));
@@ -676,7 +698,8 @@ int ml_mask_matching_backward(const ml_shape* s, const ml_params* p, const float
   ba.logits = mask_logits;
   ba.dtype = mask_dtype;
   ba.lab16 = d.counts_mode ? nullptr : pa.lab16;
-  ba.counts8 = d.counts_mode ? pa.counts8 : nullptr;
+  ba.counts = d.counts_mode ? pa.counts : nullptr;
+  ba.cw = d.cw;
   ba.pred_to_gt = pred_to_gt;
   ba.stats = stats;
   ba.list = grad_prefilled ? (const int*)(sv + SL.list) : nullptr;
@@ -728,8 +751,8 @@ bool dense_plan(const ml_dense_shape* s, bool dice, bool backward, DensePlan& P,
     return false;
   }
   d.s = d.Ht / d.H;
-  if (d.s > 15) {
-    err = "target/logit scale factor above 15 overflows the per-cell uint8 counts";
+  if (d.s > 255) {
+    err = "target/logit scale factors above 255 are not supported (per-cell counts are 16-bit)";
     return false;
   }
   if (d.C > 65535) {
@@ -741,7 +764,8 @@ bool dense_plan(const ml_dense_shape* s, bool dice, bool backward, DensePlan& P,
   d.HW = d.H * d.W;
   d.HWp = ceil_div(d.HW, kStep) * kStep;
   d.counts_mode = d.s > 1;
-  P.tgt_bytes = align256(d.counts_mode ? (size_t)d.B * d.C * d.HWp : (size_t)d.B * d.HWp * 2);
+  d.cw = d.s >= 16 ? 2 : 1;
+  P.tgt_bytes = align256(d.counts_mode ? (size_t)d.B * d.C * d.HWp * d.cw : (size_t)d.B * d.HWp * 2);
   P.partial_off = P.tgt_bytes;
   P.total = P.tgt_bytes + (backward ? 0 : align256(dense_partials_bytes(d.L, d.B, d.C, d.HW, dice)));
   return true;
@@ -753,12 +777,14 @@ int dense_prep(const DensePlan& P, const int64_t* targets, unsigned char* w, Den
   PrepArgs pa{};
   pa.targets = targets;
   pa.lab16 = d.counts_mode ? nullptr : (uint16_t*)w;
-  pa.counts8 = d.counts_mode ? (uint8_t*)w : nullptr;
+  pa.counts = d.counts_mode ? (uint8_t*)w : nullptr;
+  pa.cw = d.cw;
   pa.pbits = nullptr;
   pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
   pa.GT_total = d.C; pa.GT_out = d.C; pa.bg = d.C;
   a.lab16 = pa.lab16;
-  a.counts8 = pa.counts8;
+  a.counts = pa.counts;
+  a.cw = d.cw;
   a.L = d.L; a.B = d.B; a.C = d.C; a.HW = d.HW; a.HWp = d.HWp; a.HtWt = d.Ht * d.Wt;
   a.N2 = (float)d.N2;
   if (d.B == 0) return ML_OK;

@@ -291,7 +291,7 @@ __device__ __forceinline__ void pace(int* prog, int k) {
 // redoes the range with the formulas before writing.  `setup` (the
 // workgroup's table build and barrier) is called exactly once on every path,
 // after the first D K-steps of loads are issued, so their latency overlaps it.
-template <int DT, int RT, int NT, bool CNT, bool TAB, class Setup>
+template <int DT, int RT, int NT, int CNT, bool TAB, class Setup>
 __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
                                           int64_t ks, int64_t KS, const unsigned char* lut,
                                           float* out, float* rs_out, int* prog, Setup&& setup) {
@@ -360,41 +360,58 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       if (nt >= nt_used) continue;
-      u32x4_t bp, bv;
-      if constexpr (!CNT) {
+      // CNT == 2 (u16 counts): B = hi + lo with hi = v & 0xFF00 and lo =
+      // v & 0xFF, both exact in bf16 (counts and N2 - n reach s*s > 256,
+      // which bf16 does not hold exactly), so each product runs twice
+      constexpr int NB = CNT == 2 ? 2 : 1;
+      u32x4_t bp[NB], bv[NB];
+      if constexpr (CNT == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint32_t m = pk_min_u16(L2[i] ^ colL[nt], 0x00010001u);
-          bp[i] = pk_mul_lo_u16(m, coefB[nt]);
-          bv[i] = pk_sub_u16(baseB[nt], bp[i]);
+          bp[0][i] = pk_mul_lo_u16(m, coefB[nt]);
+          bv[0][i] = pk_sub_u16(baseB[nt], bp[0][i]);
         }
       } else {
+        // real columns: B = n, B' = N2 - n; ones column: B = N2, B' = 0;
+        // padding: both 0 (integers: counts never exceed N2)
         const int slot = nt * 16 + r;
-        const float kB = slot < G ? 1.f : 0.f;
-        const float cB = slot == G ? a.N2 : 0.f;
+        const uint32_t N2i = (uint32_t)a.N2;
         const uint32_t act = colL[nt] & 0xFFFFu;
-        const uint2 cv = *(const uint2*)(a.counts8 + (b * a.GT_total + act) * a.HWp + cell0);
-        const uint32_t cw[2] = {cv.x, cv.y};
+        uint32_t n[8];
+        counts8_u32(a.counts, CNT == 2 ? 2 : 1, (b * a.GT_total + act) * a.HWp + cell0, n);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t word = cw[i >> 1];
-          const int sh = (i & 1) * 16;
-          const float n0 = (float)((word >> sh) & 0xFF);
-          const float n1 = (float)((word >> (sh + 8)) & 0xFF);
-          bv[i] = pack_bf16x2(kB * n0 + cB, kB * n1 + cB);
-          bp[i] = pack_bf16x2(kB * (a.N2 - n0), kB * (a.N2 - n1));
+          uint32_t v[2], p[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            v[h] = slot < G ? n[2 * i + h] : (slot == G ? N2i : 0u);
+            p[h] = slot < G ? N2i - n[2 * i + h] : 0u;
+          }
+          if constexpr (NB == 1) {
+            bv[0][i] = pack_bf16x2((float)v[0], (float)v[1]);
+            bp[0][i] = pack_bf16x2((float)p[0], (float)p[1]);
+          } else {
+            bv[0][i] = pack_bf16x2((float)(v[0] & 0xFF00u), (float)(v[1] & 0xFF00u));
+            bp[0][i] = pack_bf16x2((float)(p[0] & 0xFF00u), (float)(p[1] & 0xFF00u));
+            bv[NB - 1][i] = pack_bf16x2((float)(v[0] & 0xFFu), (float)(v[1] & 0xFFu));
+            bp[NB - 1][i] = pack_bf16x2((float)(p[0] & 0xFFu), (float)(p[1] & 0xFFu));
+          }
         }
       }
-      const bf16x8_t Bp = __builtin_bit_cast(bf16x8_t, bp);
-      const bf16x8_t Bv = __builtin_bit_cast(bf16x8_t, bv);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
+      for (int h = 0; h < NB; ++h) {
+        const bf16x8_t Bp = __builtin_bit_cast(bf16x8_t, bp[h]);
+        const bf16x8_t Bv = __builtin_bit_cast(bf16x8_t, bv[h]);
 #pragma unroll
-        for (int sp = 0; sp < NS; ++sp) {
-          acc[0][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0][rt][sp], Bp, acc[0][rt][nt], 0, 0, 0);
-          acc[0][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1][rt][sp], Bv, acc[0][rt][nt], 0, 0, 0);
-          acc[1][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2][rt][sp], Bv, acc[1][rt][nt], 0, 0, 0);
-          acc[2][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[3][rt][sp], Bv, acc[2][rt][nt], 0, 0, 0);
+        for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+          for (int sp = 0; sp < NS; ++sp) {
+            acc[0][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0][rt][sp], Bp, acc[0][rt][nt], 0, 0, 0);
+            acc[0][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1][rt][sp], Bv, acc[0][rt][nt], 0, 0, 0);
+            acc[1][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2][rt][sp], Bv, acc[1][rt][nt], 0, 0, 0);
+            acc[2][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[3][rt][sp], Bv, acc[2][rt][nt], 0, 0, 0);
+          }
         }
       }
     }
@@ -616,7 +633,7 @@ constexpr int kClassOf = NT == 2 ? 0 : NT == 7 ? 1 : 2;
 // the class (item = task index * KS + split), with the class's tasks, count
 // and K-split read from the device schedule.  The grid has
 // max(slots, tasks) waves, so every item has a wave.
-template <int DT, int RT, int NT, bool CNT, bool TAB>
+template <int DT, int RT, int NT, int CNT, bool TAB>
 __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs a) {
   constexpr int CI = kClassOf<NT>;
   constexpr int WV = cost_waves(NT, TAB);
@@ -652,7 +669,7 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
 
 // ---- launch plan ---------------------------------------------------------------
 // Resident waves of one cost kernel instance on the current device (cached).
-template <int DT, int RT, int NT, bool CNT, bool TAB>
+template <int DT, int RT, int NT, int CNT, bool TAB>
 static int occ_slots() {
   static std::atomic<int> cache[64];
   int dev = 0;
@@ -671,15 +688,17 @@ static int occ_slots() {
   return v;
 }
 
+// cnt: 0 label map, 1 u8 counts, 2 u16 counts
 template <int DT, int RT, int NT>
-static int occ_slots_for(bool cnt, bool tab) {
-  if (cnt) return occ_slots<DT, RT, NT, true, false>();
-  if (DT == ML_BF16 && tab) return occ_slots<DT, RT, NT, false, DT == ML_BF16>();
-  return occ_slots<DT, RT, NT, false, false>();
+static int occ_slots_for(int cnt, bool tab) {
+  if (cnt == 1) return occ_slots<DT, RT, NT, 1, false>();
+  if (cnt == 2) return occ_slots<DT, RT, NT, 2, false>();
+  if (DT == ML_BF16 && tab) return occ_slots<DT, RT, NT, 0, DT == ML_BF16>();
+  return occ_slots<DT, RT, NT, 0, false>();
 }
 
 template <int DT, int RT>
-static void plan_slots(CostPlan& p, bool cnt, bool tab) {
+static void plan_slots(CostPlan& p, int cnt, bool tab) {
   for (int ci = 0; ci < p.nclass; ++ci) {
     int v = 0;
     switch (ci) {
@@ -693,7 +712,7 @@ static void plan_slots(CostPlan& p, bool cnt, bool tab) {
 
 CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
   CostPlan p = bound_cost_plan(d);
-  const bool cnt = d.counts_mode;
+  const int cnt = d.counts_mode ? d.cw : 0;
   switch (dtype) {
     case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false); break;
     case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab); break;
@@ -707,12 +726,14 @@ static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st
   constexpr int CI = kClassOf<NT>;
   const int WV = cost_waves(NT, DT == ML_BF16 && tab && !d.counts_mode);
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), WV));
-  if (d.counts_mode)
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, true, false>), grid, dim3(64 * WV), 0, st, a);
+  if (d.counts_mode && d.cw == 2)
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, 2, false>), grid, dim3(64 * WV), 0, st, a);
+  else if (d.counts_mode)
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, 1, false>), grid, dim3(64 * WV), 0, st, a);
   else if (DT == ML_BF16 && tab)
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, DT == ML_BF16>), grid, dim3(64 * WV), 0, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, 0, DT == ML_BF16>), grid, dim3(64 * WV), 0, st, a);
   else
-    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, false, false>), grid, dim3(64 * WV), 0, st, a);
+    hipLaunchKernelGGL((cost_kernel<DT, RT, NT, 0, false>), grid, dim3(64 * WV), 0, st, a);
   return check_launch("pair_cost");
 }
 

@@ -15,7 +15,7 @@
 // reference gives every low-resolution cell its own block of 64 threads and
 // reads the C logits of that cell with stride H*W; here a workgroup streams a
 // contiguous chunk of one (l, b, c) plane (coalesced 16-byte loads) against
-// the compact targets (u16 labels for s == 1, u8 counts for s > 1) shared by
+// the compact targets (u16 labels for s == 1, u8 / u16 counts for s > 1) shared by
 // all planes of the image.  Sums are float64 per workgroup, combined in a
 // fixed order by one small kernel, so results are deterministic (the
 // reference's float / double atomics are not).
@@ -100,7 +100,7 @@ __device__ __forceinline__ void dense_store8(void* base, int dt, int64_t i, cons
 // counts of class c for 8 cells starting at cell0
 __device__ __forceinline__ void dense_count8(const DenseArgs& a, int64_t b, int64_t c,
                                              int64_t cell0, float n[8]) {
-  if (a.counts8 == nullptr) {
+  if (a.counts == nullptr) {
     const uint4 lv = *(const uint4*)(a.lab16 + b * a.HWp + cell0);
     const uint32_t w[4] = {lv.x, lv.y, lv.z, lv.w};
     const uint32_t c32 = (uint32_t)c;
@@ -110,10 +110,7 @@ __device__ __forceinline__ void dense_count8(const DenseArgs& a, int64_t b, int6
       n[2 * k + 1] = (w[k] >> 16) == c32 ? 1.f : 0.f;
     }
   } else {
-    const uint2 cv = *(const uint2*)(a.counts8 + (b * a.C + c) * a.HWp + cell0);
-    const uint32_t w[2] = {cv.x, cv.y};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) n[k] = (float)((w[k >> 2] >> ((k & 3) * 8)) & 0xFFu);
+    counts8_f(a.counts, a.cw, (b * a.C + c) * a.HWp + cell0, n);
   }
 }
 

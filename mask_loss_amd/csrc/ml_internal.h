@@ -121,6 +121,7 @@ struct Dims {
   int64_t ks_max;            // most K-splits per task (>= 8 K-steps per wave)
   int nslot;                 // 16 * NT
   bool counts_mode;          // s > 1: per-cell count operands
+  int cw;                    // bytes per count: 1 (u8, s <= 15) or 2 (u16, s >= 16)
 };
 
 bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d, std::string& err);
@@ -145,7 +146,7 @@ inline SavedLayout saved_layout(const Dims& d) {
 
 // Byte offsets inside the caller's workspace.
 struct Layout {
-  size_t lab16, counts8, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
+  size_t lab16, counts, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
       sep, tot, rowIT, rowstat, img, layer, gate, total;
 };
 Layout make_layout(const Dims& d, bool force_masks);
@@ -158,7 +159,8 @@ CostPlan bound_cost_plan(const Dims& d);
 struct PrepArgs {
   const int64_t* targets;
   uint16_t* lab16;
-  uint8_t* counts8;
+  uint8_t* counts;       // s > 1: [B][GT_total][HWp] counts of cw bytes each
+  int cw = 1;
   // forward only (else null): per preparation workgroup, kPresWords words of
   // presence bits of its GT labels, [B][nblk][kPresWords]; every word is
   // rewritten on each call, so nothing needs clearing first
@@ -184,7 +186,8 @@ struct PrepArgs {
 struct CostArgs {
   const void* logits;
   const uint16_t* lab16;
-  const uint8_t* counts8;
+  const uint8_t* counts;  // s > 1: [B][GT_total][HWp] counts of cw bytes each
+  int cw;
   const int* ncols;
   const int* colmap;
   const int* sched;  // device schedule (see CostPlan)
@@ -269,7 +272,8 @@ struct BwdArgs {
   const void* logits;
   int dtype;
   const uint16_t* lab16;
-  const uint8_t* counts8;
+  const uint8_t* counts;  // s > 1: [B][GT_total][HWp] counts of cw bytes each
+  int cw;
   const int64_t* pred_to_gt;
   const float* stats;     // per-query stats or null
   const int* list;        // matched-row list (count, rows): only these rows are written
@@ -298,7 +302,8 @@ struct DenseArgs {
   const void* logits;
   int dtype;
   const uint16_t* lab16;   // s == 1: label per cell (0xFFFF outside [0, C))
-  const uint8_t* counts8;  // s > 1: [B][C][HWp] per-cell counts
+  const uint8_t* counts;   // s > 1: [B][C][HWp] per-cell counts of cw bytes each
+  int cw;
   int64_t L, B, C, HW, HWp, HtWt;
   float N2;
   ElemParams ep;           // focal terms (sigmoid CE)
@@ -375,5 +380,29 @@ __device__ inline void zero_fill_range(u32x4_t* p, int64_t n16, unsigned char* t
   if (blk == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
 }
 int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, hipStream_t st);
+
+// Counts of one label at 8 consecutive cells starting at element `idx` of the
+// count tensor: u8 (cw == 1) or u16 (cw == 2).  idx is a multiple of 8, so the
+// run is one aligned 8- or 16-byte load.  The reference's uint8 counts
+// (src/cuda/utils.cuh:9) overflow for s >= 16; u16 holds up to s = 255.
+__device__ __forceinline__ void counts8_u32(const uint8_t* base, int cw, int64_t idx, uint32_t n[8]) {
+  if (cw == 1) {
+    const uint2 v = *(const uint2*)(base + idx);
+    const uint32_t w[2] = {v.x, v.y};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) n[k] = (w[k >> 2] >> ((k & 3) * 8)) & 0xFFu;
+  } else {
+    const uint4 v = *(const uint4*)(base + 2 * idx);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) n[k] = (w[k >> 1] >> ((k & 1) * 16)) & 0xFFFFu;
+  }
+}
+__device__ __forceinline__ void counts8_f(const uint8_t* base, int cw, int64_t idx, float n[8]) {
+  uint32_t u[8];
+  counts8_u32(base, cw, idx, u);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) n[k] = (float)u[k];
+}
 
 }  // namespace ml

@@ -1,9 +1,10 @@
 // Target preparation: int64 label map -> compact per-image target operands.
 //
 //   s == 1 : u16 label per cell (labels outside [0, GT_total) -> 0xFFFF)
-//   s  > 1 : u8 count of each label inside the s x s block of every cell
+//   s  > 1 : count of each label inside the s x s block of every cell
 //            (B, GT_total, HWp), the reference's count tensor
-//            (src/cuda/utils.cuh:6-36)
+//            (src/cuda/utils.cuh:6-36); u8 for s <= 15, u16 for s >= 16
+//            (where the reference's uint8 counts overflow, utils.cuh:9)
 // plus, for the forward, which GTs have pixels (the reference's per-GT areas
 // of src/cuda/pw_mask.cu:391 are only ever tested against zero) and, per
 // image, the compacted list of output columns whose GT is non-empty, and the
@@ -253,8 +254,14 @@ __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
       for (int64_t dx = 0; dx < a.s; ++dx) {
         const int64_t lab = row[dx];
         if ((uint64_t)lab < (uint64_t)a.GT_total) {
-          uint8_t* c = a.counts8 + (b * a.GT_total + lab) * a.HWp + cell;
-          *c = (uint8_t)(*c + 1);
+          const int64_t e = (b * a.GT_total + lab) * a.HWp + cell;
+          if (a.cw == 1) {
+            uint8_t* c = a.counts + e;
+            *c = (uint8_t)(*c + 1);
+          } else {
+            uint16_t* c = (uint16_t*)a.counts + e;
+            *c = (uint16_t)(*c + 1);
+          }
           if (mark && lab != prev) pres_mark(pres, lab);
         }
         prev = lab;
@@ -285,7 +292,7 @@ int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   if (!d.counts_mode) {
     hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);
   } else {
-    rc = launch_fill_i32((int*)a.counts8, 0, d.B * d.GT_total * d.HWp / 4, st);
+    rc = launch_fill_i32((int*)a.counts, 0, d.B * d.GT_total * d.HWp * d.cw / 4, st);
     if (rc) return rc;
     hipLaunchKernelGGL(prep_counts_kernel, grid, dim3(256), 0, st, a);
   }

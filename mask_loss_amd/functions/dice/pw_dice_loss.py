@@ -48,7 +48,7 @@ def pairwise_dice_loss_sampling_py(
     L, B, C, h, w = logits.shape
     Bt, Ht, Wt = targets.shape
     assert B == Bt, "Batch size mismatch"
-    coords = _sampling_coords(B, num_points, point_coords, logits.device)
+    coords = _sampling_coords(B, num_points, point_coords, logits.device, targets, background_index)
     out = mask_loss.forward_pw_dice_loss_sampling(
         logits.contiguous(), targets.to(device=logits.device, dtype=torch.long).contiguous(), coords,
         float(smooth if smooth is not None else 1.0),

@@ -39,10 +39,10 @@ class PairwiseSigmoidCELossFunction(Function):
         return (None,) * 9
 
 
-def _sampling_coords(B, num_points, point_coords, device):
+def _sampling_coords(B, num_points, point_coords, device, targets=None, background_index=None):
     if point_coords is None:
         assert num_points > 0, "num_points must be > 0"
-        return shared_point_coords(B, int(num_points), device)
+        return shared_point_coords(B, int(num_points), device, targets, background_index)
     assert point_coords.dim() == 3 and point_coords.shape[0] == B and point_coords.shape[2] == 2, \
         "point_coords must be (B, P, 2)"
     assert point_coords.shape[1] > 0, "num_points must be > 0"
@@ -62,13 +62,14 @@ def pairwise_sigmoid_cross_entropy_loss_sampling_py(
     sampled bilinearly at the points, labels by the floor mapping
     long(x * (W_t - 1)); the cost is the mean over the points.  The points
     are ``point_coords`` (B, P, 2) in [0, 1] if given, else ``num_points``
-    drawn with ``torch.rand(1, P, 2)`` per image as in the reference."""
+    drawn with ``torch.rand(1, P, 2)`` for the images the reference draws
+    for (see shared_point_coords), in its order."""
     assert logits.dim() == 5, "logits must have shape (L, B, C, h, w)"
     L, B, C, h, w = logits.shape
     Bt, Ht, Wt = targets.shape
     assert B == Bt, "Batch size mismatch between logits and targets"
     fg, fa = _focal(focal_gamma, focal_alpha)
-    coords = _sampling_coords(B, num_points, point_coords, logits.device)
+    coords = _sampling_coords(B, num_points, point_coords, logits.device, targets, background_index)
     out = mask_loss.forward_pw_sigmoid_ce_loss_sampling(
         logits.contiguous(), targets.to(device=logits.device, dtype=torch.long).contiguous(), coords,
         background_index if background_index is not None else -1,

@@ -91,12 +91,27 @@ def get_uncertain_point_coords_with_randomness(
     return point_coords
 
 
-def shared_point_coords(B, num_points, device):
-    """One point set per image, (B, P, 2): ``torch.rand(1, P, 2)`` drawn per
-    image in order, the draws of the reference's pairwise sampling costs
-    (functions/sigmoid/pw_sigmoid_ce.py:486, functions/dice/pw_dice_loss.py:232;
-    the reference skips the draw for an image with no GT, this draws for
-    every image)."""
+def shared_point_coords(B, num_points, device, targets=None, background_index=None):
+    """One point set per image, (B, P, 2), with the reference's draws
+    (functions/sigmoid/pw_sigmoid_ce.py:465-486, functions/dice/pw_dice_loss.py:206-232):
+    ``torch.rand(1, P, 2)`` per image, in image order, only for the images the
+    reference draws for -- none when the label maps hold no GT class
+    (targets.max() + 1 <= 0, or only the background class), else every image
+    with a label other than ``background_index``.  The other images' rows are
+    zero; their costs are +inf whatever the points.  Without ``targets`` every
+    image draws.  Deciding which images draw reads the label maps back to the
+    host, as the reference's torch.unique does."""
     if B == 0:
         return torch.empty(0, num_points, 2, device=device)
-    return torch.cat([torch.rand(1, num_points, 2, device=device) for _ in range(B)], dim=0)
+    draw = [True] * B
+    if targets is not None:
+        t = targets.reshape(B, -1)
+        gt_all = int(t.max().item()) + 1 if t.numel() else 0
+        G = gt_all - (1 if background_index is not None and 0 <= background_index < gt_all else 0)
+        if gt_all <= 0 or G <= 0:
+            draw = [False] * B
+        elif background_index is not None:
+            draw = (t != background_index).any(dim=1).tolist()
+    rows = [torch.rand(1, num_points, 2, device=device) if d
+            else torch.zeros(1, num_points, 2, device=device) for d in draw]
+    return torch.cat(rows, dim=0)

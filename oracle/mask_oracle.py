@@ -124,32 +124,34 @@ def pairwise_mask_costs(mask_logits, mask_targets, GT_total, background_index,
     counts = label_counts(mask_targets, H, W, GT_total).astype(np.float64)  # (B,G,HW)
     area = counts.sum(axis=2)  # (B, G)
     ap, an = _alphas(mask_alpha)
-    e = elementwise(z.reshape(L, B, Q, H * W), mask_gamma, ug, ug_min)
-    coeff_neg = an * e.mn * e.cn
-    coeff_pos = ap * e.mp * e.cp
-    base = (N2 * e.w * coeff_neg).sum(-1)            # (L,B,Q)   pw_mask.cu:139
-    p_total = (N2 * e.w * e.p).sum(-1)                 # pw_mask.cu:140
-    wsum = (N2 * e.w).sum(-1)                          # pw_mask.cu:141
-    if not normalize:
-        wsum = np.full_like(wsum, float(Ht * Wt))      # pw_mask.cu:200-202
-    wsum = np.maximum(wsum, EPS)                       # pw_mask.cu:203
+    # every output column k at once: n[b, j, k] = count of GT slot a(k) at cell j
+    acts = np.array([out_to_actual(k, bg) for k in range(GT_out)], dtype=np.int64)
+    nT = np.ascontiguousarray(np.swapaxes(counts[:, acts, :], 1, 2))  # (B, HW, GT_out)
+    empty = area[:, acts] == 0                         # pw_mask.cu:209-217
     bce = np.empty((L, B, Q, GT_out))
     dice = np.empty((L, B, Q, GT_out))
-    delta_c = e.w * (coeff_pos - coeff_neg)
-    wp = e.w * e.p
-    for k in range(GT_out):
-        a = out_to_actual(k, bg)
-        n = counts[:, a, :]  # (B, HW)
-        d = np.einsum("lbqj,bj->lbq", delta_c, n)      # pw_mask.cu:268-271
-        inter = np.einsum("lbqj,bj->lbq", wp, n)
-        tsum = np.einsum("lbqj,bj->lbq", e.w, n)
-        b_k = (base + d) / wsum * sigmoid_scale        # pw_mask.cu:300
-        d_k = (1.0 - (2.0 * inter + smooth) / (p_total + tsum + smooth)) * dice_scale
-        empty = area[:, a] == 0
-        b_k[:, empty, :] = np.inf
-        d_k[:, empty, :] = np.inf
-        bce[..., k] = b_k
-        dice[..., k] = d_k
+    zr = z.reshape(L, B, Q, H * W)
+    # query rows in chunks of about 2^22 logits (bounded temporaries)
+    rows = max(1, (1 << 22) // max(1, H * W))
+    for l in range(L):
+        for b in range(B):
+            for q0 in range(0, Q, rows):
+                e = elementwise(zr[l, b, q0:q0 + rows], mask_gamma, ug, ug_min)
+                coeff_neg = an * e.mn * e.cn
+                coeff_pos = ap * e.mp * e.cp
+                base = (N2 * e.w * coeff_neg).sum(-1)          # pw_mask.cu:139
+                p_total = (N2 * e.w * e.p).sum(-1)             # pw_mask.cu:140
+                wsum = (N2 * e.w).sum(-1)                      # pw_mask.cu:141
+                if not normalize:
+                    wsum = np.full_like(wsum, float(Ht * Wt))  # pw_mask.cu:200-202
+                wsum = np.maximum(wsum, EPS)                   # pw_mask.cu:203
+                d = (e.w * (coeff_pos - coeff_neg)) @ nT[b]    # pw_mask.cu:268-271
+                inter = (e.w * e.p) @ nT[b]
+                tsum = e.w @ nT[b]
+                bk = (base[:, None] + d) / wsum[:, None] * sigmoid_scale   # pw_mask.cu:300
+                dk = (1.0 - (2.0 * inter + smooth) / (p_total[:, None] + tsum + smooth)) * dice_scale
+                bce[l, b, q0:q0 + rows] = np.where(empty[b][None, :], np.inf, bk)
+                dice[l, b, q0:q0 + rows] = np.where(empty[b][None, :], np.inf, dk)
     return bce, dice
 
 
@@ -407,11 +409,16 @@ def matching_backward(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logi
                       dice_scale=1.0, cls_scale=1.0, background_index=-1, ug=1.0,
                       ug_min=0.05, num_masks=-1.0, force_cls=False, force_masks=False,
                       mask_gamma=0.0, mask_alpha=-1.0, cls_gamma=0.0, cls_alpha=-1.0,
-                      void_class_index=-1, use_softmax=False, normalize=True):
+                      void_class_index=-1, use_softmax=False, normalize=True,
+                      denoms=None, rows=None):
     """(grad_mask_logits, grad_cls_logits), reference
     src/cuda/mask_matching_backward.cu:21-216 (mask kernel), :218-376 (class
     kernel) and :378-621 (host: denominators, counts, coefficients).
-    Uncertainty weights and their normaliser are constants (detached)."""
+    Uncertainty weights and their normaliser are constants (detached).
+
+    denoms: (mask, cls) per-layer denominators to use instead of those of
+    `pred_to_gt` (a slice of a larger batch); rows: only these (l, b, q) rows
+    are computed, the others stay zero."""
     z = np.asarray(mask_logits, dtype=np.float64)
     L, B, Q, H, W = z.shape
     zc = np.asarray(cls_logits, dtype=np.float64)
@@ -429,6 +436,8 @@ def matching_backward(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logi
     need_cls = force_cls or has_void
     p2g = np.asarray(pred_to_gt)
     md, cd = denominators(p2g, B, Q, num_masks, force_masks, force_cls, has_void)
+    if denoms is not None:
+        md, cd = (np.asarray(v, dtype=np.float64).reshape(L) for v in denoms)
     inv_md = 1.0 / md
     cls_coeff = cls_scale / cd
     counts = label_counts(mask_targets, H, W, GT_total).astype(np.float64)
@@ -438,78 +447,78 @@ def matching_backward(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logi
     g_mask = np.asarray(g_mask, dtype=np.float64)
     g_dice = np.asarray(g_dice, dtype=np.float64)
     g_cls = np.asarray(g_cls, dtype=np.float64)
-    for l in range(L):
-        for b in range(B):
-            for q in range(Q):
-                out = int(p2g[l, b, q])
-                act = out + (1 if out >= bg else 0)
-                matched = out >= 0 and act < GT_total
-                # ---- mask logits (mask_matching_backward.cu:47-215)
-                if matched or force_masks:
-                    mc = g_mask[l] * inv_md[l]
-                    dc = g_dice[l] * inv_md[l]
-                    if not (mc == 0.0 and dc == 0.0):
-                        zz = z[l, b, q].reshape(-1)
-                        e = elementwise(zz, mask_gamma, ug, ug_min)
-                        t = counts[b, act] if matched else np.zeros_like(zz)
-                        P = (e.w * e.p * area).sum()
-                        T = (e.w * t).sum()
-                        I = (e.w * e.p * t).sum()
-                        S = (e.w * area).sum() if normalize else area * H * W
-                        S = max(S, EPS)
-                        D = P + T + smooth
-                        num = 2.0 * I + smooth
-                        D2 = max(D * D, 1e-20)
-                        negc = np.maximum(area - t, 0.0)
-                        gpos = -e.w * ap * t * e.mp * (mask_gamma * e.p * e.cp + (1.0 - e.p))
-                        gneg = e.w * an * negc * e.mn * (mask_gamma * (1.0 - e.p) * e.cn + e.p)
-                        gs = (gpos + gneg) * sigmoid_scale / S
-                        pp = e.p * (1.0 - e.p)
-                        gd = (num * e.w * pp * area - 2.0 * D * e.w * pp * t) / D2 * dice_scale
-                        gm[l, b, q] = (mc * gs + dc * gd).reshape(H, W)
-                # ---- class logits (mask_matching_backward.cu:239-375)
-                if not (matched or need_cls):
-                    continue
-                base = g_cls[l] * cls_coeff[l]
-                if base == 0.0:
-                    continue
-                y = -1
-                if matched:
-                    y = int(cls_targets[b, act])
-                    if y < 0 or y >= C:
-                        continue
-                zz = zc[l, b, q]
-                if use_softmax:
-                    if matched or (force_cls and has_void):
-                        tgt = y if matched else void
-                        m = zz.max()
-                        ex = np.exp(zz - m)
-                        sm = ex / ex.sum()
-                        gr = sm.copy()
-                        gr[tgt] -= 1.0
-                        gc[l, b, q] = base * gr
-                    elif has_void:
-                        gr = np.zeros(C)
-                        gr[void] = base * (1.0 / (1.0 + math.exp(-zz[void])) - 1.0)
-                        gc[l, b, q] = gr
-                    continue
-                cap, can = _alphas(cls_alpha)
-                e = elementwise(zz, cls_gamma, 0.0, 0.0)
-                posg = -cap * e.mp * (cls_gamma * e.p * e.cp + (1.0 - e.p))
-                negg = can * e.mn * (cls_gamma * (1.0 - e.p) * e.cn + e.p)
-                if matched:
-                    gr = negg.copy()
-                    gr[y] = posg[y]
-                    gc[l, b, q] = base / C * gr
-                elif force_cls:
-                    gr = negg.copy()
-                    if has_void:
-                        gr[void] = posg[void]
-                    gc[l, b, q] = base / C * gr
-                elif has_void:
-                    gr = np.zeros(C)
-                    gr[void] = base * posg[void]
-                    gc[l, b, q] = gr
+    todo = rows if rows is not None else [(l, b, q) for l in range(L) for b in range(B)
+                                          for q in range(Q)]
+    for l, b, q in todo:
+        out = int(p2g[l, b, q])
+        act = out + (1 if out >= bg else 0)
+        matched = out >= 0 and act < GT_total
+        # ---- mask logits (mask_matching_backward.cu:47-215)
+        if matched or force_masks:
+            mc = g_mask[l] * inv_md[l]
+            dc = g_dice[l] * inv_md[l]
+            if not (mc == 0.0 and dc == 0.0):
+                zz = z[l, b, q].reshape(-1)
+                e = elementwise(zz, mask_gamma, ug, ug_min)
+                t = counts[b, act] if matched else np.zeros_like(zz)
+                P = (e.w * e.p * area).sum()
+                T = (e.w * t).sum()
+                I = (e.w * e.p * t).sum()
+                S = (e.w * area).sum() if normalize else area * H * W
+                S = max(S, EPS)
+                D = P + T + smooth
+                num = 2.0 * I + smooth
+                D2 = max(D * D, 1e-20)
+                negc = np.maximum(area - t, 0.0)
+                gpos = -e.w * ap * t * e.mp * (mask_gamma * e.p * e.cp + (1.0 - e.p))
+                gneg = e.w * an * negc * e.mn * (mask_gamma * (1.0 - e.p) * e.cn + e.p)
+                gs = (gpos + gneg) * sigmoid_scale / S
+                pp = e.p * (1.0 - e.p)
+                gd = (num * e.w * pp * area - 2.0 * D * e.w * pp * t) / D2 * dice_scale
+                gm[l, b, q] = (mc * gs + dc * gd).reshape(H, W)
+        # ---- class logits (mask_matching_backward.cu:239-375)
+        if not (matched or need_cls):
+            continue
+        base = g_cls[l] * cls_coeff[l]
+        if base == 0.0:
+            continue
+        y = -1
+        if matched:
+            y = int(cls_targets[b, act])
+            if y < 0 or y >= C:
+                continue
+        zz = zc[l, b, q]
+        if use_softmax:
+            if matched or (force_cls and has_void):
+                tgt = y if matched else void
+                m = zz.max()
+                ex = np.exp(zz - m)
+                sm = ex / ex.sum()
+                gr = sm.copy()
+                gr[tgt] -= 1.0
+                gc[l, b, q] = base * gr
+            elif has_void:
+                gr = np.zeros(C)
+                gr[void] = base * (1.0 / (1.0 + math.exp(-zz[void])) - 1.0)
+                gc[l, b, q] = gr
+            continue
+        cap, can = _alphas(cls_alpha)
+        e = elementwise(zz, cls_gamma, 0.0, 0.0)
+        posg = -cap * e.mp * (cls_gamma * e.p * e.cp + (1.0 - e.p))
+        negg = can * e.mn * (cls_gamma * (1.0 - e.p) * e.cn + e.p)
+        if matched:
+            gr = negg.copy()
+            gr[y] = posg[y]
+            gc[l, b, q] = base / C * gr
+        elif force_cls:
+            gr = negg.copy()
+            if has_void:
+                gr[void] = posg[void]
+            gc[l, b, q] = base / C * gr
+        elif has_void:
+            gr = np.zeros(C)
+            gr[void] = base * posg[void]
+            gc[l, b, q] = gr
     return gm, gc
 
 

@@ -112,7 +112,13 @@ def test_dense_workspace_query():
         for bwd in (0, 1):
             assert lib.ml_dense_loss_workspace_size(ctypes.byref(good), 1, dice, bwd) > 0
     assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 64, 64, 256, 250)), 1, 0, 0) == 0
-    assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 4, 4, 64, 64)), 1, 0, 0) == 0  # s = 16
+    # s = 16 and s = 17 take 16-bit counts (twice the bytes of s = 15's 8-bit ones);
+    # s = 256 does not fit them
+    w15 = lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 4, 4, 60, 60)), 1, 0, 1)
+    w16 = lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 4, 4, 64, 64)), 1, 0, 1)
+    assert w15 > 0 and w16 == 2 * w15
+    assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 4, 4, 68, 68)), 1, 0, 0) > 0
+    assert lib.ml_dense_loss_workspace_size(ctypes.byref(DShape(1, 2, 4, 1, 1, 256, 256)), 1, 0, 0) == 0
 
 
 def test_point_sampling_queries_and_host_tensors_rejected():

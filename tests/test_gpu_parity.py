@@ -85,6 +85,11 @@ COST_CASES = [
     dict(name="f16_default", kw=dict(dtype="float16"), p={}),
     dict(name="f32_counts_s2", kw=dict(s=2, H=12, W=12), p={}),
     dict(name="f32_counts_s4", kw=dict(s=4, H=8, W=8), p={}),
+    # 16-bit counts: s = 16 (n and N2 - n up to 256) and s = 17 (289: the
+    # one-hot operands split into high and low bf16 terms)
+    dict(name="f32_counts_s16", kw=dict(s=16, H=4, W=4), p={}),
+    dict(name="f32_counts_s17", kw=dict(s=17, H=3, W=5, Q=24), p=dict(mask_gamma=2.0, mask_alpha=0.25)),
+    dict(name="bf16_counts_s17", kw=dict(s=17, H=4, W=3, dtype="bfloat16", sigma=3.0), p={}),
     dict(name="f32_focal", kw={}, p=dict(mask_gamma=2.0, mask_alpha=0.25, cls_gamma=2.0, cls_alpha=0.25)),
     dict(name="f32_focal_g1", kw={}, p=dict(mask_gamma=1.0, mask_alpha=0.6, cls_gamma=1.5)),
     dict(name="f32_ug0_nonorm", kw={}, p=dict(ug=0.0, normalize=False)),
@@ -176,6 +181,7 @@ MATCH_CASES = [
     dict(name="inf_thresh_low", kw={}, p={}, m=dict(inf_thresh=2.0)),
     dict(name="counts_s2_force", kw=dict(s=2, H=12, W=12), p=dict(mask_gamma=2.0, mask_alpha=0.25),
          m=dict(force_masks=True, force_cls=True)),
+    dict(name="counts_s17_force", kw=dict(s=17, H=4, W=4), p={}, m=dict(force_masks=True, force_cls=True)),
     dict(name="empty_image", kw=dict(empty_image=True), p={}, m=dict(force_cls=True, void=8)),
     dict(name="q_tail_1024", kw=dict(Q=130, H=8, W=8, G=20), p={}, m={}),
     # cost matrices too large for LDS (300 x 250 floats): the first columns'
@@ -217,15 +223,93 @@ def test_matching_forward(ml, case):
     close(m.numpy(), rm, rt, 1e-2)
     close(d.numpy(), rd, rt, 1e-2)
     close(c.numpy(), rc, 1e-5, 1e-2)
-    # 3. oracle's own float64 assignment agrees wherever it is not a near-tie
+    # 3. the oracle's own float64 assignment agrees wherever it is not a near-tie
+    check_f64_assignment(ref_sep, p2g.numpy(), rt, M)
+
+
+def assignment_cost(c64, a):
+    """Total float64 cost of assignment a (query -> column or -1) on one slice."""
+    return float(sum(c64[q, g] for q, g in enumerate(a) if g >= 0))
+
+
+def check_f64_assignment(ref_sep, p2g, rt, M, exact=False):
+    """The north-star rule for indices: on each (layer, image) slice the GPU's
+    assignment equals the one the reference solver finds on the float64 oracle
+    costs, unless the two differ by no more than the cost tolerance, i.e. the
+    oracle's optimum is not separated from the GPU's choice by more than
+    rt * sum |matched oracle costs|.  `exact`: the case is constructed with a
+    clear gap (or exact ties), so the indices must be equal."""
     rt64 = ref_sep.sum(0)
-    op2g, _ = OA.assign_batch(rt64.reshape(L * B, Q, G), M["inf_thresh"], M["K"], M["strategy"])
+    L, B, Q, G = rt64.shape
+    c = rt64.reshape(L * B, Q, G)
+    op2g, _ = OA.assign_batch(c, M["inf_thresh"], M["K"], M["strategy"])
+    got = np.asarray(p2g).reshape(L * B, Q)
     for s_ in range(L * B):
-        if np.array_equal(op2g[s_], p2g.numpy().reshape(L * B, Q)[s_]):
+        if np.array_equal(op2g[s_], got[s_]):
             continue
-        cost_of = lambda a: sum(rt64.reshape(L * B, Q, G)[s_, q, g] for q, g in enumerate(a) if g >= 0)
-        gap = abs(cost_of(p2g.numpy().reshape(L * B, Q)[s_]) - cost_of(op2g[s_]))
-        assert gap <= 10 * rt * max(1.0, abs(cost_of(op2g[s_]))), f"slice {s_}: gap {gap}"
+        assert not exact, f"slice {s_}: assignment differs from the float64 optimum"
+        gap = assignment_cost(c[s_], got[s_]) - assignment_cost(c[s_], op2g[s_])
+        tol = rt * sum(abs(c[s_, q, g]) for q, g in enumerate(op2g[s_]) if g >= 0)
+        assert abs(gap) <= tol, f"slice {s_}: float64 cost gap {gap:.3e} > {tol:.3e}"
+    return op2g
+
+
+def separated_case(seed, Q=48, G=10, H=32, W=32, dtype="bfloat16", ties=False):
+    """bf16 inputs whose float64 optimum is separated from every other
+    assignment: query 3k+1 carries GT k's mask as +/-6 logits (a strong
+    match), the others are N(0, 3) noise.  ties: query 3k+2 repeats query
+    3k+1 exactly (mask and class logits), so two queries tie exactly for
+    GT k in both float32 and float64 and the solver's tie rule (lowest index)
+    decides."""
+    x = make_case(seed, B=2, Q=Q, G=G, H=H, W=W, dtype="float32", sigma=3.0)
+    z = x["z64"].astype(np.float32).copy()
+    zc = x["zc64"].astype(np.float32).copy()
+    for b in range(2):
+        for k in range(G):
+            if 3 * k + 1 >= Q:
+                break
+            m = x["tgt_np"][b] == k + 1
+            if not m.any():
+                continue
+            z[0, b, 3 * k + 1] = np.where(m, 6.0, -6.0)
+            zc[0, b, 3 * k + 1, int(x["ct_np"][b, k + 1])] = 4.0
+            if ties and 3 * k + 2 < Q:
+                z[0, b, 3 * k + 2] = z[0, b, 3 * k + 1]
+                zc[0, b, 3 * k + 2] = zc[0, b, 3 * k + 1]
+    zt, z64 = rounded(z, dtype)
+    return dict(x, z=zt.cuda(), z64=z64, zc=torch.from_numpy(zc).cuda(),
+                zc64=zc.astype(np.float64), dtype=dtype)
+
+
+@pytest.mark.parametrize("ties", [False, True], ids=["clear_gap", "exact_ties"])
+def test_assignment_bf16_separated(ml, ties):
+    """bf16 logits (costs from the bf16 table): with a clear gap, and with
+    exact ties decided by the tie rule, the indices equal the float64
+    optimum's bit for bit."""
+    x = separated_case(61, ties=ties)
+    P, M = params(dict(use_softmax=True)), mparams(dict(force_cls=True, void=8))
+    p2g = matching_call(ml, x, P, M)[0].cpu().numpy()
+    ref_sep = oracle_costs(x, P)
+    op2g = check_f64_assignment(ref_sep, p2g, RTOL["bfloat16"], M, exact=True)
+    G = ref_sep.shape[-1]
+    for b in range(2):  # the strong matches (or, with ties, their twins) are the ones taken
+        for k in range(G):
+            if 3 * k + 2 < x["z64"].shape[2] and (x["tgt_np"][b] == k + 1).any():
+                took = [q for q in (3 * k + 1, 3 * k + 2) if op2g[b][q] == k]
+                assert took == [3 * k + 1] or (ties and len(took) == 1), (b, k, took)
+
+
+def test_assignment_bf16_near_tie(ml):
+    """Two queries one bf16 step apart in a single cell: their costs differ by
+    far less than the tolerance, so either may take the GT; the GPU's choice
+    must then cost no more than rt * sum|costs| above the float64 optimum."""
+    x = separated_case(62, ties=True)
+    z = x["z"].clone()
+    z.view(torch.int16)[0, 0, 2, 0, 0] += 1  # one bf16 step in one cell of query 2
+    x = dict(x, z=z, z64=z.float().cpu().numpy().astype(np.float64))
+    P, M = params(dict(use_softmax=True)), mparams(dict(force_cls=True, void=8))
+    p2g = matching_call(ml, x, P, M)[0].cpu().numpy()
+    check_f64_assignment(oracle_costs(x, P), p2g, RTOL["bfloat16"], M)
 
 
 BWD_CASES = [
@@ -233,6 +317,9 @@ BWD_CASES = [
     dict(name="f32_sigmoid_focal_forcemasks", kw={}, p=dict(mask_gamma=2.0, mask_alpha=0.25,
          cls_gamma=2.0, cls_alpha=0.25), m=dict(force_masks=True, void=8)),
     dict(name="f32_counts_s2", kw=dict(s=2, H=12, W=12), p={}, m=dict(force_cls=True)),
+    dict(name="f32_counts_s17", kw=dict(s=17, H=4, W=3), p={}, m=dict(force_cls=True)),
+    dict(name="bf16_counts_s16", kw=dict(s=16, H=4, W=4, dtype="bfloat16", sigma=3.0), p={},
+         m=dict(force_cls=True)),
     dict(name="f32_nonorm_ug0", kw={}, p=dict(ug=0.0, normalize=False), m={}),
     dict(name="bf16_softmax", kw=dict(dtype="bfloat16", sigma=3.0), p=dict(use_softmax=True),
          m=dict(force_cls=True, void=8)),

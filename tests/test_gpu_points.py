@@ -159,10 +159,22 @@ def test_sampling_wrappers_draw_like_the_reference(ml):
     got = pairwise_sigmoid_cross_entropy_loss_sampling_py(zt, tt, background_index=0, num_points=700)
     gd = pairwise_dice_loss_sampling_py(zt, tt, smooth=1.0, background_index=0, num_points=700)
     assert got.dtype == torch.bfloat16 and got.shape == (2, 3, 5, int(t.max()))
-    # the same draws: torch.rand(1, P, 2) per image, in order
+    # the reference's draws: torch.rand(1, P, 2) per image in order, except for
+    # image 0, which holds only the background (pw_sigmoid_ce.py:480-486)
     torch.manual_seed(1234)
-    c1 = torch.cat([torch.rand(1, 700, 2, device="cuda") for _ in range(3)]).cpu().numpy()
-    c2 = torch.cat([torch.rand(1, 700, 2, device="cuda") for _ in range(3)]).cpu().numpy()
+
+    def draws():
+        r = [torch.rand(1, 700, 2, device="cuda") for _ in range(2)]
+        return torch.cat([torch.zeros(1, 700, 2, device="cuda")] + r).cpu().numpy()
+
+    c1 = draws()
+    c2 = draws()
+    # and then the generator stands where the reference's leaves it
+    nxt = torch.rand(1, device="cuda").item()
+    torch.manual_seed(1234)
+    pairwise_sigmoid_cross_entropy_loss_sampling_py(zt, tt, background_index=0, num_points=700)
+    pairwise_dice_loss_sampling_py(zt, tt, smooth=1.0, background_index=0, num_points=700)
+    assert torch.rand(1, device="cuda").item() == nxt
     rb = PO.pairwise_sigmoid_ce_sampling(z64, t, c1, background_index=0)
     rd = PO.pairwise_dice_sampling(z64, t, c2, background_index=0)
     close(got.double().cpu().numpy(), rb, 2e-2, 1e-2)
@@ -281,3 +293,20 @@ def test_point_sampled_matching_step_gradient_reaches_dense_logits(ml):
                                  use_softmax=True)
     ref = PO.point_sample_backward(gzs[0, :, :, 0, :], c, h, w)[None]
     close(zt.grad.double().cpu().numpy(), ref, 1e-5, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
+@pytest.mark.parametrize("P", [1025, 12544])
+@pytest.mark.parametrize("H,W", [(32, 32), (37, 29)])
+def test_point_sample_many_points(ml, dt, P, H, W):
+    """More points than the gather's 1024-thread workgroup: its point loop
+    takes several rounds (12,544 is configuration 2's count).  32 x 32 planes
+    are staged several per workgroup; 37 x 29 planes are not a multiple of the
+    16-byte staging loads."""
+    rng = np.random.default_rng(P + H)
+    x64, x = as_dtype(rng.normal(0, 2, size=(2, 6, H, W)), dt)
+    c = coords_with_edges(rng, 2, P)
+    got = ml.point_sample(x, torch.from_numpy(c).cuda(), False)
+    assert got.dtype == TDT[dt] and got.shape == (2, 6, P)
+    ref = PO.point_sample(x64, c, False)
+    close(got.double().cpu().numpy(), ref, SAMPLE_RTOL[dt], np.abs(x64).max())

@@ -89,6 +89,9 @@ PW_CASES = [
     dict(name="f16", kw=dict(dtype="float16"), p={}),
     dict(name="f32_s2_bg0_focal", kw=dict(s=2, H=8, W=8), p=dict(bg=0, gamma=2.0, alpha=0.25)),
     dict(name="f32_s4_nonorm_ug0", kw=dict(s=4, H=8, W=8), p=dict(ug=0.0, normalize=False)),
+    # 16-bit counts (the reference's uint8 counts overflow from s = 16 on)
+    dict(name="f32_s16_u16_counts", kw=dict(s=16, H=4, W=4), p=dict(bg=0)),
+    dict(name="bf16_s17_split_counts", kw=dict(s=17, H=3, W=5, dtype="bfloat16", sigma=3.0), p={}),
     dict(name="f32_bg_mid_ug2", kw=dict(C=7, H=9, W=7), p=dict(bg=2, ug=2.0, ug_min=0.1)),
     dict(name="f32_many_gt", kw=dict(C=3, H=32, W=32, labels=60), p=dict(bg=0)),
     dict(name="bf16_extreme", kw=dict(dtype="bfloat16", sigma=3.0, extreme=True, H=32, W=32), p={}),
@@ -141,6 +144,7 @@ DENSE_CASES = [
     dict(name="bf16_s1", kw=dict(dtype="bfloat16", sigma=3.0), p={}),
     dict(name="f16_s2", kw=dict(dtype="float16", s=2, H=8, W=8), p={}),
     dict(name="f32_s4_focal", kw=dict(s=4, H=8, W=8, C=9), p=dict(gamma=2.0, alpha=0.25)),
+    dict(name="f32_s17_u16_counts", kw=dict(s=17, H=3, W=5, C=4), p=dict(gamma=2.0, alpha=0.25)),
     dict(name="f32_focal_g15", kw=dict(C=3), p=dict(gamma=1.5, alpha=0.6)),
     dict(name="f32_odd_tail", kw=dict(H=7, W=5, C=4, B=3), p=dict(num_masks=2.5)),
     dict(name="f32_big_plane", kw=dict(H=96, W=96, C=3), p={}),

@@ -146,6 +146,28 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
                              int32_t* void_found, ml_event_t void_ready,
                              void* workspace, size_t workspace_bytes, ml_stream_t stream);
 
+/* ---- matching forward without allocation -------------------------------------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  ml_mask_matching_forward with the same arguments and
+ * results, minus workspace / workspace_bytes: its scratch is a static device
+ * array of ML_NOALLOC_SCRATCH_BYTES (128 MiB) on each device it runs on, held
+ * until the process ends; the call itself allocates and frees nothing.
+ * Shapes that need more scratch than that fail with ML_EUNSUPPORTED (the
+ * headline shape, B=16, Q=200, 256x256, up to 100 GT columns, fits).  Calls
+ * that overlap on one device share the array and race: serialise them (one
+ * stream, or wait between calls).  The array's contents need no clearing
+ * between calls. */
+#define ML_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int ml_mask_matching_forward_noalloc(const ml_shape* s, const ml_params* p, int mask_dtype,
+                                     const void* mask_logits, const int64_t* mask_targets,
+                                     int cls_dtype, const void* cls_logits,
+                                     const int64_t* cls_targets, int64_t* pred_to_gt,
+                                     int64_t* pred_round, float* layer_means,
+                                     float* separate_costs, void* saved, void* grad_mask_prefill,
+                                     int32_t* void_found, ml_event_t void_ready,
+                                     ml_stream_t stream);
+
 /* ---- matching backward ------------------------------------------------------
  * grad_{mask,dice,cls}: (L,) float upstream gradients of the layer means.
  * grad_mask_logits: (L,B,Q,H,W) in mask_dtype; grad_cls_logits: (L,B,Q,C) in

@@ -150,10 +150,28 @@ CostPlan bound_cost_plan(const Dims& d) {
     if (c < p.nclass) f += cap * 3 * d.rows * 16 * class_nt(c);
   }
   p.float_total = f;
+  p.slot_total = (int64_t)p.nclass * cap;
   return p;
 }
 
+void pack_cost_plan(CostPlan& p, const Dims& d) {
+  int64_t f = 0, sl = 0;
+  for (int c = 0; c < kClasses; ++c) {
+    const int64_t cap = c < p.nclass ? std::max<int64_t>(p.slots[c], p.ntasks) : 0;
+    p.slot_base[c] = sl;
+    p.float_base[c] = f;
+    sl += cap;
+    f += cap * 3 * d.rows * 16 * class_nt(c);
+  }
+  p.float_total = f;
+  p.slot_total = sl;
+}
+
 Layout make_layout(const Dims& d, bool force_masks) {
+  return make_layout(d, force_masks, bound_cost_plan(d));
+}
+
+Layout make_layout(const Dims& d, bool force_masks, const CostPlan& pl) {
   Layout L;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -168,11 +186,9 @@ Layout make_layout(const Dims& d, bool force_masks) {
   L.ncols = take((size_t)d.B * 4);
   L.colmap = take((size_t)d.B * d.nslot * 4);
   L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
-  const CostPlan pl = bound_cost_plan(d);
-  const int64_t cap = std::max<int64_t>(kCostSlots, pl.ntasks);
   L.sched = take((size_t)sched_ints(pl.ntasks) * 4);
   L.partials = take((size_t)pl.float_total * 4);
-  L.rowsum = take(force_masks ? (size_t)pl.nclass * cap * d.rows * 2 * 4 : 0);
+  L.rowsum = take(force_masks ? (size_t)pl.slot_total * d.rows * 2 * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
   L.tot = take((size_t)d.LB * ceil_div(d.Q * d.GT_out, 4) * 16);
   L.rowIT = take((size_t)d.LB * d.Q * d.nslot * 8);
@@ -240,17 +256,19 @@ static int check_params(const ml_params* p, int64_t C, bool matching) {
   return ML_OK;
 }
 
+int check_matching_params(const ml_params* p, int64_t C) { return check_params(p, C, true); }
+
 static bool dtype_ok(int dt) { return dt == ML_F32 || dt == ML_BF16 || dt == ML_F16; }
 
 // Shared forward: prep -> cost -> assign (-> layer).
-static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
-                        const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
-                        const void* cls_logits, const int64_t* cls_targets, int64_t* pred_to_gt,
-                        int64_t* pred_round, float* layer_means, float* sep, void* saved,
-                        void* prefill, int32_t* void_found, hipEvent_t void_ready, void* ws,
-                        size_t ws_bytes, hipStream_t st, bool costs_only,
-                        float* bce_out = nullptr, float* dice_out = nullptr,
-                        const float* pt_coords = nullptr, int64_t pt_Hs = 0, int64_t pt_Ws = 0) {
+int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
+                 const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
+                 const void* cls_logits, const int64_t* cls_targets, int64_t* pred_to_gt,
+                 int64_t* pred_round, float* layer_means, float* sep, void* saved,
+                 void* prefill, int32_t* void_found, hipEvent_t void_ready, void* ws,
+                 size_t ws_bytes, hipStream_t st, bool costs_only, float* bce_out,
+                 float* dice_out, const float* pt_coords, int64_t pt_Hs, int64_t pt_Ws,
+                 bool packed) {
   if (!dtype_ok(mask_dtype) || (cls_logits && !dtype_ok(cls_dtype)))
     return fail(ML_EINVAL, "unsupported dtype");
   if (!cls_logits && !costs_only) return fail(ML_EINVAL, "matching needs class logits");
@@ -267,7 +285,10 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   const SavedLayout SL = saved_layout(d);
   unsigned char* sv = (unsigned char*)saved;
   float* stats = saved ? (float*)(sv + SL.stats) : nullptr;
-  const Layout L = make_layout(d, force_masks);
+  const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
+  CostPlan plan = make_cost_plan(d, mask_dtype, tab);
+  if (packed) pack_cost_plan(plan, d);
+  const Layout L = packed ? make_layout(d, force_masks, plan) : make_layout(d, force_masks);
   // point-sampling front end: presence records of the full label map after the layout
   const size_t pt_pbits = align256(L.total);
   const int pt_nblk = pt_coords ? prep_blocks_map(pt_Hs, pt_Ws) : 0;
@@ -276,8 +297,6 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   unsigned char* w = (unsigned char*)ws;
   int rc;
 
-  const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
-  const CostPlan plan = make_cost_plan(d, mask_dtype, tab);
   PrepArgs pa;
   pa.targets = mask_targets;
   // with a saved state the compact labels go straight into it (the backward reuses them)
@@ -430,6 +449,19 @@ static int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   return ML_OK;
 }
 
+// Workspace bytes of the matching forward with the packed cost plan (what
+// forward_impl with packed = true needs), or 0 with `err` set.
+size_t forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype,
+                            std::string& err) {
+  Dims d;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err) || !check_assign_dims(d, err)) return 0;
+  const bool force_masks = p->force_unmatched_masks_to_empty != 0;
+  const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
+  CostPlan plan = make_cost_plan(d, mask_dtype, tab);
+  pack_cost_plan(plan, d);
+  return make_layout(d, force_masks, plan).total;
+}
+
 }  // namespace ml
 
 using namespace ml;
@@ -520,7 +552,8 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
   return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
                       cls_targets, pred_to_gt, pred_round, layer_means, separate_costs, saved,
                       grad_mask_prefill, void_found, (hipEvent_t)void_ready, workspace,
-                      workspace_bytes, (hipStream_t)stream, false);
+                      workspace_bytes, (hipStream_t)stream, false, nullptr, nullptr, nullptr, 0,
+                      0, false);
 }
 
 int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mask_dtype,
@@ -532,7 +565,8 @@ int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mas
   if (rc) return rc;
   return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
                       cls_targets, nullptr, nullptr, nullptr, separate_costs, nullptr, nullptr,
-                      nullptr, nullptr, workspace, workspace_bytes, (hipStream_t)stream, true);
+                      nullptr, nullptr, workspace, workspace_bytes, (hipStream_t)stream, true,
+                      nullptr, nullptr, nullptr, 0, 0, false);
 }
 
 int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int dtype,
@@ -547,7 +581,8 @@ int ml_pairwise_sigmoid_dice_forward(const ml_shape* s, const ml_params* p, int 
     return fail(ML_EINVAL, "uncertainty_gamma_min must be in [0, 1]");
   return forward_impl(s, p, dtype, logits, targets, ML_F32, nullptr, nullptr, nullptr, nullptr,
                       nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, workspace,
-                      workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out);
+                      workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out, nullptr, 0,
+                      0, false);
 }
 
 // ---- point-sampling front end ------------------------------------------------
@@ -616,7 +651,8 @@ int ml_pairwise_sigmoid_dice_points_forward(const ml_shape* s, const ml_params* 
     return fail(ML_EINVAL, "uncertainty_gamma_min must be in [0, 1]");
   return forward_impl(s, p, dtype, point_logits, targets, ML_F32, nullptr, nullptr, nullptr,
                       nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, workspace,
-                      workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out, coords, Hs, Ws);
+                      workspace_bytes, (hipStream_t)stream, true, bce_out, dice_out, coords, Hs,
+                      Ws, false);
 }
 
 size_t ml_mask_matching_backward_workspace_size(const ml_shape* s, const ml_params* p,

@@ -70,6 +70,7 @@ struct CostPlan {
   int64_t ks_max;
   int64_t ntasks;                // L * B * rtiles
   int64_t float_total;           // partials size (floats)
+  int64_t slot_total;            // work-item slots of all classes (row-sum records)
 };
 // Device schedule (ints in the workspace): n[kClasses], ks[kClasses],
 // list[kClasses][ntasks] (task ids per class, ascending), idx[ntasks]
@@ -149,11 +150,18 @@ struct Layout {
   size_t lab16, counts, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
       sep, tot, rowIT, rowstat, img, layer, gate, total;
 };
-Layout make_layout(const Dims& d, bool force_masks);
+// Workspace layout for the cost plan `pl` (its float_total / slot_total size
+// the partial-sum regions).
+Layout make_layout(const Dims& d, bool force_masks, const CostPlan& pl);
+Layout make_layout(const Dims& d, bool force_masks);  // with bound_cost_plan(d)
 // Plan slots / offsets of the cost launches (queries kernel occupancy on the
 // current device; the workspace bound uses kCostSlots only).
 CostPlan make_cost_plan(const Dims& d, int dtype, bool tab);
 CostPlan bound_cost_plan(const Dims& d);
+// Region offsets re-packed for the plan's own slot counts (class c holds
+// max(slots[c], ntasks) work items): the smallest layout that gives the same
+// K-splits, and so the same results, as the bound layout.
+void pack_cost_plan(CostPlan& p, const Dims& d);
 
 // ---- kernel argument blocks ------------------------------------------------
 struct PrepArgs {
@@ -316,6 +324,20 @@ struct DenseArgs {
   const float *I_in, *P_in, *T_in;             // dice backward
   void* grad;                                  // (L, B, C, H, W) in dtype
 };
+
+// ---- the shared forward (ml_capi.hip) ---------------------------------------
+// prep -> cost -> finalize -> assignment (costs_only: no assignment) on `st`,
+// scratch from `ws` (ws_bytes).  packed: the cost plan's regions are packed
+// for its own slot counts (pack_cost_plan) instead of the kCostSlots bound.
+int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype, const void* mask_logits,
+                 const int64_t* mask_targets, int cls_dtype, const void* cls_logits,
+                 const int64_t* cls_targets, int64_t* pred_to_gt, int64_t* pred_round,
+                 float* layer_means, float* sep, void* saved, void* prefill, int32_t* void_found,
+                 hipEvent_t void_ready, void* ws, size_t ws_bytes, hipStream_t st, bool costs_only,
+                 float* bce_out, float* dice_out, const float* pt_coords, int64_t pt_Hs,
+                 int64_t pt_Ws, bool packed);
+size_t forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, std::string& err);
+int check_matching_params(const ml_params* p, int64_t C);
 
 // ---- instrumentation: bracket a launch with events when profiling is on ------
 void prof_begin(const char* name, hipStream_t st);

@@ -173,9 +173,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   const int qin = (int)((uint32_t)q - rtile * (uint32_t)a.rows);
   const int64_t task = lb * a.rtiles + rtile;
   const int64_t tidx = a.sched[2 * kClasses + kClasses * a.plan.ntasks + task];
-  int ksc[kClasses];
+  int ksc[kClasses], nc[kClasses];
 #pragma unroll
-  for (int c = 0; c < kClasses; ++c) ksc[c] = a.sched[kClasses + c];
+  for (int c = 0; c < kClasses; ++c) {
+    ksc[c] = a.sched[kClasses + c];
+    nc[c] = a.sched[c];
+  }
   float zc[kFinCls] = {};
   int oslot[kFinCols] = {};
   int64_t oy[kFinCols] = {};
@@ -199,11 +202,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
 
   // round trip 2: the partials (need the column class) and the targets' logits
   const int ci = class_of(G + 1);
-  int KS = ksc[0];
+  int KS = ksc[0], n_ci = nc[0];
 #pragma unroll
   for (int c = 1; c < kClasses; ++c)
-    if (ci == c) KS = ksc[c];
-  const RowPartials rp = row_partials_at(a.partials, a.plan, ci, tidx, KS, qin, a.rows);
+    if (ci == c) {
+      KS = ksc[c];
+      n_ci = nc[c];
+    }
+  const RowPartials rp = row_partials_at(a.partials, a.plan, ci, tidx, KS, n_ci, qin, a.rows);
   if constexpr (FAST) {
 #pragma unroll
     for (int j = 0; j < kFinCols; ++j) zy[j] = cls_at<CDT>(a.cls_logits, zb + min(max(oy[j], (int64_t)0), C - 1));
@@ -338,7 +344,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
     if (a.force_masks) {
       float ub = 0.f, up = 0.f;
       for (int ks = 0; ks < rp.KS; ++ks) {
-        const float* rs = a.rowsum + ((rp.slot0 + ks) * a.rows + q % a.rows) * 2;
+        const float* rs = a.rowsum + ((rp.slot0 + ks * rp.slot_stride) * a.rows + q % a.rows) * 2;
         ub += rs[0];
         up += rs[1];
       }

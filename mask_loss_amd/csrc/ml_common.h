@@ -43,11 +43,13 @@ __device__ __forceinline__ float load_elem_f16(const uint16_t* p, int64_t i) {
 }
 
 // ---------------------------------------------------------------------------
-// packed 16-bit integer helpers (one-hot target operands)
+// packed 16-bit integer helpers (one-hot target operands); pk_min_u16 and
+// pk_sub_sat_u16 take their second operand in a scalar register, so it must be
+// wave-uniform (every caller passes a constant)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t pk_min_u16(uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(r) : "v"(a), "s"(b));
   return r;
 }
 __device__ __forceinline__ uint32_t pk_mul_lo_u16(uint32_t a, uint32_t b) {
@@ -57,7 +59,7 @@ __device__ __forceinline__ uint32_t pk_mul_lo_u16(uint32_t a, uint32_t b) {
 }
 __device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "v"(b));
+  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(r) : "v"(a), "s"(b));
   return r;
 }
 __device__ __forceinline__ uint32_t pk_sub_u16(uint32_t a, uint32_t b) {

@@ -22,9 +22,10 @@
 //
 // Per-cell planes: bf16 logits take only 65536 values, so for them the four
 // planes are read from a per-workgroup LDS table built with the same float32
-// formulas (|z| in [2^-16, 64): one entry per bf16 value; |z| < 2^-16: the
-// z = 0 entry; |z| >= 64, inf and nan read a NaN marker, and a wave whose
-// sums come out NaN redoes its K-range with the formulas).  Other dtypes
+// formulas (|z| in [2^-9, 64): one entry per bf16 value; |z| < 2^-9: the
+// z = 0 entry, which the bf16 planes of such z match to within one rounding
+// step; |z| >= 64, inf and nan read a NaN marker, and a wave whose sums come
+// out NaN redoes its K-range with the formulas).  Other dtypes
 // evaluate the formulas directly and split each plane into NS bf16 terms so
 // products keep float32 accuracy.
 #include <algorithm>
@@ -50,9 +51,9 @@ struct InTraits<ML_F16> {
 };
 
 // ---- LUT geometry (bytes): positive block at 0, negative block at 32768 ----
-constexpr uint32_t kLutBase = 111u << 7;         // bf16 magnitude bits of 2^-16
+constexpr uint32_t kLutBase = 118u << 7;         // bf16 magnitude bits of 2^-9
 constexpr uint32_t kLutOver = 0x4280u;           // bf16 magnitude bits of 64.0
-constexpr uint32_t kLutN = kLutOver - kLutBase;  // 2816 regular entries
+constexpr uint32_t kLutN = kLutOver - kLutBase;  // 1920 regular entries
 constexpr uint32_t kLutSub = kLutBase - 1;       // idx = sat(m - kLutSub): 0 = tiny
 constexpr uint32_t kLutBlock = kLutN + 2;        // tiny + regular + overflow slot
 constexpr uint32_t kLutNegOff = 32768;
@@ -61,15 +62,15 @@ constexpr int kDepth = 4;  // K-steps of logits in flight per wave
 
 __device__ __forceinline__ uint32_t pk_lshl3_u16(uint32_t a) {
   uint32_t r;
-  asm("v_pk_lshlrev_b16 %0, %1, %2" : "=v"(r) : "v"(0x00030003u), "v"(a));
+  asm("v_pk_lshlrev_b16 %0, %1, %2" : "=v"(r) : "s"(0x00030003u), "v"(a));
   return r;
 }
 
 // (a & m) | (b & ~m) in one v_bfi_b32 (written out, the compiler splits it
-// into and / or / bitop3)
+// into and / or / bitop3); m wave-uniform (a scalar register)
 __device__ __forceinline__ uint32_t bfi32(uint32_t m, uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(m), "v"(a), "v"(b));
   return r;
 }
 
@@ -99,7 +100,7 @@ __device__ void build_lut(unsigned char* lut, const ElemParams& ep) {
     const uint32_t j = e - sgn * kLutBlock;
     uint2 v;
     if (j <= kLutN) {
-      const uint32_t mag = j == 0 ? 0u : kLutSub + j;  // j == 0: |z| < 2^-16 -> z = 0
+      const uint32_t mag = j == 0 ? 0u : kLutSub + j;  // j == 0: |z| < 2^-9 -> z = 0
       const float z = __uint_as_float(((sgn << 15) | mag) << 16);
       float neg, pos, wp, w, nu, pu;
       planes_formula(z, ep, neg, pos, wp, w, nu, pu);
@@ -656,7 +657,7 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
     setup();
     return;
   }
-  const int64_t i = w / KS, ks = w % KS;
+  const int64_t i = w % n, ks = w / n;
   const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
   constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
@@ -665,6 +666,329 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
   // pace the waves only where many share the workgroup's CU
   cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs, WV >= 16 ? prog_s : nullptr,
                                   setup);
+}
+
+// ---- bf16 table path with LDS-staged logits (16-row tiles, <= 32 columns) ------
+// HBM streams a row best in long runs, while a 16x16x32 MFMA operand spreads
+// one K-step over 16 rows (64 bytes each).  So the logits go through LDS: a
+// group of 4 K-steps (16 rows x 128 cells, 4 KB) is fetched by four
+// global_load_lds_dwordx4, each moving 1 KB as 4 rows x 256 contiguous bytes
+// straight into the wave's LDS ring, and read back in the operand layout with
+// one ds_read_b128 per K-step.  Instruction i, lane l fetches the 16-byte
+// chunk c = (l & 15) ^ R of row R = 4 i + (l >> 4); the hardware stores lane
+// l at ring slot 64 i + l = 16 R + (c ^ R), so the reader of K-step s (lane
+// (r, g4) wants chunk 4 s + g4 of row r) finds it at slot
+// 16 r + ((4 s + g4) ^ r), and the 16 lanes of each read phase touch 16
+// different bank groups.  The ring holds kRingGroups groups, so a group's
+// fetch is in flight while the previous one is computed, without costing
+// registers.  Work items are ordered task-fastest (see row_partials_at), so
+// a workgroup's 16 waves stream 16 adjacent row tiles at the same offset.
+//
+// LDS map of a 16-wave workgroup: positive table block [0, 8 kLutBlock), the
+// rings of waves 0 and 1 in the gap before the negative block at kLutNegOff,
+// the negative block, then the rings of waves 2..15 (163,072 bytes).
+constexpr int kGroupSteps = 4;            // K-steps per group
+constexpr uint32_t kGroupBytes = 4096;    // 16 rows x 128 cells x 2 bytes
+constexpr int kRingGroups = 2;
+constexpr uint32_t kRingBytes = kRingGroups * kGroupBytes;
+constexpr uint32_t kDmaWaves = 16;
+constexpr uint32_t kLutBlockBytes = kLutBlock * 8;
+
+static_assert(((kLutBlockBytes + 255) & ~255u) + 2 * kRingBytes <= kLutNegOff,
+              "two rings fit between the table blocks");
+constexpr uint32_t kDmaLds =
+    ((kLutNegOff + kLutBlockBytes + 255) & ~255u) + (kDmaWaves - 2) * kRingBytes;
+static_assert(kDmaLds <= 160 * 1024, "table and rings fit the LDS of one CU");
+
+// Ring bases are 256-byte aligned, so a reader's address of K-step s is its
+// step-0 address with bits 6-7 flipped: (4 s + g4) ^ r = (g4 ^ r) ^ 4 s.
+constexpr uint32_t kRingLo = (kLutBlockBytes + 255) & ~255u;
+constexpr uint32_t kRingHi = (kLutNegOff + kLutBlockBytes + 255) & ~255u;
+__device__ __forceinline__ uint32_t ring_base(int wave) {
+  return wave < 2 ? kRingLo + wave * kRingBytes : kRingHi + (wave - 2) * kRingBytes;
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One ds_read_b128 of the wave's ring, complete on return.  Written as
+// assembly: the compiler would otherwise wait for every outstanding fetch
+// before any LDS read, since it cannot tell which ring slot a
+// global_load_lds writes.
+__device__ __forceinline__ uint4 ring_read(uint32_t addr) {
+  uint4 v;
+  asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Table entries of 8 bf16 cells (as lut_lookup8) read with assembly, and the
+// wait for them tied to their registers.  lut_base: the table's LDS address.
+__device__ __forceinline__ void lut_lookup8_asm(const uint4& x, uint32_t lut_base, uint64_t E[8]) {
+  const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t m = u[i] & 0x7FFF7FFFu;
+    const uint32_t idx =
+        pk_min_u16(pk_sub_sat_u16(m, kLutSub * 0x10001u), (kLutN + 1) * 0x10001u);
+    const uint32_t addr = bfi32(0x80008000u, u[i], pk_lshl3_u16(idx));
+    asm volatile("ds_read_b64 %0, %1" : "=v"(E[2 * i]) : "v"(lut_base + (addr & 0xFFFFu)) : "memory");
+    asm volatile("ds_read_b64 %0, %1" : "=v"(E[2 * i + 1]) : "v"(lut_base + (addr >> 16)) : "memory");
+  }
+}
+// Wait for every outstanding LDS read; E (table entries) and x (ring words
+// read earlier) are tied to it, so nothing that uses them moves above it.
+__device__ __forceinline__ void lds_wait(uint64_t E[8], uint4& x) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(E[0]), "+v"(E[1]), "+v"(E[2]), "+v"(E[3]), "+v"(E[4]), "+v"(E[5]), "+v"(E[6]),
+                 "+v"(E[7]), "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
+}
+// One ds_read_b128 of the ring, not waited for (see lds_wait).
+__device__ __forceinline__ uint4 ring_read_async(uint32_t addr) {
+  uint4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lut_planes64(const uint64_t E64[8], bf16x8_t A[4]) {
+  uint2 E[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) E[i] = make_uint2((uint32_t)E64[i], (uint32_t)(E64[i] >> 32));
+  lut_planes(E, A);
+}
+// 16 bytes of labels, loaded with assembly; label_wait<N> waits until at most
+// N vector-memory operations issued after it are outstanding.
+__device__ __forceinline__ u32x4_t label_load(const void* p) {
+  u32x4_t v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void label_wait(u32x4_t& v) {
+  asm volatile("s_waitcnt vmcnt(%1)" : "+v"(v) : "n"(N));
+}
+// Drain every vector-memory operation; the label registers are tied to it,
+// so loads issued but never used (the pipeline's last ones) keep their
+// registers until they have landed (an assembly load's destination would
+// otherwise count as free at once and could be reused while it is in flight).
+__device__ __forceinline__ void drain_loads(u32x4_t (&l)[4]) {
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(l[0]), "+v"(l[1]), "+v"(l[2]), "+v"(l[3]) : : "memory");
+}
+
+template <int NT, class Setup>
+__device__ __forceinline__ void cost_wave_dma(const CostArgs& a, int64_t lb, int64_t rtile,
+                                              int64_t ks, int64_t KS, const unsigned char* lut,
+                                              uint32_t ring, float* out, Setup&& setup) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, g4 = lane >> 4;
+  const int64_t b = lb % a.B;
+  const int G = __builtin_amdgcn_readfirstlane(a.ncols[b]);
+  const int nt_used = (G + 1 + 15) >> 4;
+  const int64_t q0 = rtile * 16;
+
+  uint32_t colL[NT], coefB[NT], baseB[NT];
+  const uint32_t n2pair = pack_bf16x2(a.N2, a.N2);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int slot = nt * 16 + r;
+    colL[nt] = 0;
+    coefB[nt] = slot < G ? 0x3F803F80u : 0u;
+    baseB[nt] = slot < G ? 0x3F803F80u : (slot == G ? n2pair : 0u);
+    if (slot < G) {
+      const int c = a.colmap[b * a.nslot + slot];
+      const int act = c + (c >= a.bg ? 1 : 0);
+      colL[nt] = (uint32_t)act * 0x10001u;
+    }
+  }
+  f32x4_t acc[3][NT];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[i][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // this wave's K-steps: whole groups [g0, g1) of the row's full K-steps
+  const int64_t full = a.HW / kStep;
+  const int64_t ngr = ceil_div(full, kGroupSteps);
+  const int64_t gper = ceil_div(ngr, KS);
+  const int64_t g0 = min(ngr, ks * gper), g1 = min(ngr, g0 + gper);
+  const int64_t s0 = g0 * kGroupSteps;
+  const int nst = (int)(min(full, g1 * kGroupSteps) - s0);
+  const bool has_tail = (a.HW % kStep) != 0 && ks == KS - 1;
+
+  // fetch sources: instruction i of a group reads row R = 4 i + (lane >> 4)
+  // (clamped to the last query) at chunk (lane & 15) ^ R; element offsets
+  // from zrow0 stay below 2^31 (host check)
+  const uint16_t* zrow0 = (const uint16_t*)a.logits + (lb * a.Q + q0) * a.HW;
+  const uint32_t HW32 = (uint32_t)a.HW, qlast = (uint32_t)(a.Q - 1 - q0);
+  auto fetch_group = [&](int slot, int64_t g) {  // g in [g0, g1)
+    const uint32_t cell0 = (uint32_t)(g * (kGroupSteps * kStep));
+    const bool edge = cell0 + kGroupSteps * kStep > HW32;  // wave-uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t R = 4u * i + g4;
+      uint32_t cell = cell0 + 8u * (((uint32_t)lane & 15u) ^ R);
+      if (edge) cell = min(cell, HW32 - 8u);  // past the row end: its last chunk (never used)
+      const uint32_t off = min(R, qlast) * HW32 + cell;
+      __builtin_amdgcn_global_load_lds((const void*)(zrow0 + off),
+                                       (lds_void_t*)(size_t)(ring + slot * kGroupBytes + i * 1024), 16, 0, 0);
+    }
+  };
+  // reader of K-step s: ring + slot * kGroupBytes + 16 (16 r + ((4 s + g4) ^ r))
+  const uint32_t rd = ring + 16u * (16u * r + ((uint32_t)g4 ^ (uint32_t)r));
+  auto step_addr = [&](int t) {
+    const int s = t & (kGroupSteps - 1), slot = (t / kGroupSteps) & (kRingGroups - 1);
+    return (rd ^ (64u * s)) + slot * kGroupBytes;
+  };
+  const uint16_t* labp = a.lab16 + b * a.HWp + g4 * 8;
+  u32x4_t lbuf[kGroupSteps];
+  auto fetch_l = [&](int j, int t) {
+    const int64_t st = s0 + (t < nst ? t : nst - 1);
+    lbuf[j] = label_load(labp + st * kStep);
+  };
+
+  auto mma = [&](const bf16x8_t (&A)[4], const uint4& lv) {
+    const uint32_t L2[4] = {lv.x, lv.y, lv.z, lv.w};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt >= nt_used) continue;
+      u32x4_t bp, bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t m = pk_min_u16(L2[i] ^ colL[nt], 0x00010001u);
+        bp[i] = pk_mul_lo_u16(m, coefB[nt]);
+        bv[i] = pk_sub_u16(baseB[nt], bp[i]);
+      }
+      const bf16x8_t Bp = __builtin_bit_cast(bf16x8_t, bp);
+      const bf16x8_t Bv = __builtin_bit_cast(bf16x8_t, bv);
+      acc[0][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0], Bp, acc[0][nt], 0, 0, 0);
+      acc[0][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1], Bv, acc[0][nt], 0, 0, 0);
+      acc[1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2], Bv, acc[1][nt], 0, 0, 0);
+      acc[2][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[3], Bv, acc[2][nt], 0, 0, 0);
+    }
+  };
+
+  // Every load of the pipeline is issued in this order, so the vmcnt waits
+  // below are exact: labels of steps 0..3, groups 0 and 1; then per step t:
+  // [refill of this group's slot (s = 3)] [label of step t + 4].  The label
+  // of step t is then followed by exactly (near the start: at least) 7 later
+  // loads when it is used, and a group's fetch by at least 2 when its first
+  // step is read from the ring (two steps before that step).  LDS reads run
+  // two steps ahead for the ring and one for the table: step t waits for
+  // both (lds_wait), then issues the ring read of step t + 2 and the table
+  // reads of step t + 1.
+  if (nst > 0) {
+    const int ngl = (int)(g1 - g0);
+    const uint32_t lut_base = (uint32_t)(size_t)(lds_void_t*)lut;
+#pragma unroll
+    for (int j = 0; j < kGroupSteps; ++j) fetch_l(j, j);
+    fetch_group(0, g0);
+    fetch_group(1, g0 + (ngl > 1 ? 1 : 0));
+    setup();
+    __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): group 0 landed (group 1 may be in flight)
+    uint64_t E[8];
+    uint4 xr[2];  // ring words of steps t + 1 (xr[(t + 1) & 1]) and t + 2
+    lut_lookup8_asm(ring_read(step_addr(0)), lut_base, E);
+    xr[1] = nst > 1 ? ring_read_async(step_addr(1)) : make_uint4(0u, 0u, 0u, 0u);
+    for (int t0 = 0; t0 < nst; t0 += kGroupSteps) {
+#pragma unroll
+      for (int s = 0; s < kGroupSteps; ++s) {  // s compile-time: lbuf and xr stay in registers
+        const int t = t0 + s;
+        if (t < nst) {
+          uint4& xn = xr[(s + 1) & 1];  // step t + 1
+          uint4& xnn = xr[s & 1];       // step t + 2
+          lds_wait(E, xn);
+          bf16x8_t A[4];
+          lut_planes64(E, A);
+          if (t + 1 < nst) lut_lookup8_asm(xn, lut_base, E);
+          if (t + 2 < nst) {
+            if (s == kGroupSteps - 2)  // step t + 2 opens the next group: its fetch has landed
+              __builtin_amdgcn_s_waitcnt(0x0F72);  // when at most 2 later loads are pending
+            xnn = ring_read_async(step_addr(t + 2));
+          }
+          if (s == kGroupSteps - 1) {  // every step of this slot is read: refill it two groups on
+            const int k = t0 / kGroupSteps;
+            fetch_group(k & (kRingGroups - 1), g0 + min(k + kRingGroups, ngl - 1));
+          }
+          label_wait<7>(lbuf[s]);
+          __builtin_amdgcn_sched_barrier(0);
+          mma(A, __builtin_bit_cast(uint4, lbuf[s]));
+          __builtin_amdgcn_sched_barrier(0);
+          fetch_l(s, t + kGroupSteps);
+        }
+      }
+    }
+    drain_loads(lbuf);  // also: no fetch may land in LDS after the wave ends
+  } else {
+    setup();
+  }
+
+  // |z| >= 64, inf or nan somewhere in the range (the ones column's w plane
+  // sees every cell): formulas, one step at a time
+  bool bad = false;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bad |= __builtin_isnan(acc[2][nt][e]);
+  bad = __ballot(bad) != 0;
+  const ElemParams ep = a.ep;
+  const int64_t rowoff = (lb * a.Q + min(q0 + r, a.Q - 1)) * a.HW + g4 * 8;
+  auto formula_step = [&](int64_t st, int64_t nvalid) {
+    Raw8<ML_BF16> raw;
+    const uint16_t* zp = (const uint16_t*)a.logits + rowoff + st * kStep;
+    uint32_t u[4] = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < 8; ++k)
+      if (k < nvalid) u[k >> 1] |= (uint32_t)zp[k] << ((k & 1) * 16);
+    raw.w[0] = make_uint4(u[0], u[1], u[2], u[3]);
+    bf16x8_t T[4][1];
+    float ub = 0.f, up = 0.f;
+    if (nvalid >= 8) planes8_formula<ML_BF16, 1, false>(raw, ep, 8, false, T, ub, up);
+    else planes8_formula<ML_BF16, 1, true>(raw, ep, nvalid, false, T, ub, up);
+    const bf16x8_t A[4] = {T[0][0], T[1][0], T[2][0], T[3][0]};
+    mma(A, *(const uint4*)(labp + st * kStep));
+  };
+  if (bad) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[i][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int64_t st = s0; st < s0 + nst; ++st) formula_step(st, 8);
+  }
+  if (has_tail) formula_step(full, a.HW - (full * kStep + g4 * 8));
+
+  constexpr int nslot = 16 * NT;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt >= nt_used) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[(i * 16 + g4 * 4 + e) * nslot + nt * 16 + r] = acc[i][nt][e];
+    }
+}
+
+template <int NT>
+__global__ __launch_bounds__(64 * kDmaWaves) void cost_dma_kernel(CostArgs a) {
+  constexpr int CI = kClassOf<NT>;
+  __shared__ __align__(16) unsigned char lds[kDmaLds];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t n = __builtin_amdgcn_readfirstlane(a.sched[CI]);
+  const int64_t KS = __builtin_amdgcn_readfirstlane(a.sched[kClasses + CI]);
+  const int64_t total = n * KS;
+  const int64_t w0 = (int64_t)blockIdx.x * kDmaWaves;
+  if (w0 >= total) return;  // the whole workgroup is idle
+  auto setup = [&]() {
+    build_lut(lds, a.ep);
+    __syncthreads();
+  };
+  const int64_t w = w0 + wave;
+  if (w >= total) {
+    setup();
+    return;
+  }
+  const int64_t i = w % n, ks = w / n;
+  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
+  const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
+  constexpr int64_t tile = 3 * 16 * 16 * NT;
+  float* out = a.partials + a.plan.float_base[CI] + w * tile;
+  const uint32_t ring = (uint32_t)(size_t)(lds_void_t*)lds + ring_base(wave);
+  cost_wave_dma<NT>(a, lb, rtile, ks, KS, lds, ring, out, setup);
 }
 
 // ---- launch plan ---------------------------------------------------------------
@@ -688,6 +1012,29 @@ static int occ_slots() {
   return v;
 }
 
+// The LDS-staged table kernel needs 16-byte aligned rows (HW % 8 == 0) whose
+// per-tile element offsets fit 32 bits.
+static bool dma_ok(const Dims& d) { return d.HW % 8 == 0 && d.HW >= 8 && d.HW * 16 < ((int64_t)1 << 31); }
+
+// Resident waves of the LDS-staged table kernel on the current device (cached).
+static int occ_slots_dma() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int nb = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_dma_kernel<2>, 64 * kDmaWaves, 0) !=
+            hipSuccess || nb < 1)
+      nb = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+    v = nb * cus * (int)kDmaWaves;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // cnt: 0 label map, 1 u8 counts, 2 u16 counts
 template <int DT, int RT, int NT>
 static int occ_slots_for(int cnt, bool tab) {
@@ -698,11 +1045,11 @@ static int occ_slots_for(int cnt, bool tab) {
 }
 
 template <int DT, int RT>
-static void plan_slots(CostPlan& p, int cnt, bool tab) {
+static void plan_slots(CostPlan& p, int cnt, bool tab, bool dma) {
   for (int ci = 0; ci < p.nclass; ++ci) {
     int v = 0;
     switch (ci) {
-      case 0: v = occ_slots_for<DT, RT, 2>(cnt, tab); break;
+      case 0: v = DT == ML_BF16 && tab && cnt == 0 && dma ? occ_slots_dma() : occ_slots_for<DT, RT, 2>(cnt, tab); break;
       case 1: v = occ_slots_for<DT, RT, 7>(cnt, tab); break;
       default: v = occ_slots_for<DT, RT, 16>(cnt, tab); break;
     }
@@ -714,9 +1061,9 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
   CostPlan p = bound_cost_plan(d);
   const int cnt = d.counts_mode ? d.cw : 0;
   switch (dtype) {
-    case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false); break;
-    case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab); break;
-    case ML_F16: plan_slots<ML_F16, 1>(p, cnt, false); break;
+    case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false, false); break;
+    case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab, dma_ok(d)); break;
+    case ML_F16: plan_slots<ML_F16, 1>(p, cnt, false, false); break;
   }
   return p;
 }
@@ -724,6 +1071,13 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
 template <int DT, int RT, int NT>
 static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   constexpr int CI = kClassOf<NT>;
+  if constexpr (DT == ML_BF16 && NT == 2) {
+    if (tab && !d.counts_mode && dma_ok(d)) {
+      const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), kDmaWaves));
+      hipLaunchKernelGGL((cost_dma_kernel<NT>), grid, dim3(64 * kDmaWaves), 0, st, a);
+      return check_launch("pair_cost");
+    }
+  }
   const int WV = cost_waves(NT, DT == ML_BF16 && tab && !d.counts_mode);
   const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), WV));
   if (d.counts_mode && d.cw == 2)

@@ -77,36 +77,36 @@ struct CostPlan {
 // (position of each task in its class list).
 __host__ __device__ inline int64_t sched_ints(int64_t ntasks) { return 2 * kClasses + (kClasses + 1) * ntasks; }
 
+// Work item w of column-tile class c (n_c tasks, KS_c splits) is task
+// i = w % n_c at K-split ks = w / n_c: consecutive waves take consecutive row
+// tiles at the same K offset, so the rows a workgroup streams are adjacent.
+// Item w owns partial tile float_base[c] + w * tile and row-sum slot
+// slot_base[c] + w.
+//
 // Where the K-split partial sums of query row (lb, q) live: split 0's value
 // of plane 0 at column slot 0, the stride between splits and between planes,
-// the split count, and the global slot of split 0.
+// the split count, and the row-sum slot of split 0 and the stride between
+// splits' slots.
 struct RowPartials {
   const float* p0;
-  int64_t ks_stride, plane, slot0;
+  int64_t ks_stride, plane, slot0, slot_stride;
   int KS;
 };
 // The same from values already loaded: the row's column class ci, the task's
-// index i within that class's list, the class's split count KS and the row's
-// index qin within its row tile.
+// index i within that class's list of n tasks, the class's split count KS
+// and the row's index qin within its row tile.
 __device__ inline RowPartials row_partials_at(const float* partials, const CostPlan& plan, int ci,
-                                              int64_t i, int KS, int qin, int64_t rows) {
+                                              int64_t i, int KS, int64_t n, int qin, int64_t rows) {
   const int64_t nslot_c = 16 * class_nt(ci);
   const int64_t tile = 3 * rows * nslot_c;
   RowPartials r;
   r.KS = KS;
-  r.ks_stride = tile;
+  r.ks_stride = n * tile;
   r.plane = rows * nslot_c;
-  r.p0 = partials + plan.float_base[ci] + i * KS * tile + qin * nslot_c;
-  r.slot0 = plan.slot_base[ci] + i * KS;
+  r.p0 = partials + plan.float_base[ci] + i * tile + qin * nslot_c;
+  r.slot0 = plan.slot_base[ci] + i;
+  r.slot_stride = n;
   return r;
-}
-__device__ inline RowPartials row_partials(const float* partials, const int* sched,
-                                           const CostPlan& plan, int64_t lb, int64_t q,
-                                           int64_t rows, int64_t rtiles, int G) {
-  const int ci = class_of(G + 1);
-  const int64_t task = lb * rtiles + q / rows;
-  const int64_t i = sched[2 * kClasses + kClasses * plan.ntasks + task];
-  return row_partials_at(partials, plan, ci, i, sched[kClasses + ci], (int)(q % rows), rows);
 }
 
 // Derived sizes of one call.

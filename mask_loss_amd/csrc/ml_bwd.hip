@@ -21,13 +21,16 @@
 
 namespace ml {
 
+// Gradient stores are streaming (non-temporal): the gradient is not read
+// again by this library, and dirty lines left in the caches would be written
+// back while the next cost pass streams the logits, at half its read rate.
 __device__ __forceinline__ void store8(void* base, int dt, int64_t i, const float g[8], int64_t nvalid,
                                        bool vec) {
   if (dt == ML_F32) {
     float* p = (float*)base + i;
     if (vec && nvalid >= 8) {
-      *(float4*)p = make_float4(g[0], g[1], g[2], g[3]);
-      *(float4*)(p + 4) = make_float4(g[4], g[5], g[6], g[7]);
+      __builtin_nontemporal_store(f32x4_t{g[0], g[1], g[2], g[3]}, (f32x4_t*)p);
+      __builtin_nontemporal_store(f32x4_t{g[4], g[5], g[6], g[7]}, (f32x4_t*)(p + 4));
     } else {
       for (int k = 0; k < 8; ++k)
         if (k < nvalid) p[k] = g[k];
@@ -47,7 +50,7 @@ __device__ __forceinline__ void store8(void* base, int dt, int64_t i, const floa
       }
     }
     if (vec && nvalid >= 8) {
-      *(uint4*)p = make_uint4(w[0], w[1], w[2], w[3]);
+      __builtin_nontemporal_store(u32x4_t{w[0], w[1], w[2], w[3]}, (u32x4_t*)p);
     } else {
       for (int k = 0; k < 8; ++k)
         if (k < nvalid) p[k] = (uint16_t)(w[k >> 1] >> ((k & 1) * 16));

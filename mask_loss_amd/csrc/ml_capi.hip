@@ -130,6 +130,10 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
   d.ks_max = nsteps / 8 > 1 ? nsteps / 8 : 1;
   d.counts_mode = d.s > 1;
   d.cw = d.s >= 16 ? 2 : 1;  // u8 counts overflow at s*s >= 256
+  // row-tile pairs stream 16-byte aligned rows (HW % 8 == 0) with 32-bit
+  // element offsets within a pair's 32 rows
+  d.pair_ok = dtype == ML_BF16 && !d.counts_mode && d.rows == 16 && d.HW % 8 == 0 && d.HW >= 8 &&
+              d.HW * 32 < ((int64_t)1 << 31);
   return true;
 }
 
@@ -138,7 +142,9 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
 CostPlan bound_cost_plan(const Dims& d) {
   CostPlan p{};
   p.ntasks = d.LB * d.rtiles;
+  p.rtiles = d.rtiles;
   p.ks_max = d.ks_max;
+  p.pair0 = 0;
   p.nclass = 0;
   while (p.nclass < kClasses && class_nt(p.nclass) <= d.NT) ++p.nclass;
   const int64_t cap = std::max<int64_t>(kCostSlots, p.ntasks);
@@ -147,7 +153,9 @@ CostPlan bound_cost_plan(const Dims& d) {
     p.slots[c] = (int)kCostSlots;
     p.slot_base[c] = (int64_t)c * cap;
     p.float_base[c] = f;
-    if (c < p.nclass) f += cap * 3 * d.rows * 16 * class_nt(c);
+    // row-tile pairs: up to max(slots, pairs) items of two row tiles each
+    const int64_t items = c == 0 && d.pair_ok ? 2 * cap : cap;
+    if (c < p.nclass) f += items * 3 * d.rows * 16 * class_nt(c);
   }
   p.float_total = f;
   p.slot_total = (int64_t)p.nclass * cap;
@@ -161,7 +169,7 @@ void pack_cost_plan(CostPlan& p, const Dims& d) {
     p.slot_base[c] = sl;
     p.float_base[c] = f;
     sl += cap;
-    f += cap * 3 * d.rows * 16 * class_nt(c);
+    f += (c == 0 && p.pair0 ? 2 * cap : cap) * 3 * d.rows * 16 * class_nt(c);
   }
   p.float_total = f;
   p.slot_total = sl;

@@ -741,6 +741,17 @@ __device__ __forceinline__ void lds_wait(uint64_t E[8], uint4& x) {
                : "+v"(E[0]), "+v"(E[1]), "+v"(E[2]), "+v"(E[3]), "+v"(E[4]), "+v"(E[5]), "+v"(E[6]),
                  "+v"(E[7]), "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
 }
+// Wait for every outstanding LDS read at the end of a pipeline; the
+// registers of reads nothing consumes are tied to it, so they stay reserved
+// until the data has landed.
+__device__ __forceinline__ void lds_drain(uint64_t E[8], uint4 (&x)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(E[0]), "+v"(E[1]), "+v"(E[2]), "+v"(E[3]), "+v"(E[4]), "+v"(E[5]), "+v"(E[6]),
+                 "+v"(E[7]), "+v"(x[0].x), "+v"(x[0].y), "+v"(x[0].z), "+v"(x[0].w), "+v"(x[1].x),
+                 "+v"(x[1].y), "+v"(x[1].z), "+v"(x[1].w)
+               :
+               : "memory");
+}
 // One ds_read_b128 of the ring, not waited for (see lds_wait).
 __device__ __forceinline__ uint4 ring_read_async(uint32_t addr) {
   uint4 v;
@@ -991,6 +1002,280 @@ __global__ __launch_bounds__(64 * kDmaWaves) void cost_dma_kernel(CostArgs a) {
   cost_wave_dma<NT>(a, lb, rtile, ks, KS, lds, ring, out, setup);
 }
 
+// ---- class 0 as row-tile pairs: 32x32x16 products ------------------------------
+// One wave takes 32 query rows (row tiles 2k and 2k + 1 of one image) and the
+// 32 column slots of class 0 over its K-range, in K-steps of 16 cells:
+// lane (r = lane & 31, h = lane >> 5) holds cells 8 h .. 8 h + 7 of the step
+// for query row r (A operand) and for column slot r (B operand), and its
+// accumulators hold column r at rows 8 (v / 4) + 4 h + v % 4 of register v.
+// Against the 16-row kernel, one B operand (the label compare) now serves 32
+// query rows, which halves the vector-ALU work of the column side per logit.
+// Logits go through the same LDS ring: a group is 4 K-steps (64 cells) of the
+// 32 rows, 128 bytes per row; instruction i of a group fetch has lane l load
+// row R = 8 i + (l >> 3) at chunk c = (l & 7) ^ (R & 7) into slot
+// 8 R + (c ^ (R & 7)), so the 8 lanes of each ds_read_b128 phase (8
+// consecutive rows, one chunk) touch 8 different bank groups.
+//
+// A workgroup is 4 pairs x 4 adjacent K-splits (wave = 4 pair + split): the
+// four splits of a pair are summed in LDS at the end, in the fixed order
+// (s0 + s2) + (s1 + s3), and only that sum is written, so the partial sums
+// that reach memory (and the finalize's reads of them) are a quarter of one
+// tile per wave.  The schedule's class-0 split count is the number of such
+// quads, KSq; the kernel runs 4 KSq K-ranges.
+constexpr int kPairStep = 16;                               // cells per K-step
+constexpr int kPairGroupCells = kGroupSteps * kPairStep;    // 64 cells x 32 rows = 4 KB
+constexpr int64_t kPairTile = 3 * 32 * 32;                  // partial tile (floats)
+static_assert(kPairGroupCells * 32 * 2 == (int)kGroupBytes, "a pair group fills one ring slot");
+
+template <class Setup>
+__device__ __forceinline__ void cost_wave_pair(const CostArgs& a, int64_t lb, int64_t q0, int64_t ks,
+                                               int64_t KS, const unsigned char* lut, uint32_t ring,
+                                               f32x16_t (&acc)[3], Setup&& setup) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const int64_t b = lb % a.B;
+  const int G = __builtin_amdgcn_readfirstlane(a.ncols[b]);
+
+  // column operand of slot r (see cost_wave): real columns compare labels,
+  // slot G is the ones column, the rest is padding
+  uint32_t colL = 0;
+  const uint32_t coefB = r < G ? 0x3F803F80u : 0u;
+  const uint32_t baseB = r < G ? 0x3F803F80u : (r == G ? pack_bf16x2(a.N2, a.N2) : 0u);
+  if (r < G) {
+    const int c = a.colmap[b * a.nslot + r];
+    colL = (uint32_t)(c + (c >= a.bg ? 1 : 0)) * 0x10001u;
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+
+  const int64_t full = a.HW / kPairStep;
+  const int64_t ngr = ceil_div(full, kGroupSteps);
+  const int64_t gper = ceil_div(ngr, KS);
+  const int64_t g0 = min(ngr, ks * gper), g1 = min(ngr, g0 + gper);
+  const int64_t s0 = g0 * kGroupSteps;
+  const int nst = (int)(min(full, g1 * kGroupSteps) - s0);
+  const bool has_tail = (a.HW % kPairStep) != 0 && ks == KS - 1;
+
+  // fetch sources: rows past the last query read the last query's row
+  // (never used); element offsets from zrow0 stay below 2^31 (host check)
+  const uint16_t* zrow0 = (const uint16_t*)a.logits + (lb * a.Q + q0) * a.HW;
+  const uint32_t HW32 = (uint32_t)a.HW, qlast = (uint32_t)(a.Q - 1 - q0);
+  auto fetch_group = [&](int slot, int64_t g) {  // g in [g0, g1)
+    const uint32_t cell0 = (uint32_t)(g * kPairGroupCells);
+    const bool edge = cell0 + kPairGroupCells > HW32;  // wave-uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t R = 8u * i + ((uint32_t)lane >> 3);
+      uint32_t cell = cell0 + 8u * (((uint32_t)lane & 7u) ^ (R & 7u));
+      if (edge) cell = min(cell, HW32 - 8u);  // past the row end: its last chunk (never used)
+      const uint32_t off = min(R, qlast) * HW32 + cell;
+      __builtin_amdgcn_global_load_lds((const void*)(zrow0 + off),
+                                       (lds_void_t*)(size_t)(ring + slot * kGroupBytes + i * 1024), 16, 0, 0);
+    }
+  };
+  // reader of K-step s: ring + slot * kGroupBytes + 128 r + 16 ((2 s + h) ^ (r & 7));
+  // the ring is 256-byte aligned, so that is the step-0 address with bits 5-6
+  // flipped by 2 s
+  const uint32_t rd = ring + 128u * r + 16u * ((uint32_t)h ^ ((uint32_t)r & 7u));
+  auto step_addr = [&](int t) {
+    const int s = t & (kGroupSteps - 1), slot = (t / kGroupSteps) & (kRingGroups - 1);
+    return (rd ^ (32u * s)) + slot * kGroupBytes;
+  };
+  const uint16_t* labp = a.lab16 + b * a.HWp + h * 8;
+  u32x4_t lbuf[kGroupSteps];
+  auto fetch_l = [&](int j, int t) {
+    const int64_t st = s0 + (t < nst ? t : nst - 1);
+    lbuf[j] = label_load(labp + st * kPairStep);
+  };
+
+  auto mma = [&](const bf16x8_t (&A)[4], const uint4& lv) {
+    const uint32_t L2[4] = {lv.x, lv.y, lv.z, lv.w};
+    u32x4_t bp, bv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t m = pk_min_u16(L2[i] ^ colL, 0x00010001u);
+      bp[i] = pk_mul_lo_u16(m, coefB);
+      bv[i] = pk_sub_u16(baseB, bp[i]);
+    }
+    const bf16x8_t Bp = __builtin_bit_cast(bf16x8_t, bp);
+    const bf16x8_t Bv = __builtin_bit_cast(bf16x8_t, bv);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0], Bp, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[2], Bv, acc[1], 0, 0, 0);
+    acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[3], Bv, acc[2], 0, 0, 0);
+    acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[1], Bv, acc[0], 0, 0, 0);
+  };
+
+  // The pipeline and its wait counts are those of cost_wave_dma: per K-step
+  // one label load, per group one 4-instruction fetch, in the same order.
+  if (nst > 0) {
+    const int ngl = (int)(g1 - g0);
+    const uint32_t lut_base = (uint32_t)(size_t)(lds_void_t*)lut;
+#pragma unroll
+    for (int j = 0; j < kGroupSteps; ++j) fetch_l(j, j);
+    fetch_group(0, g0);
+    fetch_group(1, g0 + (ngl > 1 ? 1 : 0));
+    setup();
+    __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4): group 0 landed (group 1 may be in flight)
+    uint64_t E[8];
+    uint4 xr[2];  // ring words of steps t + 1 (xr[(t + 1) & 1]) and t + 2
+    lut_lookup8_asm(ring_read(step_addr(0)), lut_base, E);
+    xr[1] = nst > 1 ? ring_read_async(step_addr(1)) : make_uint4(0u, 0u, 0u, 0u);
+    for (int t0 = 0; t0 < nst; t0 += kGroupSteps) {
+#pragma unroll
+      for (int s = 0; s < kGroupSteps; ++s) {  // s compile-time: lbuf and xr stay in registers
+        const int t = t0 + s;
+        if (t < nst) {
+          uint4& xn = xr[(s + 1) & 1];  // step t + 1
+          uint4& xnn = xr[s & 1];       // step t + 2
+          lds_wait(E, xn);
+          bf16x8_t A[4];
+          lut_planes64(E, A);
+          // E is consumed above the next lookups, which then reuse its
+          // registers.  Past the last step the lookups and ring reads still
+          // run (on stale ring words: table addresses stay in the table, ring
+          // addresses in the ring), so no value depends on the step count;
+          // lds_drain below waits for them.
+          __builtin_amdgcn_sched_barrier(0);
+          lut_lookup8_asm(xn, lut_base, E);
+          if (s == kGroupSteps - 2)  // step t + 2 opens the next group: its fetch has landed
+            __builtin_amdgcn_s_waitcnt(0x0F72);  // when at most 2 later loads are pending
+          xnn = ring_read_async(step_addr(t + 2));
+          if (s == kGroupSteps - 1) {  // every step of this slot is read: refill it two groups on
+            const int k = t0 / kGroupSteps;
+            fetch_group(k & (kRingGroups - 1), g0 + min(k + kRingGroups, ngl - 1));
+          }
+          label_wait<7>(lbuf[s]);
+          __builtin_amdgcn_sched_barrier(0);
+          mma(A, __builtin_bit_cast(uint4, lbuf[s]));
+          __builtin_amdgcn_sched_barrier(0);
+          fetch_l(s, t + kGroupSteps);
+        }
+      }
+    }
+    lds_drain(E, xr);
+    drain_loads(lbuf);  // also: no fetch may land in LDS after the wave ends
+  } else {
+    setup();
+  }
+
+  // |z| >= 64, inf or nan somewhere in the range: formulas, one step at a time
+  bool bad = false;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) bad |= __builtin_isnan(acc[2][e]);
+  bad = __ballot(bad) != 0;
+  const ElemParams ep = a.ep;
+  const int64_t rowoff = (lb * a.Q + min(q0 + r, a.Q - 1)) * a.HW + h * 8;
+  auto formula_step = [&](int64_t st, int64_t nvalid) {
+    Raw8<ML_BF16> raw;
+    const uint16_t* zp = (const uint16_t*)a.logits + rowoff + st * kPairStep;
+    uint32_t u[4] = {0u, 0u, 0u, 0u};
+    for (int k = 0; k < 8; ++k)
+      if (k < nvalid) u[k >> 1] |= (uint32_t)zp[k] << ((k & 1) * 16);
+    raw.w[0] = make_uint4(u[0], u[1], u[2], u[3]);
+    bf16x8_t T[4][1];
+    float ub = 0.f, up = 0.f;
+    if (nvalid >= 8) planes8_formula<ML_BF16, 1, false>(raw, ep, 8, false, T, ub, up);
+    else planes8_formula<ML_BF16, 1, true>(raw, ep, nvalid, false, T, ub, up);
+    const bf16x8_t A[4] = {T[0][0], T[1][0], T[2][0], T[3][0]};
+    mma(A, *(const uint4*)(labp + st * kPairStep));
+  };
+  if (bad) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+    for (int64_t st = s0; st < s0 + nst; ++st) formula_step(st, 8);
+  }
+  if (has_tail) formula_step(full, a.HW - (full * kPairStep + h * 8));
+}
+
+// One wave's accumulators in LDS (12 KB): 4 consecutive registers per lane
+// as one 16-byte word, consecutive lanes at consecutive words.
+__device__ __forceinline__ void acc_to_lds(float* buf, const f32x16_t (&acc)[3], int lane) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4)
+      *(f32x4_t*)(buf + ((i * 4 + v4) * 64 + lane) * 4) =
+          f32x4_t{acc[i][4 * v4], acc[i][4 * v4 + 1], acc[i][4 * v4 + 2], acc[i][4 * v4 + 3]};
+}
+__device__ __forceinline__ void acc_add_lds(f32x16_t (&acc)[3], const float* buf, int lane) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const f32x4_t x = *(const f32x4_t*)(buf + ((i * 4 + v4) * 64 + lane) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][4 * v4 + e] += x[e];
+    }
+}
+
+__global__ __launch_bounds__(64 * kDmaWaves) void cost_pair_kernel(CostArgs a) {
+  __shared__ __align__(16) unsigned char lds[kDmaLds];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t n = __builtin_amdgcn_readfirstlane(a.sched[0]);
+  const int64_t KSq = __builtin_amdgcn_readfirstlane(a.sched[kClasses]);
+  const int64_t rt = a.rtiles, prt = (rt + 1) >> 1;
+  const int64_t np = (n / rt) * prt;  // class 0 holds whole images
+  const int64_t npq = (np + 3) >> 2;
+  // workgroup g: pairs 4 (g / KSq) .. + 3 at K-split quad g % KSq (split
+  // quads fastest: measured faster than pair quads fastest on 512x512 maps)
+  const int64_t g = blockIdx.x;
+  if (g >= npq * KSq) return;  // the whole workgroup is idle
+  const int64_t pq = g / KSq, ksq = g - pq * KSq, p = 4 * pq + (wave >> 2);
+  const int kq = wave & 3;
+  auto setup = [&]() {
+    build_lut(lds, a.ep);
+    __syncthreads();
+  };
+  f32x16_t acc[3];
+  int64_t lb = 0, rp = 0;
+  if (p < np) {
+    // pair p = row tiles 2 (p % prt) (+ 1) of the class's (p / prt)-th image
+    const int64_t j = p / prt;
+    rp = p - j * prt;
+    const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + j * rt + 2 * rp]);
+    lb = task / rt;
+    const uint32_t ring = (uint32_t)(size_t)(lds_void_t*)lds + ring_base(wave);
+    cost_wave_pair(a, lb, 32 * rp, 4 * ksq + kq, 4 * KSq, lds, ring, acc, setup);
+  } else {
+    setup();
+  }
+  // sum the four splits of each pair: every wave has drained its loads, so
+  // the table and the rings are free
+  float* red = (float*)lds;
+  constexpr int kAccFloats = 3 * 16 * 64;
+  const int pp = wave >> 2;
+  __syncthreads();
+  if (p < np && kq >= 2) acc_to_lds(red + (2 * pp + kq - 2) * kAccFloats, acc, lane);
+  __syncthreads();
+  if (p < np && kq < 2) acc_add_lds(acc, red + (2 * pp + kq) * kAccFloats, lane);
+  __syncthreads();
+  if (p < np && kq == 1) acc_to_lds(red + pp * kAccFloats, acc, lane);
+  __syncthreads();
+  if (p >= np || kq != 0) return;
+  acc_add_lds(acc, red + pp * kAccFloats, lane);
+
+  // item ksq * np + p: [3][32 rows][32 slots]; rows of the second tile only
+  // for a real pair, slots up to the ones column only (what the finalize reads)
+  const int r = lane & 31, h = lane >> 5;
+  const int G = __builtin_amdgcn_readfirstlane(a.ncols[lb % a.B]);
+  const bool two = 2 * rp + 1 < rt;
+  float* out = a.partials + a.plan.float_base[0] + (ksq * np + p) * kPairTile;
+  if (r <= G) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = 8 * (v >> 2) + 4 * h + (v & 3);
+        if (two || m < 16) out[(i * 32 + m) * 32 + r] = acc[i][v];
+      }
+  }
+}
+
 // ---- launch plan ---------------------------------------------------------------
 // Resident waves of one cost kernel instance on the current device (cached).
 template <int DT, int RT, int NT, int CNT, bool TAB>
@@ -1035,6 +1320,25 @@ static int occ_slots_dma() {
   return v;
 }
 
+// Resident waves of the row-tile pair kernel on the current device (cached).
+static int occ_slots_pair() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int nb = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, cost_pair_kernel, 64 * kDmaWaves, 0) !=
+            hipSuccess || nb < 1)
+      nb = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+    v = nb * cus * (int)kDmaWaves;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 // cnt: 0 label map, 1 u8 counts, 2 u16 counts
 template <int DT, int RT, int NT>
 static int occ_slots_for(int cnt, bool tab) {
@@ -1049,7 +1353,11 @@ static void plan_slots(CostPlan& p, int cnt, bool tab, bool dma) {
   for (int ci = 0; ci < p.nclass; ++ci) {
     int v = 0;
     switch (ci) {
-      case 0: v = DT == ML_BF16 && tab && cnt == 0 && dma ? occ_slots_dma() : occ_slots_for<DT, RT, 2>(cnt, tab); break;
+      case 0:
+        v = p.pair0 ? occ_slots_pair()
+            : DT == ML_BF16 && tab && cnt == 0 && dma ? occ_slots_dma()
+                                                      : occ_slots_for<DT, RT, 2>(cnt, tab);
+        break;
       case 1: v = occ_slots_for<DT, RT, 7>(cnt, tab); break;
       default: v = occ_slots_for<DT, RT, 16>(cnt, tab); break;
     }
@@ -1060,6 +1368,7 @@ static void plan_slots(CostPlan& p, int cnt, bool tab, bool dma) {
 CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
   CostPlan p = bound_cost_plan(d);
   const int cnt = d.counts_mode ? d.cw : 0;
+  p.pair0 = dtype == ML_BF16 && tab && d.pair_ok ? 1 : 0;
   switch (dtype) {
     case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false, false); break;
     case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab, dma_ok(d)); break;
@@ -1071,6 +1380,18 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
 template <int DT, int RT, int NT>
 static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
   constexpr int CI = kClassOf<NT>;
+  if (NT == 2 && a.plan.pair0) {
+    // the schedule's K-split was chosen for row-tile pairs
+    if (DT != ML_BF16 || !tab || !d.pair_ok || d.rows != 16)
+      return fail(ML_EINVAL, "internal: row-tile pair plan without the bf16 table path");
+    // workgroups: ceil(np / 4) pair quads x KSq split quads, where np * 4 KSq
+    // <= max(slots, np) unless KSq = 1 (then np <= L B ceil(rtiles / 2)), and
+    // KSq <= ks_max / 4; surplus workgroups exit at once
+    const int64_t np_max = d.LB * ((d.rtiles + 1) / 2);
+    const int64_t wgs = ceil_div(a.plan.slots[CI], 16) + ceil_div(np_max, 4) + d.ks_max / 4 + 1;
+    hipLaunchKernelGGL(cost_pair_kernel, dim3((unsigned)wgs), dim3(64 * kDmaWaves), 0, st, a);
+    return check_launch("pair_cost");
+  }
   if constexpr (DT == ML_BF16 && NT == 2) {
     if (tab && !d.counts_mode && dma_ok(d)) {
       const dim3 grid((unsigned)ceil_div(std::max<int64_t>(a.plan.slots[CI], a.plan.ntasks), kDmaWaves));

@@ -71,6 +71,12 @@ struct CostPlan {
   int64_t ntasks;                // L * B * rtiles
   int64_t float_total;           // partials size (floats)
   int64_t slot_total;            // work-item slots of all classes (row-sum records)
+  int64_t rtiles;                // row tiles per image
+  // Class 0 runs as row-tile pairs: a wave takes row tiles 2k and 2k + 1 of
+  // one image (32 query rows, 32x32x16 products), its work item is pair k of
+  // the class's images at one K-split, and its partial tile holds both row
+  // tiles ([3][2 rows][nslot]).  No row-sum records on this path.
+  int pair0;
 };
 // Device schedule (ints in the workspace): n[kClasses], ks[kClasses],
 // list[kClasses][ntasks] (task ids per class, ascending), idx[ntasks]
@@ -101,6 +107,19 @@ __device__ inline RowPartials row_partials_at(const float* partials, const CostP
   const int64_t tile = 3 * rows * nslot_c;
   RowPartials r;
   r.KS = KS;
+  if (ci == 0 && plan.pair0) {
+    // task i = row tile rt of the class's j-th image; pair j * prt + rt / 2
+    // of the np pairs, row tile rt & 1 within it
+    const int64_t prt = (plan.rtiles + 1) >> 1;
+    const int64_t j = i / plan.rtiles, rt = i - j * plan.rtiles;
+    const int64_t p = j * prt + (rt >> 1), np = (n / plan.rtiles) * prt;
+    r.ks_stride = np * 2 * tile;
+    r.plane = 2 * rows * nslot_c;
+    r.p0 = partials + plan.float_base[0] + p * 2 * tile + ((rt & 1) * rows + qin) * nslot_c;
+    r.slot0 = plan.slot_base[0] + p;
+    r.slot_stride = np;
+    return r;
+  }
   r.ks_stride = n * tile;
   r.plane = rows * nslot_c;
   r.p0 = partials + plan.float_base[ci] + i * tile + qin * nslot_c;
@@ -123,6 +142,7 @@ struct Dims {
   int nslot;                 // 16 * NT
   bool counts_mode;          // s > 1: per-cell count operands
   int cw;                    // bytes per count: 1 (u8, s <= 15) or 2 (u16, s >= 16)
+  bool pair_ok;              // bf16 label maps whose rows suit the row-tile pair kernel
 };
 
 bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d, std::string& err);

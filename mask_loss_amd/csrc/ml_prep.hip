@@ -177,8 +177,13 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
         n = cnt[c];
         slots = a.plan.slots[c];
       }
-    int64_t ks = n > 0 ? slots / n : 1;
+    // row-tile pairs (class 0): the K-split is chosen for the pair count and
+    // stored as the number of 4-split quads (what reaches the partial sums)
+    const bool pairs = lane == 0 && a.plan.pair0;
+    const int64_t units = pairs ? (n / a.rtiles) * ((a.rtiles + 1) >> 1) : (int64_t)n;
+    int64_t ks = units > 0 ? slots / units : 1;
     ks = ks < 1 ? 1 : (ks > a.plan.ks_max ? a.plan.ks_max : ks);
+    if (pairs) ks = ks >= 8 ? ks >> 2 : 1;
     a.sched[lane] = n;
     a.sched[kClasses + lane] = (int)ks;
   }

@@ -35,7 +35,8 @@ def parse():
     ap.add_argument("--config", default="cfg3_dense_headline",
                     help="workload of the main line; cfg2_point_sampling_front_end runs only the "
                          "point-sampling front end")
-    ap.add_argument("--cpu-sample-images", type=int, default=4)
+    ap.add_argument("--cpu-sample-images", type=int, default=16,
+                    help="images of the headline step the host oracle runs (16 = the whole step)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the per-config lines of the other BASELINE configurations")
@@ -91,24 +92,80 @@ def read_prof(lib, name):
     return n.value, t.value
 
 
-def cpu_baseline(cfg, x, z, zc, p2g_gpu, total_gpu, n_img):
-    """Float64 oracle (cost, matched-loss forward, backward) on the first n_img
-    images with all of their queries, one image at a time, plus the C
-    assignment restatement on every image's GPU cost matrix; scaled to one
-    full step (B images)."""
-    import numpy as np
+def cpu_threads():
+    """Host threads for the CPU baseline: OMP_NUM_THREADS when set (the GPU
+    box's CPU share), else every core."""
+    try:
+        n = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        n = 0
+    return max(1, n or os.cpu_count() or 1)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def total_cost_matrices(cfg, x, z, zc):
+    """The fp32 total-cost matrices (L*B, Q, GT_out) of the step, as the
+    reference's matcher receives them (src/cpu/matching.cpp:665-704)."""
+    import mask_loss_amd
+    k = cfg.kwargs
+    sep = mask_loss_amd.mask_loss.pairwise_mask_loss_forward(
+        z.detach(), x["mask_targets"], zc.detach(), x["cls_targets"], k["smooth"],
+        k["sigmoid_scale"], k["dice_scale"], k["cls_scale"], k["background_index"],
+        k["uncertainty_gamma"], k["uncertainty_gamma_min"], k["mask_focal_gamma"],
+        -1.0 if k["mask_focal_alpha"] is None else k["mask_focal_alpha"], k["cls_focal_gamma"],
+        -1.0 if k["cls_focal_alpha"] is None else k["cls_focal_alpha"],
+        k["label_loss"] == "softmax", k["normalize_uncertainty"])
+    total = ((sep[0] + sep[1]) + sep[2]).double().cpu().numpy()
+    L, B, Q, G = total.shape
+    return total.reshape(L * B, Q, G)
+
+
+def cpu_matcher(total, threads):
+    """The reference's CPU stage (src/cpu/matching.cpp:690-719: the
+    assignment of every (layer, image) slice, at::parallel_for over slices):
+    the C restatement with `threads` OpenMP threads on the GPU's cost
+    matrices.  Milliseconds per step."""
     from oracle import assign as OA
+    OA.assign_batch(total[:1], 1e30, 1, 0, nthreads=1)  # load the library first
+    t0 = time.perf_counter()
+    OA.assign_batch(total, 1e30, 1, 0, nthreads=threads)
+    return (time.perf_counter() - t0) * 1e3
+
+
+def cpu_baseline(cfg, x, z, zc, p2g_gpu, total, n_img, threads):
+    """The whole step on the host: the float64 NumPy oracle (pairwise cost,
+    matched-loss forward, backward) of n_img images with all of their
+    queries, the images spread over `threads` threads (one BLAS thread each),
+    plus the C assignment restatement on every image's GPU cost matrix with
+    `threads` threads.  With n_img = B nothing is extrapolated."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
     from oracle import mask_oracle as O
     k = cfg.kwargs
     n_img = max(1, min(n_img, cfg.B))
-    t_img = 0.0
-    for b in range(n_img):
-        zb = z.detach()[:, b:b + 1].float().cpu().numpy().astype(np.float64)
-        zcb = zc.detach()[:, b:b + 1].float().cpu().numpy().astype(np.float64)
-        tgt = x["mask_targets"][b:b + 1].cpu().numpy()
-        ct = x["cls_targets"][b:b + 1].cpu().numpy()
-        p2g = p2g_gpu[:, b:b + 1]
-        t0 = time.perf_counter()
+    imgs = []
+    for b in range(n_img):  # host copies outside the timed region
+        imgs.append((z.detach()[:, b:b + 1].float().cpu().numpy().astype(np.float64),
+                     zc.detach()[:, b:b + 1].float().cpu().numpy().astype(np.float64),
+                     x["mask_targets"][b:b + 1].cpu().numpy(),
+                     x["cls_targets"][b:b + 1].cpu().numpy(), p2g_gpu[:, b:b + 1]))
+
+    def one(b):
+        zb, zcb, tgt, ct, p2g = imgs[b]
         sep = O.pairwise_mask_loss_forward(zb, tgt, zcb, ct, k["smooth"], k["sigmoid_scale"],
                                            k["dice_scale"], k["cls_scale"], k["background_index"],
                                            k["uncertainty_gamma"], k["uncertainty_gamma_min"], 0.0,
@@ -118,19 +175,24 @@ def cpu_baseline(cfg, x, z, zc, p2g_gpu, total_gpu, n_img):
         O.matching_backward(np.ones(1), np.ones(1), np.ones(1), zb, tgt, zcb, ct, p2g,
                             background_index=0, force_cls=True, void_class_index=cfg.C,
                             use_softmax=True)
-        t_img += time.perf_counter() - t0
+
     t0 = time.perf_counter()
-    L, B, Q, G = total_gpu.shape
-    OA.assign_batch(total_gpu.reshape(L * B, Q, G), 1e30, 1, 0, nthreads=1)
-    t_match = time.perf_counter() - t0
+    with threadpool_limits(limits=1):
+        with ThreadPoolExecutor(threads) as ex:
+            list(ex.map(one, range(n_img)))
+    t_img = time.perf_counter() - t0
+    t_match = cpu_matcher(total, threads)
     scale = cfg.B / n_img
-    ms = (t_img * scale + t_match) * 1e3
+    ms = t_img * scale * 1e3 + t_match
+    sample = (f"float64 NumPy oracle on {n_img} of {cfg.B} images, all {cfg.Q} queries each "
+              f"(cost + matched loss fwd/bwd, {threads} threads, {t_img:.1f} s wall)")
+    sample += f" scaled x{scale:g}" if n_img < cfg.B else " (the whole step, not extrapolated)"
+    sample += (f", plus the C assignment restatement on all {total.shape[0]} GPU cost "
+               f"matrices with {threads} threads ({t_match:.1f} ms)")
     return {
-        "value": round(ms, 1), "unit": "ms/step", "cores": 1, "kind": "port",
-        "sample": (f"float64 NumPy oracle on {n_img} of {cfg.B} images, all {cfg.Q} queries each "
-                   f"(cost + matched loss fwd/bwd, {t_img:.1f} s) scaled x{scale:.0f}, plus the C "
-                   f"assignment restatement on all {L * B} GPU cost matrices "
-                   f"({t_match * 1e3:.1f} ms)"),
+        "value": round(ms, 1), "unit": "ms/step", "cores": threads, "kind": "port",
+        "sample": sample, "cpu_model": cpu_model(), "cpu_count": os.cpu_count(),
+        "matcher_ms": round(t_match, 2),
     }
 
 
@@ -181,11 +243,19 @@ def time_steps(step, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def other_config(cfg, dev, steps, warmup):
+def other_config(cfg, dev, steps, warmup, cpu=True):
     """ms/step, images/s and the step's fraction of the HBM / MFMA roofline for
-    another BASELINE configuration (same step, fewer timed steps)."""
+    another BASELINE configuration (same step, fewer timed steps), and the
+    reference's CPU stage (the assignment) timed on the host."""
     x, z, zc, step, state = make_step(cfg, dev)
     ms = time_steps(step, steps, warmup)
+    cpu_m = None
+    if cpu:
+        threads = cpu_threads()
+        cpu_m = {"matcher_ms": round(cpu_matcher(total_cost_matrices(cfg, x, z, zc), threads), 2),
+                 "threads": threads, "kind": "port",
+                 "what": "C restatement of the reference's assignment (src/cpu/matching.cpp:476-571, "
+                         "690-719) on the step's GPU cost matrices"}
     M = int((state["p2g"] >= 0).sum().item())
     e = z.element_size()
     sb = step_bytes_of(cfg, e, M)
@@ -194,7 +264,8 @@ def other_config(cfg, dev, steps, warmup):
     return {"workload": cfg.name, "ms_per_step": round(ms, 4),
             "images_per_s": round(cfg.B * cfg.L / (ms * 1e-3), 1), "dtype": cfg.dtype,
             "matched": M, "step_algorithmic_bytes": sb, "hbm_floor_us": round(t_hbm, 1),
-            "roofline_frac": round(t_roof / (ms * 1e3), 4), "steps": steps, "warmup": warmup}
+            "roofline_frac": round(t_roof / (ms * 1e3), 4), "steps": steps, "warmup": warmup,
+            "cpu_matcher": cpu_m}
 
 
 def point_front_end(dev, steps, warmup):
@@ -364,17 +435,15 @@ def main():
 
     cpu = None
     if not a.no_cpu_baseline:
-        sep = mask_loss_amd.mask_loss.pairwise_mask_loss_forward(
-            z.detach(), x["mask_targets"], zc.detach(), x["cls_targets"], 1.0, 1.0, 1.0, 1.0, 0,
-            1.0, 0.05, 0.0, -1.0, 0.0, -1.0, True, True)
-        total = ((sep[0] + sep[1]) + sep[2]).double().cpu().numpy()
-        cpu = cpu_baseline(cfg, x, z, zc, p2g.cpu().numpy(), total, a.cpu_sample_images)
+        cpu = cpu_baseline(cfg, x, z, zc, p2g.cpu().numpy(), total_cost_matrices(cfg, x, z, zc),
+                           a.cpu_sample_images, cpu_threads())
 
     others = []
     if not a.no_other_configs:
         for oc in synth.CONFIGS:
             if oc.name != cfg.name:
-                others.append(other_config(oc, dev, a.other_steps, a.other_warmup))
+                others.append(other_config(oc, dev, a.other_steps, a.other_warmup,
+                                           cpu=not a.no_cpu_baseline))
         others.append(point_front_end(dev, a.other_steps, a.other_warmup))
 
     out = {

@@ -376,15 +376,57 @@ __device__ __forceinline__ double readlane_d(double v, int lane) {
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
-// Minimum over the wave, returned in every lane: DPP swaps within each row of
-// 16 lanes (xor 1, xor 2, half-row mirror, row mirror), then the four row
-// minima through readlane.  min is exact, so the order does not matter.
-__device__ __forceinline__ double wave_min_dpp(double v) {
-  v = fmin(v, dpp_d<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = fmin(v, dpp_d<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = fmin(v, dpp_d<0x141>(v));  // row_half_mirror
-  v = fmin(v, dpp_d<0x140>(v));  // row_mirror
-  return fmin(fmin(readlane_d(v, 0), readlane_d(v, 16)), fmin(readlane_d(v, 32), readlane_d(v, 48)));
+// (value, column) pairs ordered by value, then by column: the reference's
+// argmin picks the lowest column index among equal minima (strict '<' in
+// an ascending scan, src/cpu/matching.cpp:146-149).
+__device__ __forceinline__ void lex_take(double& v, int& j, double ov, int oj) {
+  // bitwise, not short-circuit: no branch per comparison
+  const bool take = (ov < v) | ((ov == v) & (oj < j));
+  v = take ? ov : v;
+  j = take ? oj : j;
+}
+template <int CTRL>
+__device__ __forceinline__ void lex_dpp(double& v, int& j) {
+  const double ov = dpp_d<CTRL>(v);
+  const int oj = __builtin_amdgcn_update_dpp(0, j, CTRL, 0xF, 0xF, false);
+  lex_take(v, j, ov, oj);
+}
+// Lexicographic minimum of (v, j) over the wave, returned in every lane:
+// four DPP levels within each row of 16 lanes, then the four row results
+// through readlane.
+__device__ __forceinline__ void wave_argmin_dpp(double& v, int& j) {
+  lex_dpp<0xB1>(v, j);   // quad_perm [1,0,3,2]
+  lex_dpp<0x4E>(v, j);   // quad_perm [2,3,0,1]
+  lex_dpp<0x141>(v, j);  // row_half_mirror
+  lex_dpp<0x140>(v, j);  // row_mirror
+  double bv = readlane_d(v, 0);
+  int bj = __builtin_amdgcn_readlane(j, 0);
+#pragma unroll
+  for (int r = 16; r < 64; r += 16) lex_take(bv, bj, readlane_d(v, r), __builtin_amdgcn_readlane(j, r));
+  v = bv;
+  j = bj;
+}
+// Register slot t (wave-uniform) of lane l: the slot is selected in every
+// lane first, then one readlane fetches lane l's.  Each comparison takes its
+// own opaque copy of t, so the compiler cannot turn the select chain into a
+// dynamically indexed array (which it would place in scratch memory).
+__device__ __forceinline__ bool slot_is(int t, int k) {
+  asm volatile("" : "+s"(t));
+  return t == k;
+}
+template <int NJ>
+__device__ __forceinline__ int sel_i(const int (&x)[NJ], int t, int l) {
+  int r = x[0];
+#pragma unroll
+  for (int k = 1; k < NJ; ++k) r = slot_is(t, k) ? x[k] : r;
+  return __builtin_amdgcn_readlane(r, l);
+}
+template <int NJ>
+__device__ __forceinline__ double sel_d(const double (&x)[NJ], int t, int l) {
+  double r = x[0];
+#pragma unroll
+  for (int k = 1; k < NJ; ++k) r = slot_is(t, k) ? x[k] : r;
+  return readlane_d(r, l);
 }
 
 // ---------------------------------------------------------------------------
@@ -397,35 +439,13 @@ __device__ __forceinline__ double wave_min_dpp(double v) {
 // potential u[p] and its cost-matrix row; the row being inserted keeps its
 // potential and cost row in wave-uniform registers.  So the Dijkstra steps
 // touch LDS only for the cost entries: every potential update is a register
-// add, the row of a newly reached column is a readlane, and the minimum is a
-// DPP reduction.  Each row potential receives the same float64 additions in
+// add, the row of a newly reached column is a readlane, and the argmin is one
+// DPP reduction over (minv, column) pairs, which also yields the column.  The
+// relaxation of a lane's NJ columns has no branches, so its chains
+// interleave.  Each row potential receives the same float64 additions in
 // the same order as in the reference (one += delta per step in which its
 // column is in the tree), so the assignment is the reference's bit for bit.
 // ---------------------------------------------------------------------------
-// Register slot t of lane l, broadcast: every slot is read with readlane and
-// the uniform index picks one (a select chain over registers would be folded
-// back into a dynamically indexed array in scratch memory).
-template <int NJ>
-__device__ __forceinline__ int rl_i(const int (&x)[NJ], int t, int l) {
-  int r = __builtin_amdgcn_readlane(x[0], l);
-#pragma unroll
-  for (int k = 1; k < NJ; ++k) {
-    const int y = __builtin_amdgcn_readlane(x[k], l);
-    r = k == t ? y : r;
-  }
-  return r;
-}
-template <int NJ>
-__device__ __forceinline__ double rl_d(const double (&x)[NJ], int t, int l) {
-  double r = readlane_d(x[0], l);
-#pragma unroll
-  for (int k = 1; k < NJ; ++k) {
-    const double y = readlane_d(x[k], l);
-    r = k == t ? y : r;
-  }
-  return r;
-}
-
 // Cost rows of one image, [column][query] with row stride ldq: rows c < nl
 // in LDS, the others read in place from finalize's total-cost plane (L2).
 // CM, a compile-time choice so that each read is a ds_read or a global load:
@@ -502,59 +522,49 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
 #pragma unroll
         for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
       }
-      double lmin = INFINITY;
+      // relax every free column (no branches: the NJ chains interleave) and
+      // keep this lane's lexicographic (minv, column) minimum; slots ascend
+      // in column index, so a strict '<' keeps the lowest column on ties
+      double bv = INFINITY;
+      int bj = 0x7FFFFFFF;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        if (valid[t] && !((used >> t) & 1u)) {
-          const double raw = (double)rawf[t];
-          const double cij = cost_ok(raw, thr) ? raw : BIG;
-          const double cur = cij - ui0 - v[t];
-          if (cur < minv[t]) {
-            minv[t] = cur;
-            wy[t] = j0;
-          }
-          lmin = fmin(lmin, minv[t]);
-        }
+        const bool act = valid[t] && !((used >> t) & 1u);
+        const double raw = (double)rawf[t];
+        const double cij = cost_ok(raw, thr) ? raw : BIG;
+        const double cur = cij - ui0 - v[t];
+        const bool upd = act && cur < minv[t];
+        minv[t] = upd ? cur : minv[t];
+        wy[t] = upd ? j0 : wy[t];
+        const bool better = act && minv[t] < bv;
+        bv = better ? minv[t] : bv;
+        bj = better ? 1 + lane + 64 * t : bj;
       }
-      const double delta = wave_min_dpp(lmin);
-      if (!isfinite(delta)) {
+      wave_argmin_dpp(bv, bj);
+      const double delta = bv;
+      if (!isfinite(delta)) {  // unreachable with finite costs (n >= M free columns)
         ok = false;
         break;
       }
-      int j1 = 0;
+      const int j1 = bj;
+      // potentials: columns in the tree (and column 0 = row i), others' minv;
+      // invalid slots keep minv = +inf and are never in the tree
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        if (j1 == 0) {
-          const bool hit = valid[t] && !((used >> t) & 1u) && minv[t] == delta;
-          const uint64_t m = __ballot(hit);
-          if (m) j1 = 1 + (__ffsll((unsigned long long)m) - 1) + 64 * t;
-        }
-      }
-      if (j1 == 0) {  // unreachable with finite costs
-        ok = false;
-        break;
-      }
-      // potentials: columns in the tree (and column 0 = row i), others' minv
-#pragma unroll
-      for (int t = 0; t < NJ; ++t) {
-        if (valid[t]) {
-          if ((used >> t) & 1u) {
-            ucol[t] += delta;
-            v[t] -= delta;
-          } else {
-            minv[t] -= delta;
-          }
-        }
+        const bool in_tree = (used >> t) & 1u;
+        ucol[t] = in_tree ? ucol[t] + delta : ucol[t];
+        v[t] = in_tree ? v[t] - delta : v[t];
+        minv[t] = in_tree ? minv[t] : minv[t] - delta;
       }
       ucur += delta;
       const int ol = (j1 - 1) & 63, ot = (j1 - 1) >> 6;
       if (lane == ol) used |= 1u << ot;
       j0 = j1;
-      const int pj0 = rl_i<NJ>(pj, ot, ol);
+      const int pj0 = sel_i<NJ>(pj, ot, ol);
       if (pj0 == 0) break;
       // next row of the tree: the one matched to column j1
-      ui0 = rl_d<NJ>(ucol, ot, ol);
-      col = rl_i<NJ>(rcol, ot, ol);
+      ui0 = sel_d<NJ>(ucol, ot, ol);
+      col = sel_i<NJ>(rcol, ot, ol);
     }
     if (!ok) break;
     // augment along way[] from the free column j0 back to column 0: each
@@ -562,7 +572,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     // row) of the column it was reached from; column 0 holds row i.
     for (int steps = 0; j0 != 0 && steps <= n; ++steps) {
       const int ol = (j0 - 1) & 63, ot = (j0 - 1) >> 6;
-      const int jp = rl_i<NJ>(wy, ot, ol);
+      const int jp = sel_i<NJ>(wy, ot, ol);
       int np, nr;
       double nu;
       if (jp == 0) {
@@ -571,9 +581,9 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         nr = colcur;
       } else {
         const int pl = (jp - 1) & 63, pt = (jp - 1) >> 6;
-        np = rl_i<NJ>(pj, pt, pl);
-        nu = rl_d<NJ>(ucol, pt, pl);
-        nr = rl_i<NJ>(rcol, pt, pl);
+        np = sel_i<NJ>(pj, pt, pl);
+        nu = sel_d<NJ>(ucol, pt, pl);
+        nr = sel_i<NJ>(rcol, pt, pl);
       }
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {

@@ -149,8 +149,7 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
 // the first two round trips is unconditional (indices clamped into range).
 template <int CDT, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void finalize_kernel(AssignArgs a) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's fill gate and finish count
-    if (a.gate) *a.gate = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's finish count
     if (a.done) *a.done = 0;
   }
   __shared__ float sl[4][3][256 + 16];
@@ -648,7 +647,7 @@ __device__ void greedy_wave(const CostRows<CM>& cost, const int* preds, int n,
 // then, with a saved state, the list of matched query rows in ascending order
 // (wave ballots, one blockDim-row chunk at a time) for the backward.  One
 // workgroup.
-__device__ void layer_pass(const LayerArgs& a) {
+__device__ void layer_pass(const LayerArgs& a, int* sbuf, int nsbuf) {
   for (int64_t l = threadIdx.x; l < a.L; l += blockDim.x) {
     float m = 0.f, d = 0.f, c = 0.f, cnt = 0.f;
     for (int64_t b = 0; b < a.B; ++b) {
@@ -671,37 +670,51 @@ __device__ void layer_pass(const LayerArgs& a) {
     a.layer[l * ML_LAYERS + ML_LAYER_INV_CLS_DEN] = 1.f / cd;
   }
   if (a.list == nullptr) return;
-  __shared__ int wcnt[16];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int nw = blockDim.x >> 6;
-  const uint64_t below = (1ull << lane) - 1ull;
-  const int64_t n = a.L * a.B * a.Q;
+  // the matched-row list: the slices' own lists (mrows, written by their
+  // assignment workgroups) concatenated in slice order, i.e. ascending row
+  // index; slices in chunks of CH (prefix and count of each in sbuf), each
+  // chunk one block scan of the counts and one flattened copy
+  __shared__ int wtot[16];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int wave = tid >> 6, lane = tid & 63, nw = nt >> 6;
+  const int64_t LB = a.L * a.B;
+  const int CH = min(nt, nsbuf / 2);
   int base = 0;
-  constexpr int U = 4;  // rows per thread whose loads are in flight together
-  for (int64_t r0 = 0; r0 < n; r0 += U * (int64_t)blockDim.x) {
-    bool m[U];
+  for (int64_t c0 = 0; c0 < LB; c0 += CH) {
+    const int nc = (int)min((int64_t)CH, LB - c0);
+    const int cnt = tid < nc ? (int)a.img[(c0 + tid) * 4 + 3] : 0;
+    int incl = cnt;  // inclusive scan within the wave
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t r = r0 + u * (int64_t)blockDim.x + threadIdx.x;
-      m[u] = r < n && a.pred_to_gt[r] >= 0;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      incl += lane >= o ? y : 0;
     }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t r = r0 + u * (int64_t)blockDim.x + threadIdx.x;
-      const uint64_t bal = __ballot(m[u]);
-      if (lane == 0) wcnt[wave] = __popcll(bal);
-      __syncthreads();
-      int off = base, tot = base;
-      for (int w = 0; w < nw; ++w) {
-        off += w < wave ? wcnt[w] : 0;
-        tot += wcnt[w];
+    if (lane == 63) wtot[wave] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < nw; ++w) {
+      before += w < wave ? wtot[w] : 0;
+      total += wtot[w];
+    }
+    if (tid < nc) {
+      sbuf[tid] = before + incl - cnt;  // exclusive prefix within the chunk
+      sbuf[CH + tid] = cnt;
+    }
+    __syncthreads();
+    for (int g = tid; g < total; g += nt) {
+      // the last slice whose prefix is <= g holds output g
+      int lo = 0, hi = nc - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sbuf[mid] <= g) lo = mid;
+        else hi = mid - 1;
       }
-      if (m[u]) a.list[1 + off + __popcll(bal & below)] = (int)r;
-      __syncthreads();
-      base = tot;
+      a.list[1 + base + g] = a.mrows[(c0 + lo) * a.Q + (g - sbuf[lo])];
     }
+    base += total;
+    __syncthreads();  // sbuf and wtot are reused by the next chunk
   }
-  if (threadIdx.x == 0) a.list[0] = base;
+  if (tid == 0) a.list[0] = base;
 }
 
 // CM: where the image's cost rows live (CostRows): all in LDS when the
@@ -709,8 +722,10 @@ __device__ void layer_pass(const LayerArgs& a) {
 // in place from finalize's total-cost plane.
 // Workgroups L*B .. L*B + fill_blocks - 1 zero-fill the gradient buffer:
 // the assignment keeps one CU per image busy with a serial chain and leaves
-// HBM idle, so the fill runs beside it in the same launch.
-constexpr uint64_t kGateTicks = 3000;  // 30 us of the 100 MHz real-time counter
+// HBM idle, so the fill runs beside it in the same launch, from its start
+// (the fill's writes slow the images' row staging a little, which the
+// solvers' slack absorbs: measured 7 us shorter than a fill that waits for
+// the staging).
 
 // Copy the cost rows of image b's non-empty GT columns (colmap order) from
 // finalize's plane into LDS (those CM keeps there) and mark the valid ones (a cost that is
@@ -762,15 +777,6 @@ __device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int6
 template <int NJ, int CM>
 __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   if ((int64_t)blockIdx.x >= a.L * a.B) {
-    // Start once every image's cost matrix is staged (the fill's writes would
-    // otherwise stretch those reads several times), or after kGateTicks.
-    if (threadIdx.x == 0) {
-      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-      while (__hip_atomic_load(a.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < a.L * a.B &&
-             __builtin_amdgcn_s_memrealtime() - t0 < kGateTicks)
-        __builtin_amdgcn_s_sleep(4);
-    }
-    __syncthreads();
     zero_fill_range(a.fill, a.fill_n16, a.fill_tail, a.fill_ntail,
                     (int64_t)blockIdx.x - a.L * a.B, a.fill_blocks);
     return;
@@ -812,7 +818,6 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   if ((Q & 3) == 0) stage_rows<4, NJ, CM>(a, lb, b, costL, a.lds_rows, colok);
   else stage_rows<1, NJ, CM>(a, lb, b, costL, a.lds_rows, colok);
   __syncthreads();
-  if (tid == 0 && a.fill_blocks) __hip_atomic_fetch_add(a.gate, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- 2. assignment on wave 0
   if (wave == 0) {
@@ -944,6 +949,10 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       nm += __popcll(m);
     }
     wave_sync();
+    if (a.layer_args.list) {  // this slice's part of the saved matched-row list
+      int* mr = a.layer_args.mrows + lb * Q;
+      for (int k = lane; k < nm; k += 64) mr[k] = (int)(lb * Q + mq[k]);
+    }
     for (int64_t q = lane; q < Q; q += 64) {
       const int c = p2g[q];
       int64_t rnd = -1;
@@ -1034,12 +1043,15 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
       __threadfence();
     }
     __syncthreads();
-    if (last) layer_pass(a.layer_args);
+    if (last) layer_pass(a.layer_args, (int*)smem, (int)(L.total / 4));
   }
 }
 
 
-__global__ __launch_bounds__(1024) void layer_kernel(LayerArgs a) { layer_pass(a); }
+__global__ __launch_bounds__(1024) void layer_kernel(LayerArgs a) {
+  __shared__ int sbuf[2048];
+  layer_pass(a, sbuf, 2048);
+}
 
 // Denominators from pred_to_gt alone (backward without saved statistics,
 // src/cuda/mask_matching_backward.cu:480-508).  One wave per layer.

@@ -202,8 +202,9 @@ Layout make_layout(const Dims& d, bool force_masks, const CostPlan& pl) {
   L.rowIT = take((size_t)d.LB * d.Q * d.nslot * 8);
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
   L.img = take((size_t)d.LB * 4 * 4);
+  L.mrows = take((size_t)d.LB * d.Q * 4);
   L.layer = take((size_t)d.L * ML_LAYERS * 4);
-  L.gate = take(16);
+  L.done = take(16);
   L.total = o;
   return L;
 }
@@ -393,8 +394,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.fill_n16 = (int64_t)(prefill_bytes / 16);
   aa.fill_tail = (unsigned char*)prefill + prefill_bytes / 16 * 16;
   aa.fill_ntail = (int64_t)(prefill_bytes % 16);
-  aa.gate = (int*)(w + L.gate);
-  aa.done = costs_only ? nullptr : (int*)(w + L.gate) + 1;
+  aa.done = costs_only ? nullptr : (int*)(w + L.done);
   aa.fill_blocks = prefill_bytes && !costs_only
                        ? (int)std::min<int64_t>(kFillBlocks, std::max<int64_t>(1, ceil_div(aa.fill_n16, 256)))
                        : 0;
@@ -439,6 +439,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   la.means = layer_means;
   la.pred_to_gt = pred_to_gt;
   la.list = saved ? (int*)(sv + SL.list) : nullptr;
+  la.mrows = (int*)(w + L.mrows);
   la.L = d.L; la.B = d.B; la.Q = d.Q;
   la.num_masks = p->num_masks;
   la.force_masks = force_masks;

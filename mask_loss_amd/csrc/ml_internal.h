@@ -168,7 +168,7 @@ inline SavedLayout saved_layout(const Dims& d) {
 // Byte offsets inside the caller's workspace.
 struct Layout {
   size_t lab16, counts, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
-      sep, tot, rowIT, rowstat, img, layer, gate, total;
+      sep, tot, rowIT, rowstat, img, mrows, layer, done, total;
 };
 // Workspace layout for the cost plan `pl` (its float_total / slot_total size
 // the partial-sum regions).
@@ -235,6 +235,8 @@ struct LayerArgs {
   float* means;        // (3, L)
   const int64_t* pred_to_gt;
   int* list;           // matched-row list of the saved state, or null
+  int* mrows;          // [L*B][Q]: slice lb's matched rows (lb * Q + q, ascending), its
+                       // count in img[lb * 4 + 3]; written by the assignment when list is set
   int64_t L, B, Q;
   double num_masks;
   int force_masks, force_cls, has_void;
@@ -271,9 +273,6 @@ struct AssignArgs {
   unsigned char* fill_tail;
   int64_t fill_ntail;
   int fill_blocks;
-  // fill start gate: finalize zeroes it, each assignment workgroup adds 1 once
-  // its cost matrix is staged, and the fill workgroups wait (bounded) for L*B
-  int* gate;
   // finished-image count (zeroed by finalize): the assignment workgroup that
   // finishes last runs the per-layer pass `layer_args`, or done == null
   int* done;

@@ -155,8 +155,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   __shared__ float sl[4][3][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // 32-bit index arithmetic: the host checks L * B * Q < 2^31
+  const uint32_t nrows = (uint32_t)(a.L * a.B * a.Q), nrow_blocks = (nrows + 3u) / 4u;
+  if (blockIdx.x >= nrow_blocks) {  // the launch's slice of the gradient's zero fill
+    fill_slice(a.fin_fill, blockIdx.x - nrow_blocks);
+    return;
+  }
   const uint32_t row32 = blockIdx.x * 4u + (uint32_t)wave;
-  if (row32 >= (uint32_t)(a.L * a.B * a.Q)) return;
+  if (row32 >= nrows) return;
   const uint32_t lb32 = row32 / (uint32_t)a.Q;
   const int64_t row = row32, lb = lb32, q = row32 - lb32 * (uint32_t)a.Q, b = lb32 % (uint32_t)a.B;
   const int64_t GTo = a.GT_out, C = a.C;
@@ -321,8 +326,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
     if (a.out_dice) a.out_dice[o] = dice;
     if (labels) a.sep[2 * term + o] = cls;
     // total cost, matching.cpp:665, stored [column][query]: the assignment
-    // reads cost rows of one GT across all queries
-    if (a.tot) a.tot[lb * a.tot_stride + c * a.Q + q] = (bce + dice) + cls;
+    // reads cost rows of one GT across all queries.  A NaN stands for every
+    // non-finite total, so the assignment tests a cost with one comparison
+    // (raw < inf_thresh is cost_ok(raw)).
+    if (a.tot) {
+      const float t = (bce + dice) + cls;
+      a.tot[lb * a.tot_stride + c * a.Q + q] = __builtin_isfinite(t) ? t : __builtin_nanf("");
+    }
   };
   if constexpr (FAST) {
 #pragma unroll
@@ -362,11 +372,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
 // ---------------------------------------------------------------------------
 // wave64 helpers: DPP lane exchanges and a min-reduction without LDS traffic
 // ---------------------------------------------------------------------------
-template <int CTRL>
-__device__ __forceinline__ double dpp_d(double v) {
+// DPP move of one float64 with no initial value: the callers use only the
+// lanes that the control word writes.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double mov_dpp_d(double v) {
   const uint64_t u = (uint64_t)__double_as_longlong(v);
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)u, CTRL, ROWS, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), CTRL, ROWS, 0xF, false);
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 __device__ __forceinline__ double readlane_d(double v, int lane) {
@@ -375,56 +387,76 @@ __device__ __forceinline__ double readlane_d(double v, int lane) {
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
   return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
-// (value, column) pairs ordered by value, then by column: the reference's
-// argmin picks the lowest column index among equal minima (strict '<' in
-// an ascending scan, src/cpu/matching.cpp:146-149).
-__device__ __forceinline__ void lex_take(double& v, int& j, double ov, int oj) {
-  // bitwise, not short-circuit: no branch per comparison
-  const bool take = (ov < v) | ((ov == v) & (oj < j));
-  v = take ? ov : v;
-  j = take ? oj : j;
+// The high word of a float64, and a float64 with its high word replaced.
+__device__ __forceinline__ uint32_t hi_word(double x) {
+  return (uint32_t)((uint64_t)__double_as_longlong(x) >> 32);
 }
-template <int CTRL>
-__device__ __forceinline__ void lex_dpp(double& v, int& j) {
-  const double ov = dpp_d<CTRL>(v);
-  const int oj = __builtin_amdgcn_update_dpp(0, j, CTRL, 0xF, 0xF, false);
-  lex_take(v, j, ov, oj);
+__device__ __forceinline__ double with_hi(double x, uint32_t hi) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | (uint32_t)u));
 }
-// Lexicographic minimum of (v, j) over the wave, returned in every lane:
-// four DPP levels within each row of 16 lanes, then the four row results
-// through readlane.
-__device__ __forceinline__ void wave_argmin_dpp(double& v, int& j) {
-  lex_dpp<0xB1>(v, j);   // quad_perm [1,0,3,2]
-  lex_dpp<0x4E>(v, j);   // quad_perm [2,3,0,1]
-  lex_dpp<0x141>(v, j);  // row_half_mirror
-  lex_dpp<0x140>(v, j);  // row_mirror
-  double bv = readlane_d(v, 0);
-  int bj = __builtin_amdgcn_readlane(j, 0);
-#pragma unroll
-  for (int r = 16; r < 64; r += 16) lex_take(bv, bj, readlane_d(v, r), __builtin_amdgcn_readlane(j, r));
-  v = bv;
-  j = bj;
+// v_min_f64 as the hardware does it in IEEE mode (the kernels' mode): a quiet
+// NaN operand yields the other operand.  Written out so that the compiler
+// adds no canonicalising instructions around it.
+__device__ __forceinline__ double min_f64(double a, double b) {
+  double r;
+  asm("v_min_f64 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+// Minimum of v over the wave (quiet NaNs ignored), wave-uniform: four DPP
+// levels within each row of 16 lanes, then row_bcast:15 into rows 1 and 3
+// and row_bcast:31 into rows 2 and 3 leave the wave's minimum in lane 63.
+__device__ __forceinline__ double wave_min_f64(double v) {
+  v = min_f64(v, mov_dpp_d<0xB1, 0xF>(v));   // quad_perm [1,0,3,2]
+  v = min_f64(v, mov_dpp_d<0x4E, 0xF>(v));   // quad_perm [2,3,0,1]
+  v = min_f64(v, mov_dpp_d<0x141, 0xF>(v));  // row_half_mirror
+  v = min_f64(v, mov_dpp_d<0x140, 0xF>(v));  // row_mirror
+  v = min_f64(v, mov_dpp_d<0x142, 0xA>(v));  // row_bcast:15
+  v = min_f64(v, mov_dpp_d<0x143, 0xC>(v));  // row_bcast:31
+  return readlane_d(v, 63);
+}
+// Index of the lowest set bit of a 64-bit lane mask, -1 (all ones) when the
+// mask is empty (s_ff1_i32_b64).
+__device__ __forceinline__ uint32_t first_lane(uint64_t m) {
+  return m ? (uint32_t)__builtin_ctzll(m) : 0xFFFFFFFFu;
 }
 // Register slot t (wave-uniform) of lane l: the slot is selected in every
-// lane first, then one readlane fetches lane l's.  Each comparison takes its
-// own opaque copy of t, so the compiler cannot turn the select chain into a
-// dynamically indexed array (which it would place in scratch memory).
-__device__ __forceinline__ bool slot_is(int t, int k) {
-  asm volatile("" : "+s"(t));
-  return t == k;
-}
+// lane first, then one readlane fetches lane l's.  SlotMask's comparisons
+// t == k each take their own opaque copy of t, and an empty volatile asm
+// statement separates the steps of a select chain: otherwise the compiler
+// turns the chain into a dynamically indexed array (which it places in
+// scratch memory).
 template <int NJ>
-__device__ __forceinline__ int sel_i(const int (&x)[NJ], int t, int l) {
+struct SlotMask {
+  bool is[NJ];
+  __device__ __forceinline__ explicit SlotMask(int t) {
+    t = __builtin_amdgcn_readfirstlane(t);
+#pragma unroll
+    for (int k = 0; k < NJ; ++k) {
+      int c = t;
+      asm volatile("" : "+s"(c));
+      is[k] = c == k;
+    }
+  }
+};
+template <int NJ>
+__device__ __forceinline__ int sel_i(const int (&x)[NJ], const SlotMask<NJ>& m, int l) {
   int r = x[0];
 #pragma unroll
-  for (int k = 1; k < NJ; ++k) r = slot_is(t, k) ? x[k] : r;
+  for (int k = 1; k < NJ; ++k) {
+    asm volatile("");
+    r = m.is[k] ? x[k] : r;
+  }
   return __builtin_amdgcn_readlane(r, l);
 }
 template <int NJ>
-__device__ __forceinline__ double sel_d(const double (&x)[NJ], int t, int l) {
+__device__ __forceinline__ double sel_d(const double (&x)[NJ], const SlotMask<NJ>& m, int l) {
   double r = x[0];
 #pragma unroll
-  for (int k = 1; k < NJ; ++k) r = slot_is(t, k) ? x[k] : r;
+  for (int k = 1; k < NJ; ++k) {
+    asm volatile("");
+    r = m.is[k] ? x[k] : r;
+  }
   return readlane_d(r, l);
 }
 
@@ -437,13 +469,22 @@ __device__ __forceinline__ double sel_d(const double (&x)[NJ], int t, int l) {
 // potential v, its matched row p (0 = free), and, for that row, the row
 // potential u[p] and its cost-matrix row; the row being inserted keeps its
 // potential and cost row in wave-uniform registers.  So the Dijkstra steps
-// touch LDS only for the cost entries: every potential update is a register
-// add, the row of a newly reached column is a readlane, and the argmin is one
-// DPP reduction over (minv, column) pairs, which also yields the column.  The
-// relaxation of a lane's NJ columns has no branches, so its chains
-// interleave.  Each row potential receives the same float64 additions in
-// the same order as in the reference (one += delta per step in which its
-// column is in the tree), so the assignment is the reference's bit for bit.
+// touch LDS only for the cost entries, and every potential update is a
+// register operation.  A column in the tree (and an unused slot) holds a
+// quiet NaN in minv: no relaxation updates it (cur < NaN is false), the
+// minimum ignores it (v_min_f64) and no comparison with delta matches it,
+// so the steps carry no separate "used" state.  delta is one float64 DPP
+// minimum over the wave; the entering column is the lowest one whose minv
+// equals delta (one ballot per slot, its lowest lane, the lowest slot): the
+// reference's scan keeps the first of equal minima (strict '<',
+// src/cpu/matching.cpp:146-149), and a column's index grows with its slot,
+// then its lane.  The next cost row's reads are issued as soon as its
+// column is known, before the potential updates.  Each potential receives
+// the same float64 operations in the same order as in the reference (one
+// += delta or -= delta per step; a column outside the tree adds delta x 0,
+// which leaves the value, up to the sign of a zero, which no later
+// comparison or sum can see), so the assignment is the reference's bit for
+// bit.
 // ---------------------------------------------------------------------------
 // Cost rows of one image, [column][query] with row stride ldq: rows c < nl
 // in LDS, the others read in place from finalize's total-cost plane (L2).
@@ -458,9 +499,9 @@ struct CostRows {
   // and never a flat load through a pointer chosen at run time
   const lds_f32* lds;
   const global_f32* glb;
-  int64_t ldq;
-  int64_t nl;
-  __device__ __forceinline__ bool in_lds(int64_t c) const {
+  int ldq;  // c * ldq fits 31 bits: Q <= 1024, and the column arrays fit the LDS
+  int nl;
+  __device__ __forceinline__ bool in_lds(int c) const {
     return CM == kCostLds || (CM == kCostSplit && c < nl);
   }
   // one element (per-lane column): split mode reads the plane in place, where
@@ -471,6 +512,24 @@ struct CostRows {
   }
 };
 
+// The row of column col, at the slots' query indices: a wave-uniform branch
+// between a ds_read row and an in-place global row.
+template <int NJ, int CM>
+__device__ __forceinline__ void read_cost_row(const CostRows<CM>& cost, int col,
+                                              const int (&predj)[NJ], float (&rawf)[NJ]) {
+  if (cost.in_lds(col)) {
+    const lds_f32* crow = cost.lds + col * cost.ldq;
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+  } else {
+    const global_f32* crow = cost.glb + (uint32_t)(col * cost.ldq);
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+  }
+}
+
+// thr: the cost threshold.  The cost plane holds a NaN for every non-finite
+// cost (finalize_kernel), so `raw < thr` is cost_ok(raw).
 template <int NJ, int CM>
 __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n,
                                const int* hrows, int M, double thr, double BIG, int* p, int* way,
@@ -482,6 +541,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
   for (int k = lane; k < n; k += 64) asg[k] = -1;
   wave_sync();
   if (M == 0 || n == 0 || n < M) return true;
+  const double kQNaN = __longlong_as_double(0x7FF8000000000000ll);
   double v[NJ], ucol[NJ];
   int pj[NJ], rcol[NJ], predj[NJ];
   bool valid[NJ];
@@ -497,73 +557,66 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
   }
   bool ok = true;
   for (int i = 1; i <= M && ok; ++i) {
-    double minv[NJ];
+    // minv: a quiet NaN marks a column in the tree (and an unused slot);
+    // f: 1.0 for a column in the tree, else 0.0 (its low word stays 0)
+    double minv[NJ], f[NJ];
     int wy[NJ];
-    unsigned used = 0;  // bit t: column 1 + lane + 64 t is in the tree
 #pragma unroll
     for (int t = 0; t < NJ; ++t) {
-      minv[t] = INFINITY;
+      minv[t] = valid[t] ? INFINITY : kQNaN;
+      f[t] = 0.0;
       wy[t] = 0;
     }
     double ucur = 0.0;  // potential of row i (column 0 of the reference)
-    const int colcur = hrows[i - 1];
+    const int colcur = __builtin_amdgcn_readfirstlane(hrows[i - 1]);
     int j0 = 0;
     double ui0 = ucur;
-    int col = colcur;
+    float rawf[NJ];
+    read_cost_row<NJ, CM>(cost, colcur, predj, rawf);
     for (;;) {
-      float rawf[NJ];  // all reads issued together (predj is in range for every lane)
-      if (cost.in_lds(col)) {  // wave-uniform
-        const lds_f32* crow = cost.lds + (int64_t)col * cost.ldq;
-#pragma unroll
-        for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
-      } else {
-        const global_f32* crow = cost.glb + (int64_t)col * cost.ldq;
-#pragma unroll
-        for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
-      }
-      // relax every free column (no branches: the NJ chains interleave) and
-      // keep this lane's lexicographic (minv, column) minimum; slots ascend
-      // in column index, so a strict '<' keeps the lowest column on ties
-      double bv = INFINITY;
-      int bj = 0x7FFFFFFF;
+      // relax every column outside the tree (no branches: the NJ chains
+      // interleave) and keep this lane's minimum
+      double lmin = INFINITY;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const bool act = valid[t] && !((used >> t) & 1u);
         const double raw = (double)rawf[t];
-        const double cij = cost_ok(raw, thr) ? raw : BIG;
+        const double cij = raw < thr ? raw : BIG;
         const double cur = cij - ui0 - v[t];
-        const bool upd = act && cur < minv[t];
+        const bool upd = cur < minv[t];
         minv[t] = upd ? cur : minv[t];
         wy[t] = upd ? j0 : wy[t];
-        const bool better = act && minv[t] < bv;
-        bv = better ? minv[t] : bv;
-        bj = better ? 1 + lane + 64 * t : bj;
+        lmin = min_f64(lmin, minv[t]);
       }
-      wave_argmin_dpp(bv, bj);
-      const double delta = bv;
-      if (!isfinite(delta)) {  // unreachable with finite costs (n >= M free columns)
+      const double delta = wave_min_f64(lmin);
+      if (!(delta < INFINITY)) {  // unreachable with finite costs (n >= M free columns)
         ok = false;
         break;
       }
-      const int j1 = bj;
-      // potentials: columns in the tree (and column 0 = row i), others' minv;
-      // invalid slots keep minv = +inf and are never in the tree
+      // key = j1 - 1 of the entering column: the lowest (slot, lane) whose
+      // minv equals delta (an empty slot gives all ones)
+      uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+      for (int t = 0; t < NJ; ++t)
+        key = min(key, first_lane(__builtin_amdgcn_ballot_w64(minv[t] == delta)) | (uint32_t)(64 * t));
+      // potentials: columns in the tree (and column 0 = row i) move by delta
+      // (f = 1), the others' minv by -delta; then column j1 enters the tree
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const bool in_tree = (used >> t) & 1u;
-        ucol[t] = in_tree ? ucol[t] + delta : ucol[t];
-        v[t] = in_tree ? v[t] - delta : v[t];
-        minv[t] = in_tree ? minv[t] : minv[t] - delta;
+        ucol[t] = __builtin_fma(delta, f[t], ucol[t]);
+        v[t] = __builtin_fma(-delta, f[t], v[t]);
+        const bool enter = lane + 64 * t == (int)key;
+        minv[t] = with_hi(minv[t] - delta, enter ? 0x7FF80000u : hi_word(minv[t] - delta));
+        f[t] = with_hi(f[t], enter ? 0x3FF00000u : hi_word(f[t]));
       }
       ucur += delta;
-      const int ol = (j1 - 1) & 63, ot = (j1 - 1) >> 6;
-      if (lane == ol) used |= 1u << ot;
-      j0 = j1;
-      const int pj0 = sel_i<NJ>(pj, ot, ol);
-      if (pj0 == 0) break;
-      // next row of the tree: the one matched to column j1
-      ui0 = sel_d<NJ>(ucol, ot, ol);
-      col = sel_i<NJ>(rcol, ot, ol);
+      j0 = (int)key + 1;
+      const int ol = (int)(key & 63u), ot = (int)(key >> 6);
+      const SlotMask<NJ> sm(ot);
+      if (sel_i<NJ>(pj, sm, ol) == 0) break;  // j1 is free: augment
+      // next row of the tree: the one matched to column j1 (its potential
+      // took no delta above: j1 was outside the tree)
+      ui0 = sel_d<NJ>(ucol, sm, ol);
+      read_cost_row<NJ, CM>(cost, sel_i<NJ>(rcol, sm, ol), predj, rawf);
     }
     if (!ok) break;
     // augment along way[] from the free column j0 back to column 0: each
@@ -571,7 +624,8 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     // row) of the column it was reached from; column 0 holds row i.
     for (int steps = 0; j0 != 0 && steps <= n; ++steps) {
       const int ol = (j0 - 1) & 63, ot = (j0 - 1) >> 6;
-      const int jp = sel_i<NJ>(wy, ot, ol);
+      const SlotMask<NJ> sm(ot);
+      const int jp = sel_i<NJ>(wy, sm, ol);
       int np, nr;
       double nu;
       if (jp == 0) {
@@ -580,13 +634,15 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         nr = colcur;
       } else {
         const int pl = (jp - 1) & 63, pt = (jp - 1) >> 6;
-        np = sel_i<NJ>(pj, pt, pl);
-        nu = sel_d<NJ>(ucol, pt, pl);
-        nr = sel_i<NJ>(rcol, pt, pl);
+        const SlotMask<NJ> pm(pt);
+        np = sel_i<NJ>(pj, pm, pl);
+        nu = sel_d<NJ>(ucol, pm, pl);
+        nr = sel_i<NJ>(rcol, pm, pl);
       }
+      const bool me = lane == ol;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const bool mine = lane == ol && t == ot;
+        const bool mine = me & sm.is[t];
         pj[t] = mine ? np : pj[t];
         ucol[t] = mine ? nu : ucol[t];
         rcol[t] = mine ? nr : rcol[t];
@@ -803,8 +859,8 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   CostRows<CM> crows;
   crows.lds = (const lds_f32*)costL;
   crows.glb = (const global_f32*)(a.tot + lb * a.tot_stride);
-  crows.ldq = Q;
-  crows.nl = a.lds_rows;
+  crows.ldq = (int)Q;
+  crows.nl = (int)a.lds_rows;
   const int64_t term = a.L * a.B * Q * GTo;
   const float* sep = a.sep + lb * Q * GTo;
 
@@ -1122,7 +1178,7 @@ int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   if (rows == 0) return ML_OK;
   if (rows >= ((int64_t)1 << 31)) return fail(ML_EINVAL, "L * B * Q must be below 2^31");
   ProfScope ps_("finalize", st);
-  const dim3 grid((unsigned)ceil_div(rows, 4));
+  const dim3 grid((unsigned)(ceil_div(rows, 4) + a.fin_fill.blocks));
   const bool fast = a.cls_logits && a.C >= 1 && a.C <= 64 * kFinCls && a.GT_out >= 1 &&
                     a.GT_out <= 64 * kFinCols;
   const int dt = a.cls_logits ? a.cls_dtype : ML_BF16;

@@ -305,8 +305,25 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   if (ws_bytes < need) return fail(ML_EWORKSPACE, "workspace too small");
   unsigned char* w = (unsigned char*)ws;
   int rc;
+  // the gradient's zero fill (16-byte words): slices for the column pass and
+  // the finalize launch, the rest (and any tail bytes) for the assignment
+  // launch, or one fill kernel without an assignment launch
+  const size_t prefill_bytes =
+      prefill && !costs_only ? (size_t)(d.LB * d.Q * d.HW) * (mask_dtype == ML_F32 ? 4 : 2) : 0;
+  const int64_t fill_n16 = (int64_t)(prefill_bytes / 16);
+  auto slice = [&](int64_t from, int64_t cap) {
+    FillSlice f;
+    f.n16 = d.LB > 0 ? std::max<int64_t>(0, std::min<int64_t>(fill_n16 - from, cap / 16)) : 0;
+    f.p = f.n16 ? (u32x4_t*)prefill + from : nullptr;
+    f.blocks = f.n16 ? (int)std::min<int64_t>(kFillBlocks, ceil_div(f.n16, 1024)) : 0;
+    return f;
+  };
+  const FillSlice prep_fill = slice(0, kPrepFillBytes);
+  const FillSlice fin_fill = slice(prep_fill.n16, kFinFillBytes);
+  const int64_t assign_from = prep_fill.n16 + fin_fill.n16;
 
   PrepArgs pa;
+  pa.fill = prep_fill;
   pa.targets = mask_targets;
   // with a saved state the compact labels go straight into it (the backward reuses them)
   pa.lab16 = (uint16_t*)(saved && !d.counts_mode ? sv + SL.lab16 : w + L.lab16);
@@ -387,15 +404,14 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.pred_round = pred_round;
   aa.stats = stats;
   aa.img = (float*)(w + L.img);
-  // the gradient's zero fill: extra workgroups of the assignment launch
-  const size_t prefill_bytes =
-      prefill ? (size_t)(d.LB * d.Q * d.HW) * (mask_dtype == ML_F32 ? 4 : 2) : 0;
-  aa.fill = (u32x4_t*)prefill;
-  aa.fill_n16 = (int64_t)(prefill_bytes / 16);
+  // the rest of the gradient's zero fill: extra workgroups of the assignment launch
+  aa.fin_fill = fin_fill;
+  aa.fill = (u32x4_t*)prefill + assign_from;
+  aa.fill_n16 = fill_n16 - assign_from;
   aa.fill_tail = (unsigned char*)prefill + prefill_bytes / 16 * 16;
   aa.fill_ntail = (int64_t)(prefill_bytes % 16);
   aa.done = costs_only ? nullptr : (int*)(w + L.done);
-  aa.fill_blocks = prefill_bytes && !costs_only
+  aa.fill_blocks = prefill_bytes
                        ? (int)std::min<int64_t>(kFillBlocks, std::max<int64_t>(1, ceil_div(aa.fill_n16, 256)))
                        : 0;
   aa.L = d.L; aa.B = d.B; aa.Q = d.Q; aa.C = d.C; aa.HW = d.HW; aa.Ht = d.Ht; aa.Wt = d.Wt;

@@ -33,6 +33,12 @@ constexpr int kPresLabels = 32 * kPresWords;
 // assignment (measured on MI355X: 64 still write at the full rate while
 // leaving the other CUs to the latency-bound assignment).
 constexpr int kFillBlocks = 64;
+// Slices of that fill given instead to the preparation's column pass and to
+// the finalize launch, as extra workgroups beside their own work: both are
+// short, latency-bound launches that leave HBM nearly idle, so these bytes
+// come off the assignment launch, where the fill outlasts a short assignment.
+constexpr int64_t kPrepFillBytes = (int64_t)24 << 20;
+constexpr int64_t kFinFillBytes = (int64_t)48 << 20;
 
 // Column-tile classes of the cost contraction: an image with G non-empty GT
 // columns (+ the ones column) is handled by the kernel instance whose tile
@@ -184,10 +190,19 @@ CostPlan bound_cost_plan(const Dims& d);
 void pack_cost_plan(CostPlan& p, const Dims& d);
 
 // ---- kernel argument blocks ------------------------------------------------
+// Part of the gradient's zero fill done by `blocks` extra workgroups of a
+// launch: 16-byte words [0, n16) from p.
+struct FillSlice {
+  u32x4_t* p = nullptr;
+  int64_t n16 = 0;
+  int blocks = 0;
+};
+
 struct PrepArgs {
   const int64_t* targets;
   uint16_t* lab16;
   uint8_t* counts;       // s > 1: [B][GT_total][HWp] counts of cw bytes each
+  FillSlice fill;        // done by extra workgroups of the column pass
   int cw = 1;
   // forward only (else null): per preparation workgroup, kPresWords words of
   // presence bits of its GT labels, [B][nblk][kPresWords]; every word is
@@ -268,6 +283,7 @@ struct AssignArgs {
   float* img;            // [LB][4]: mask, dice, cls sums, matched count
   // gradient zero-fill done by extra workgroups of the assignment launch
   // (blockIdx.x >= L*B), or fill_blocks == 0
+  FillSlice fin_fill;  // done by extra workgroups of the finalize launch
   u32x4_t* fill;
   int64_t fill_n16;
   unsigned char* fill_tail;
@@ -403,13 +419,13 @@ size_t dense_partials_bytes(int64_t L, int64_t B, int64_t C, int64_t HW, bool di
 int launch_zero_fill(void* p, size_t bytes, hipStream_t st);
 
 // Zero `n16` 16-byte words, then `ntail` trailing bytes, as workgroup `blk`
-// of `nblk` (256 threads each).  Streaming (non-temporal) stores: the buffer
+// of `nblk` (of equal size).  Streaming (non-temporal) stores: the buffer
 // is a gradient that is not read again before the backward, so it should not
 // displace the forward's working set from the L2.
 __device__ inline void zero_fill_range(u32x4_t* p, int64_t n16, unsigned char* tail,
                                        int64_t ntail, int64_t blk, int64_t nblk) {
-  const int64_t stride = nblk * 256;
-  int64_t i = blk * 256 + threadIdx.x;
+  const int64_t nt = blockDim.x, stride = nblk * nt;
+  int64_t i = blk * nt + threadIdx.x;
   const u32x4_t z = {0u, 0u, 0u, 0u};
   for (; i + 3 * stride < n16; i += 4 * stride) {
     __builtin_nontemporal_store(z, p + i);
@@ -419,6 +435,9 @@ __device__ inline void zero_fill_range(u32x4_t* p, int64_t n16, unsigned char* t
   }
   for (; i < n16; i += stride) __builtin_nontemporal_store(z, p + i);
   if (blk == 0 && threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+__device__ inline void fill_slice(const FillSlice& f, int64_t blk) {
+  zero_fill_range(f.p, f.n16, nullptr, 0, blk, f.blocks);
 }
 int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, hipStream_t st);
 

@@ -279,8 +279,15 @@ __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
   }
 }
 
-// One workgroup: runs once every presence record of the preparation grid is in.
-__global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) { columns_and_schedule(a); }
+// Workgroup 0: runs once every presence record of the preparation grid is
+// in.  Workgroups 1 .. a.fill.blocks: a slice of the gradient's zero fill.
+__global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) {
+  if (blockIdx.x > 0) {
+    fill_slice(a.fill, blockIdx.x - 1);
+    return;
+  }
+  columns_and_schedule(a);
+}
 
 // Preparation workgroups per image (the presence records' count).
 int prep_blocks(const Dims& d) {
@@ -303,7 +310,7 @@ int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   }
   if ((rc = check_launch("prep"))) return rc;
   if (a.pbits) {
-    hipLaunchKernelGGL(prep_columns_kernel, dim3(1), dim3(1024), 0, st, a);
+    hipLaunchKernelGGL(prep_columns_kernel, dim3(1u + (unsigned)a.fill.blocks), dim3(1024), 0, st, a);
     if ((rc = check_launch("prep_columns"))) return rc;
   }
   return ML_OK;
@@ -338,7 +345,7 @@ int launch_prep_points(const PrepArgs& a, const Dims& d, int64_t Hs, int64_t Ws,
   if (rc) return rc;
   rc = launch_point_labels(a.targets, coords, d.B, Hs, Ws, d.HW, a.GT_total, nullptr, a.lab16, d.HWp, st);
   if (rc) return rc;
-  hipLaunchKernelGGL(prep_columns_kernel, dim3(1), dim3(1024), 0, st, a);
+  hipLaunchKernelGGL(prep_columns_kernel, dim3(1u + (unsigned)a.fill.blocks), dim3(1024), 0, st, a);
   return check_launch("prep_columns");
 }
 

@@ -245,13 +245,14 @@ int ml_point_sample(int dtype, const void* input, const float* coords, int64_t N
 /* ml_point_sample_backward: grad_input (N,C,H,W) = the gradient of
  *   ml_point_sample with respect to its input, for grad_out (N,C,P), both in
  *   `dtype`: each sample's gradient added to its four corner cells with its
- *   bilinear weights (grid_sample's input gradient, functions/utils.py:17;
- *   float atomics, so the last bits depend on their order, as with the
- *   reference's CUDA grid_sample backward).  Every cell of grad_input is
- *   written.  Workspace: ml_point_sample_backward_workspace_size bytes (0 when
- *   a plane's float accumulators fit 64 KB of LDS). */
+ *   bilinear weights (grid_sample's input gradient, functions/utils.py:17).
+ *   A cell's contributions are summed in float32 in an order that can change
+ *   between runs, as with the reference's CUDA grid_sample backward (float
+ *   atomics).  Every cell of grad_input is written.  Workspace:
+ *   ml_point_sample_backward_workspace_size bytes for the same shape,
+ *   P and coords_batch (0 for some shapes). */
 size_t ml_point_sample_backward_workspace_size(int dtype, int64_t N, int64_t C, int64_t H,
-                                               int64_t W);
+                                               int64_t W, int64_t P, int64_t coords_batch);
 int ml_point_sample_backward(int dtype, const void* grad_out, const float* coords, int64_t N,
                              int64_t C, int64_t H, int64_t W, int64_t P, int64_t coords_batch,
                              int align_corners, void* grad_input, float* workspace,

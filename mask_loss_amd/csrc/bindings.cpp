@@ -475,7 +475,7 @@ torch::Tensor point_sample_backward(const torch::Tensor& grad_out, const torch::
   TORCH_CHECK(H > 0 && W > 0, "point_sample backward: input must have positive spatial size");
   const int dt = dtype_code(grad_out, "grad");
   auto gin = torch::empty({N, C, H, W}, grad_out.options());
-  const size_t wsb = ml_point_sample_backward_workspace_size(dt, N, C, H, W);
+  const size_t wsb = ml_point_sample_backward_workspace_size(dt, N, C, H, W, P, std::max<int64_t>(N, 1));
   auto ws = workspace(wsb, grad_out);
   ml_ok(ml_point_sample_backward(dt, grad_out.data_ptr(), coords.data_ptr<float>(), N, C, H, W, P,
                                  std::max<int64_t>(N, 1), align_corners ? 1 : 0, gin.data_ptr(),

@@ -621,9 +621,10 @@ int ml_point_sample(int dtype, const void* input, const float* coords, int64_t N
                              (hipStream_t)stream);
 }
 
-size_t ml_point_sample_backward_workspace_size(int dtype, int64_t N, int64_t C, int64_t H, int64_t W) {
-  if (N < 0 || C < 0 || H <= 0 || W <= 0 || !dtype_ok(dtype)) return 0;
-  return point_sample_bwd_workspace(dtype, N, C, H, W);
+size_t ml_point_sample_backward_workspace_size(int dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+                                               int64_t P, int64_t coords_batch) {
+  if (N < 0 || C < 0 || H <= 0 || W <= 0 || P < 0 || coords_batch <= 0 || !dtype_ok(dtype)) return 0;
+  return point_sample_bwd_workspace(dtype, N, C, H, W, P, coords_batch);
 }
 
 int ml_point_sample_backward(int dtype, const void* grad_out, const float* coords, int64_t N,
@@ -633,7 +634,7 @@ int ml_point_sample_backward(int dtype, const void* grad_out, const float* coord
   if (N < 0 || C < 0 || H <= 0 || W <= 0 || P < 0 || coords_batch <= 0)
     return fail(ML_EINVAL, "point_sample backward: invalid shape");
   if (!dtype_ok(dtype)) return fail(ML_EINVAL, "unsupported dtype");
-  if (workspace_bytes < point_sample_bwd_workspace(dtype, N, C, H, W))
+  if (workspace_bytes < point_sample_bwd_workspace(dtype, N, C, H, W, P, coords_batch))
     return fail(ML_EWORKSPACE, "workspace too small");
   return launch_point_sample_backward(dtype, grad_out, coords, N, C, H, W, P, coords_batch,
                                       align_corners, grad_input, workspace, (hipStream_t)stream);

@@ -407,7 +407,8 @@ int launch_prep_points(const PrepArgs& a, const Dims& d, int64_t Hs, int64_t Ws,
 int launch_point_sample(int dtype, const void* in, const float* coords, int64_t N, int64_t C,
                         int64_t H, int64_t W, int64_t P, int64_t cb, int align, void* out,
                         hipStream_t st);
-size_t point_sample_bwd_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W);
+size_t point_sample_bwd_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t P,
+                                  int64_t cb);
 int launch_point_sample_backward(int dtype, const void* gout, const float* coords, int64_t N,
                                  int64_t C, int64_t H, int64_t W, int64_t P, int64_t cb, int align,
                                  void* gin, float* acc, hipStream_t st);

@@ -19,6 +19,8 @@
 // LDS); larger planes gather their corners straight from memory
 // (point_sample_kernel).  The samples are written along the point index.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "ml_internal.h"
@@ -242,24 +244,39 @@ int launch_point_sample(int dtype, const void* in, const float* coords, int64_t 
 // ---- gradient with respect to the sampled planes --------------------------------
 // grid_sample's input gradient: every sample's gradient is added to its four
 // corner cells with its bilinear weights (corners outside the plane take
-// nothing).  The additions are float atomics (LDS or global), so the last
-// bits depend on their order, as with the reference's CUDA grid_sample
-// backward, which also adds with atomics.  The atomics bound both forms: on
-// 800 planes of 128 x 128 with 12,544 points and 20% of the rows nonzero, the
-// LDS form takes 146 us against 38 us with plain (racy) adds, and global
-// float atomics into a float buffer take 1.9 ms; samples with a zero
-// gradient are skipped in both.  A deterministic form (the corner entries
-// sorted by cell once per image with a radix sort, then a fixed-order sum per
-// cell) measured 148 us with all-zero gradients and 200 us at 20% nonzero
-// rows: the sort's 18 launches alone take about 110 us.
+// nothing).  Three forms:
+// * grouped ((H + 1)(W + 1) <= 16,900, as for 128 x 128 planes, W <= 1151,
+//   up to 16,384 points, at least kCsrMinPlanes planes per coordinate set): the
+//   points of each coordinate set are sorted into buckets by their base cell
+//   once (corner_csr_kernel: a count per bucket in LDS, a scan, a scatter),
+//   then each plane's workgroup stages its point gradients in LDS and sums
+//   every cell's contributions with no atomics (point_sample_bwd_csr_kernel).
+//   The points of one bucket are summed in the order the scatter placed
+//   them, which can change between runs, as the order of the reference's
+//   CUDA atomics does.
+// * LDS float atomics per plane (point_sample_bwd_lds_kernel) for planes of
+//   up to 64 KB of accumulators otherwise.
+// * global float atomics into a float workspace and a conversion pass for
+//   larger planes.
+// On 800 planes of 128 x 128 with 12,544 points and 20% of the rows nonzero
+// (configuration 2), the grouped form takes 102 us (bucket sort 34 us, gather
+// 68 us) against 146 us for the LDS atomics (38 us with plain, racy adds:
+// the atomics bind it); global float atomics take 1.9 ms, and a radix sort
+// of the corner entries (18 launches) took 110 us alone.  Samples with a
+// zero gradient add nothing in the atomic forms; a plane whose gradient row
+// is all zero is written as zeros at once in the grouped form.
+// I: the index type (int64_t, or int where H * W and its bucket grid fit).
+template <typename I = int64_t>
 struct Corners {
-  int64_t i[4];
+  I i[4];
   float w[4];
   bool k[4];
+  I x0, y0;  // the nw corner, in [-1, W - 1] x [-1, H - 1] when some k[q] holds
 };
 
-__device__ __forceinline__ Corners corners_of(const float* cp, int64_t H, int64_t W, bool al) {
-  Corners c;
+template <typename I = int64_t>
+__device__ __forceinline__ Corners<I> corners_of(const float* cp, I H, I W, bool al) {
+  Corners<I> c;
   const float gx = __fadd_rn(__fmul_rn(2.f, cp[0]), -1.f);
   const float gy = __fadd_rn(__fmul_rn(2.f, cp[1]), -1.f);
   const float ix = unnormalize(gx, W, al);
@@ -269,7 +286,7 @@ __device__ __forceinline__ Corners corners_of(const float* cp, int64_t H, int64_
   const bool yin = y0f >= -1.f && y0f <= (float)(H - 1);
   if (!xin) x0f = -2.f;
   if (!yin) y0f = -2.f;
-  const int64_t x0 = (int64_t)x0f, y0 = (int64_t)y0f;
+  const I x0 = (I)x0f, y0 = (I)y0f;
   const float x1f = x0f + 1.f, y1f = y0f + 1.f;
   c.w[0] = (x1f - ix) * (y1f - iy);  // nw
   c.w[1] = (ix - x0f) * (y1f - iy);  // ne
@@ -281,6 +298,8 @@ __device__ __forceinline__ Corners corners_of(const float* cp, int64_t H, int64_
   c.k[1] = ok_x1 && ok_y0;
   c.k[2] = ok_x0 && ok_y1;
   c.k[3] = ok_x1 && ok_y1;
+  c.x0 = x0;
+  c.y0 = y0;
   c.i[0] = y0 * W + x0;
   c.i[1] = c.i[0] + 1;
   c.i[2] = c.i[0] + W;
@@ -322,7 +341,7 @@ __global__ __launch_bounds__(kPsBwdThreads) void point_sample_bwd_lds_kernel(
     for (int u = 0; u < kPsBwdBatch; ++u) {
       if (g[u] != 0.f) {
         const float c2[2] = {cp[u].x, cp[u].y};
-        const Corners c = corners_of(c2, H, W, al);
+        const Corners<> c = corners_of(c2, H, W, al);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (c.k[q]) atomicAdd(&accs[c.i[q]], c.w[q] * g[u]);
@@ -331,6 +350,277 @@ __global__ __launch_bounds__(kPsBwdThreads) void point_sample_bwd_lds_kernel(
   }
   __syncthreads();
   for (int64_t i = threadIdx.x; i < HW; i += kPsBwdThreads) st_val<DT>(gin, plane * HW + i, accs[i]);
+}
+
+// Grouped form.  A point whose bilinear footprint touches the plane has a
+// base cell (y0, x0) = (floor(iy), floor(ix)) in [-1, H - 1] x [-1, W - 1]:
+// bucket (y0 + 1) (W + 1) + (x0 + 1) of NB = (H + 1)(W + 1).  corner_csr_kernel
+// sorts each coordinate set's points into their buckets (a count per bucket in
+// LDS, a scan, a scatter); record k of set n (buckets in order, bucket b at
+// [off[b], off[b + 1])) is point pt[k] with its four corner weights wt[k] =
+// (nw, ne, sw, se).  Cell (y, x) is the nw corner of bucket (y, x), the ne
+// corner of bucket (y, x - 1), the sw corner of (y - 1, x) and the se corner
+// of (y - 1, x - 1): two runs of adjacent buckets, so a cell reads two
+// contiguous record ranges.  A corner outside the plane belongs to no cell,
+// so its weight is never read.
+constexpr int kCsrThreads = 1024;
+constexpr int64_t kCsrMaxBuckets = 16900;  // per-bucket counters in LDS (66 KB): 129 x 129 cells
+constexpr int64_t kCsrMaxPoints = 16384;   // a plane's point gradients in LDS (64 KB)
+constexpr int64_t kCsrMinPlanes = 8;       // planes per coordinate set that repay the grouping
+constexpr int kCsrPointsPerThread = (int)(kCsrMaxPoints / kCsrThreads);
+
+constexpr int kBandBuckets = 2304;  // bucket offsets staged per band of the gather at most
+static bool csr_form(int64_t C, int64_t H, int64_t W, int64_t P) {
+  return (H + 1) * (W + 1) <= kCsrMaxBuckets && 2 * (W + 1) <= kBandBuckets && P <= kCsrMaxPoints &&
+         C >= kCsrMinPlanes;
+}
+struct CsrLayout {
+  size_t off, pt, wt, total;  // [cb][NB + 1] u32, [cb][P] u32, [cb][P] float4
+};
+static CsrLayout csr_layout(int64_t H, int64_t W, int64_t P, int64_t cb) {
+  CsrLayout l;
+  l.off = 0;
+  l.pt = align256((size_t)cb * ((H + 1) * (W + 1) + 1) * 4);
+  l.wt = l.pt + align256((size_t)cb * P * 4);
+  l.total = l.wt + (size_t)cb * P * 16;
+  return l;
+}
+
+// One workgroup per coordinate set.
+__global__ __launch_bounds__(kCsrThreads) void corner_csr_kernel(const float* coords, int H, int W, int P,
+                                                                 int align, uint32_t* off_all,
+                                                                 uint32_t* pt_all, float4* wt_all) {
+  __shared__ uint32_t cnt[kCsrMaxBuckets];
+  __shared__ uint32_t wsum[kCsrThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t set = blockIdx.x;
+  const int NB = (H + 1) * (W + 1);
+  const float* cs = coords + set * P * 2;
+  uint32_t* off = off_all + set * (NB + 1);
+  uint32_t* pt = pt_all + set * P;
+  float4* wt = wt_all + set * P;
+  const bool al = align != 0;
+  // the set's points, kCsrPointsPerThread per thread, all loads issued at once
+  // (and again for the scatter, from the cache, rather than held across the scan)
+  float2 xy[kCsrPointsPerThread];
+  auto load_points = [&]() {
+#pragma unroll
+    for (int u = 0; u < kCsrPointsPerThread; ++u) {
+      const int p = u * kCsrThreads + tid;
+      xy[u] = p < P ? *(const float2*)(cs + 2 * p) : make_float2(0.f, 0.f);
+    }
+  };
+  load_points();
+  for (int i = tid; i < NB; i += kCsrThreads) cnt[i] = 0u;
+  __syncthreads();
+  int bk[kCsrPointsPerThread];  // the point's bucket, -1 when no corner is in the plane
+#pragma unroll
+  for (int u = 0; u < kCsrPointsPerThread; ++u) {
+    const int p = u * kCsrThreads + tid;
+    const float c2[2] = {xy[u].x, xy[u].y};
+    const Corners<int> c = corners_of<int>(c2, H, W, al);
+    const bool any = c.k[0] | c.k[1] | c.k[2] | c.k[3];
+    bk[u] = p < P && any ? (c.y0 + 1) * (W + 1) + (c.x0 + 1) : -1;
+    if (bk[u] >= 0) atomicAdd(&cnt[bk[u]], 1u);
+  }
+  __syncthreads();
+  // thread t scans the run of R consecutive buckets starting at t R
+  const int R = (NB + kCsrThreads - 1) / kCsrThreads, b0 = tid * R;
+  uint32_t run = 0;
+  for (int k = 0; k < R; ++k)
+    if (b0 + k < NB) run += cnt[b0 + k];
+  uint32_t incl = run;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  uint32_t pos = incl - run, total = 0;
+  for (int w = 0; w < kCsrThreads / 64; ++w) {
+    pos += w < wave ? wsum[w] : 0u;
+    total += wsum[w];
+  }
+  for (int k = 0; k < R; ++k)
+    if (b0 + k < NB) {
+      const uint32_t n = cnt[b0 + k];
+      off[b0 + k] = pos;
+      cnt[b0 + k] = pos;  // the bucket's next free record
+      pos += n;
+    }
+  if (tid == 0) off[NB] = total;
+  load_points();
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kCsrPointsPerThread; ++u) {
+    if (bk[u] < 0) continue;
+    const int p = u * kCsrThreads + tid;
+    const float c2[2] = {xy[u].x, xy[u].y};
+    const Corners<int> c = corners_of<int>(c2, H, W, al);
+    const uint32_t at = atomicAdd(&cnt[bk[u]], 1u);
+    pt[at] = (uint32_t)p;
+    wt[at] = make_float4(c.w[0], c.w[1], c.w[2], c.w[3]);
+  }
+}
+
+// One workgroup per plane: its point gradients into LDS (a gradient row that
+// is all zero writes a zero plane at once), then bands of RB cell rows.  The
+// buckets a band reads (rows y0 - 1 .. y0 + RB - 1) are consecutive, and so
+// are their records: the band's offsets and records are staged in LDS, and
+// each thread sums its cells' two record ranges there (a band with more than
+// kBandRecords records reads them from memory).  The next band's offsets
+// and records are loaded into registers while the current band is summed.
+// Every cell of the plane is written.  Indices are 32-bit: at most 16,900
+// buckets, 16,384 points and as many records per coordinate set.
+constexpr int kBandRecords = 3072;  // 60 KB of staged records
+constexpr int kBandCells = 2048;    // cells per band (at least one row)
+constexpr int kBandU = kBandRecords / kCsrThreads;             // records per thread
+constexpr int kBandOffU = (kBandBuckets + kCsrThreads) / kCsrThreads;  // offsets per thread
+template <int DT>
+__global__ __launch_bounds__(kCsrThreads) void point_sample_bwd_csr_kernel(
+    const void* gout, int C, int H, int W, int P, int cb, int RB, const uint32_t* off_all,
+    const uint32_t* pt_all, const float4* wt_all, void* gin) {
+  extern __shared__ __align__(16) unsigned char sm[];
+  float4* rw = (float4*)sm;                       // [kBandRecords] weights
+  uint32_t* rp = (uint32_t*)(rw + kBandRecords);  // [kBandRecords] points
+  uint32_t* bo = rp + kBandRecords;               // [kBandBuckets + 1] offsets
+  float* g = (float*)(bo + kBandBuckets + 4);     // [P]
+  const int tid = threadIdx.x;
+  const int W1 = W + 1, HW = H * W;
+  const int64_t plane = blockIdx.x, obase = plane * HW;
+  const int set = (int)((plane / C) % cb);
+  int nz = 0;
+  {
+    float v[kCsrPointsPerThread];  // all loads issued at once
+#pragma unroll
+    for (int u = 0; u < kCsrPointsPerThread; ++u) {
+      const int p = u * kCsrThreads + tid;
+      v[u] = p < P ? ld_val<DT>(gout, plane * P + p) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kCsrPointsPerThread; ++u) {
+      const int p = u * kCsrThreads + tid;
+      if (p < P) g[p] = v[u];
+      nz |= v[u] != 0.f;
+    }
+  }
+  if (!__syncthreads_or(nz)) {
+    for (int i = tid; i < HW; i += kCsrThreads) st_val<DT>(gin, obase + i, 0.f);
+    return;
+  }
+  const uint32_t* off = off_all + (int64_t)set * ((H + 1) * W1 + 1);
+  const uint32_t* pt = pt_all + (int64_t)set * P;
+  const float4* wt = wt_all + (int64_t)set * P;
+  // band y0 reads buckets [y0 W1, (y0 + rows + 1) W1): nbk + 1 offsets from y0 W1
+  auto nbk_of = [&](int y0) { return (min(RB, H - y0) + 1) * W1; };
+  // Registers that carry the next band (kBandOffU = kBandU = 3 per thread,
+  // named rather than arrays, so that they stay in registers across the sum):
+  // its offsets and records, loaded with unconditional loads at clamped
+  // indices (the set's arrays hold (H + 1) W1 + 1 offsets and P records).
+  static_assert(kBandOffU == 3 && kBandU == 3, "three carried slots per thread");
+  uint32_t no0, no1, no2, nq0, nq1, nq2;
+  float4 nw0, nw1, nw2;
+  const uint32_t last = (uint32_t)P - 1u;
+  auto fetch = [&](int y0) {
+    const int nbk = nbk_of(y0);
+    const uint32_t* o = off + y0 * W1;
+    const uint32_t r0 = o[0];  // wave-uniform
+    no0 = o[min(tid, nbk)];
+    no1 = o[min(kCsrThreads + tid, nbk)];
+    no2 = o[min(2 * kCsrThreads + tid, nbk)];
+    const uint32_t k0 = min(r0 + (uint32_t)tid, last), k1 = min(r0 + (uint32_t)(kCsrThreads + tid), last),
+                   k2 = min(r0 + (uint32_t)(2 * kCsrThreads + tid), last);
+    nq0 = pt[k0];
+    nq1 = pt[k1];
+    nq2 = pt[k2];
+    nw0 = wt[k0];
+    nw1 = wt[k1];
+    nw2 = wt[k2];
+  };
+  // every slot of the staging room is written (past the band's records and
+  // offsets with entries that no cell reads)
+  auto stage = [&]() {
+    bo[tid] = no0;
+    bo[kCsrThreads + tid] = no1;
+    if (2 * kCsrThreads + tid <= kBandBuckets) bo[2 * kCsrThreads + tid] = no2;
+    rp[tid] = nq0;
+    rp[kCsrThreads + tid] = nq1;
+    rp[2 * kCsrThreads + tid] = nq2;
+    rw[tid] = nw0;
+    rw[kCsrThreads + tid] = nw1;
+    rw[2 * kCsrThreads + tid] = nw2;
+  };
+  fetch(0);
+  stage();
+  __syncthreads();
+  for (int y0 = 0; y0 < H; y0 += RB) {
+    const int rows = min(RB, H - y0), nbk = nbk_of(y0);
+    const uint32_t r0 = bo[0], nr = bo[nbk] - r0;
+    const bool staged = nr <= (uint32_t)kBandRecords;
+    if (y0 + RB < H) fetch(y0 + RB);  // lands while this band is summed
+    const int ncell = rows * W;
+    for (int k = tid; k < ncell; k += kCsrThreads) {
+      const int yl = k / W, x = k - yl * W;
+      // local bucket (y, x) of the band: (yl + 1) W1 + (x + 1)
+      const int bn = (yl + 1) * W1 + (x + 1), bs = bn - W1;
+      float acc = 0.f;
+      if (staged) {
+        // buckets (y, x - 1), (y, x): this cell is their ne and nw corner
+        for (uint32_t j = bo[bn - 1] - r0, m = bo[bn] - r0, e = bo[bn + 1] - r0; j < e; ++j)
+          acc += (j < m ? rw[j].y : rw[j].x) * g[rp[j]];
+        // buckets (y - 1, x - 1), (y - 1, x): its se and sw corner
+        for (uint32_t j = bo[bs - 1] - r0, m = bo[bs] - r0, e = bo[bs + 1] - r0; j < e; ++j)
+          acc += (j < m ? rw[j].w : rw[j].z) * g[rp[j]];
+      } else {
+        for (uint32_t j = bo[bn - 1], m = bo[bn], e = bo[bn + 1]; j < e; ++j)
+          acc += (j < m ? wt[j].y : wt[j].x) * g[pt[j]];
+        for (uint32_t j = bo[bs - 1], m = bo[bs], e = bo[bs + 1]; j < e; ++j)
+          acc += (j < m ? wt[j].w : wt[j].z) * g[pt[j]];
+      }
+      st_val<DT>(gin, obase + (int64_t)y0 * W + k, acc);
+    }
+    if (y0 + RB < H) {
+      __syncthreads();  // every thread is done with this band's LDS
+      stage();
+      __syncthreads();
+    }
+  }
+}
+// Rows per band: at most kBandCells cells and kBandBuckets offsets, and the
+// expected records (P / NB per bucket) within half the staging room.
+static int csr_band_rows(int64_t H, int64_t W, int64_t P) {
+  const double per_bucket = (double)P / (double)((H + 1) * (W + 1));
+  int64_t rb = std::min<int64_t>(kBandCells / W, kBandBuckets / (W + 1) - 1);
+  const int64_t by_records = (int64_t)(0.5 * kBandRecords / (per_bucket * (W + 1) + 1e-9)) - 1;
+  rb = std::min(rb, by_records);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(rb, H));
+}
+static size_t csr_gather_lds(int64_t P) {
+  return (size_t)kBandRecords * 20 + (size_t)(kBandBuckets + 4) * 4 + (size_t)P * 4;
+}
+// The gather's dynamic LDS limit raised to its largest size, once per device
+// (the attribute is set with that device current); the lock makes the first
+// call of several host threads safe.
+template <int DT>
+static int csr_raise_lds() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> done[kMaxDev];
+  static std::mutex mu;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
+    return fail(ML_ELAUNCH, "point_sample backward: no current device (or more than 64)");
+  if (!done[dev].load(std::memory_order_acquire)) {
+    std::lock_guard<std::mutex> g(mu);
+    if (!done[dev].load(std::memory_order_relaxed)) {
+      const size_t most = csr_gather_lds(kCsrMaxPoints);
+      if (hipFuncSetAttribute((const void*)point_sample_bwd_csr_kernel<DT>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)most) != hipSuccess)
+        return fail(ML_ELAUNCH, "point_sample backward: cannot raise the LDS limit");
+      done[dev].store(1, std::memory_order_release);
+    }
+  }
+  return ML_OK;
 }
 
 // Planes too large for LDS: float atomics into a zeroed float buffer, then a
@@ -342,7 +632,7 @@ __global__ __launch_bounds__(kPsThreads) void point_sample_bwd_global_kernel(
   const int64_t p = (int64_t)blockIdx.x * kPsThreads + threadIdx.x;
   const int64_t n = blockIdx.y;
   if (p >= P) return;
-  const Corners c = corners_of(coords + ((n % cb) * P + p) * 2, H, W, align != 0);
+  const Corners<> c = corners_of(coords + ((n % cb) * P + p) * 2, H, W, align != 0);
   const int64_t c0 = (int64_t)blockIdx.z * kPsChan;
   const int64_t c1 = min(C, c0 + kPsChan);
   for (int64_t ch = c0; ch < c1; ++ch) {
@@ -362,8 +652,10 @@ __global__ __launch_bounds__(256) void f32_to_dtype_kernel(const float* src, voi
     st_val<DT>(dst, i, src[i]);
 }
 
-size_t point_sample_bwd_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W) {
+size_t point_sample_bwd_workspace(int dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t P,
+                                  int64_t cb) {
   (void)dtype;
+  if (csr_form(C, H, W, P)) return csr_layout(H, W, P, cb).total;
   if ((size_t)H * W * 4 <= kPsBwdLdsBytes) return 0;
   return (size_t)N * C * H * W * 4;
 }
@@ -373,6 +665,26 @@ static int launch_bwd_dt(const void* gout, const float* coords, int64_t N, int64
                          int64_t W, int64_t P, int64_t cb, int align, void* gin, float* acc,
                          hipStream_t st) {
   const int64_t planes = N * C;
+  if (csr_form(C, H, W, P)) {
+    if (!acc) return fail(ML_EWORKSPACE, "point_sample backward: a workspace is required");
+    if (planes > INT32_MAX || cb > INT32_MAX) return fail(ML_EINVAL, "point_sample backward: too many planes");
+    const CsrLayout l = csr_layout(H, W, P, cb);
+    unsigned char* w = (unsigned char*)acc;
+    uint32_t* off = (uint32_t*)(w + l.off);
+    uint32_t* pt = (uint32_t*)(w + l.pt);
+    float4* wt = (float4*)(w + l.wt);
+    const int64_t sets = std::min(cb, N);  // coordinate sets that some plane reads
+    hipLaunchKernelGGL(corner_csr_kernel, dim3((unsigned)sets), dim3(kCsrThreads), 0, st, coords, (int)H,
+                       (int)W, (int)P, align, off, pt, wt);
+    int rc = check_launch("point_sample_backward");
+    if (rc) return rc;
+    if ((rc = csr_raise_lds<DT>())) return rc;
+    hipLaunchKernelGGL(point_sample_bwd_csr_kernel<DT>, dim3((unsigned)planes), dim3(kCsrThreads),
+                       csr_gather_lds(P), st, gout, (int)C, (int)H, (int)W, (int)P, (int)cb,
+                       csr_band_rows(H, W, P), (const uint32_t*)off, (const uint32_t*)pt,
+                       (const float4*)wt, gin);
+    return check_launch("point_sample_backward");
+  }
   if ((size_t)H * W * 4 <= kPsBwdLdsBytes) {
     if (planes > INT32_MAX) return fail(ML_EINVAL, "point_sample backward: too many planes");
     hipLaunchKernelGGL(point_sample_bwd_lds_kernel<DT>, dim3((unsigned)planes), dim3(kPsBwdThreads),

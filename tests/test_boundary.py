@@ -154,10 +154,18 @@ def test_point_sampling_queries_and_host_tensors_rejected():
     assert q(ctypes.byref(good), ctypes.byref(p), 0, 0, 512) == 0
     b = lib.ml_point_sample_backward_workspace_size
     b.restype = ctypes.c_size_t
-    b.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]
-    assert b(0, 8, 100, 128, 128) == 0                 # float accumulators fit LDS
-    assert b(0, 2, 3, 130, 140) == 2 * 3 * 130 * 140 * 4  # float workspace
-    assert b(7, 2, 3, 130, 140) == 0                   # unknown dtype
+    b.argtypes = [ctypes.c_int] + [ctypes.c_int64] * 6
+    # grouped form ((H+1)(W+1) <= 16,900 buckets, <= 16,384 points, >= 8
+    # planes per coordinate set): per set, the bucket offsets, then P point
+    # indices and P float4 corner weights (each region 256-byte aligned)
+    a256 = lambda x: (x + 255) // 256 * 256
+    assert b(0, 8, 100, 128, 128, 12544, 8) == (a256(8 * (129 * 129 + 1) * 4) + a256(8 * 12544 * 4)
+                                                + 8 * 12544 * 16)
+    assert b(0, 2, 3, 16, 16, 100, 2) == 0                     # < 8 planes: LDS atomics
+    assert b(0, 2, 8, 128, 128, 17000, 2) == 0                 # > 16,384 points: LDS atomics
+    assert b(0, 2, 3, 130, 140, 100, 2) == 2 * 3 * 130 * 140 * 4  # float workspace
+    assert b(7, 2, 3, 130, 140, 100, 2) == 0                   # unknown dtype
+    assert b(0, 2, 3, 130, 140, 100, 0) == 0                   # no coordinate set
     import mask_loss_amd
     ml = mask_loss_amd.mask_loss
     x = torch.zeros(2, 3, 4, 4)

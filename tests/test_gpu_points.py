@@ -222,18 +222,26 @@ def test_validation(ml):
 
 
 @pytest.mark.parametrize("dt", ["float32", "bfloat16", "float16"])
-@pytest.mark.parametrize("H,W,P", [(9, 13, 777), (130, 140, 777), (9, 13, 17000), (130, 140, 17000)])
-def test_point_sample_backward(ml, dt, H, W, P):
-    # float atomics in LDS for the (9, 13) plane and into a float workspace
-    # for the 72.8 KB (130, 140) plane; P = 17000 gives up to a few hundred
-    # samples per cell of the small plane
-    rng = np.random.default_rng(31 + H + P)
+@pytest.mark.parametrize("H,W,P,C", [
+    (9, 13, 777, 5), (130, 140, 777, 5), (9, 13, 17000, 5), (130, 140, 17000, 5),
+    (9, 13, 777, 9), (37, 29, 1025, 8), (128, 128, 12544, 8), (9, 13, 16384, 8), (130, 140, 777, 9)])
+def test_point_sample_backward(ml, dt, H, W, P, C):
+    # C = 5 planes per coordinate set: float atomics in LDS for the (9, 13)
+    # plane and into a float workspace for the 72.8 KB (130, 140) plane;
+    # P = 17000 gives up to a few hundred samples per cell of the small plane.
+    # C >= 8 with at most 16,384 cells and points: the corner entries grouped
+    # by cell and gathered per plane (128 x 128 at configuration 2's 12,544
+    # points: eight rounds of 2048 cells, each with its ~6,300 entries staged
+    # in LDS; (9, 13) with 16,384 points: one round of ~65,000 entries, too
+    # many to stage, read from memory); (130, 140) stays on the float
+    # workspace.
+    rng = np.random.default_rng(31 + H + P + C)
     c = coords_with_edges(rng, 3, P)
-    g64, g = as_dtype(rng.normal(0, 1, size=(3, 5, P)), dt)
+    g64, g = as_dtype(rng.normal(0, 1, size=(3, C, P)), dt)
     g64[1, 2] = 0.0  # an all-zero row (an unmatched query)
     g[1, 2] = 0
     got = ml.point_sample_backward(g, torch.from_numpy(c).cuda(), H, W, False)
-    assert got.dtype == TDT[dt] and got.shape == (3, 5, H, W)
+    assert got.dtype == TDT[dt] and got.shape == (3, C, H, W)
     ref = PO.point_sample_backward(g64, c, H, W, False)
     assert (got[1, 2] == 0).all()
     # float32 sums in another order: a few ulps of the cell's largest partial sum

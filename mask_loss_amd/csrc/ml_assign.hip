@@ -543,7 +543,9 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
   if (M == 0 || n == 0 || n < M) return true;
   const double kQNaN = __longlong_as_double(0x7FF8000000000000ll);
   double v[NJ], ucol[NJ];
-  int pj[NJ], rcol[NJ], predj[NJ];
+  // pr: the column's matched row p (0 = free) in the low 16 bits and that
+  // row's cost-matrix row in the high 16 (rows <= 1024, columns <= 256)
+  int pr[NJ], predj[NJ];
   bool valid[NJ];
 #pragma unroll
   for (int t = 0; t < NJ; ++t) {
@@ -551,8 +553,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     valid[t] = j <= n;
     v[t] = 0.0;
     ucol[t] = 0.0;
-    pj[t] = 0;
-    rcol[t] = 0;
+    pr[t] = 0;
     predj[t] = valid[t] ? preds[j - 1] : 0;
   }
   bool ok = true;
@@ -593,11 +594,24 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         break;
       }
       // key = j1 - 1 of the entering column: the lowest (slot, lane) whose
-      // minv equals delta (an empty slot gives all ones)
-      uint32_t key = 0xFFFFFFFFu;
+      // minv equals delta.  ls: this lane's lowest such slot (NJ if none).
+      // When one lane holds delta, that lane and its slot; otherwise (equal
+      // minima in several lanes) the lowest slot's lowest lane, from one
+      // ballot per slot (an empty slot gives all ones).
+      int ls = NJ;
 #pragma unroll
-      for (int t = 0; t < NJ; ++t)
-        key = min(key, first_lane(__builtin_amdgcn_ballot_w64(minv[t] == delta)) | (uint32_t)(64 * t));
+      for (int t = NJ - 1; t >= 0; --t) ls = minv[t] == delta ? t : ls;
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(ls < NJ);
+      uint32_t key;
+      if (__builtin_popcountll(hit) == 1) {
+        const int l = __builtin_ctzll(hit);
+        key = (uint32_t)(64 * __builtin_amdgcn_readlane(ls, l) + l);
+      } else {
+        key = 0xFFFFFFFFu;
+#pragma unroll
+        for (int t = 0; t < NJ; ++t)
+          key = min(key, first_lane(__builtin_amdgcn_ballot_w64(minv[t] == delta)) | (uint32_t)(64 * t));
+      }
       // potentials: columns in the tree (and column 0 = row i) move by delta
       // (f = 1), the others' minv by -delta; then column j1 enters the tree
 #pragma unroll
@@ -612,11 +626,12 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       j0 = (int)key + 1;
       const int ol = (int)(key & 63u), ot = (int)(key >> 6);
       const SlotMask<NJ> sm(ot);
-      if (sel_i<NJ>(pj, sm, ol) == 0) break;  // j1 is free: augment
+      const int pr1 = sel_i<NJ>(pr, sm, ol);
+      if ((pr1 & 0xFFFF) == 0) break;  // j1 is free: augment
       // next row of the tree: the one matched to column j1 (its potential
       // took no delta above: j1 was outside the tree)
       ui0 = sel_d<NJ>(ucol, sm, ol);
-      read_cost_row<NJ, CM>(cost, sel_i<NJ>(rcol, sm, ol), predj, rawf);
+      read_cost_row<NJ, CM>(cost, pr1 >> 16, predj, rawf);
     }
     if (!ok) break;
     // augment along way[] from the free column j0 back to column 0: each
@@ -626,26 +641,23 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       const int ol = (j0 - 1) & 63, ot = (j0 - 1) >> 6;
       const SlotMask<NJ> sm(ot);
       const int jp = sel_i<NJ>(wy, sm, ol);
-      int np, nr;
+      int npr;
       double nu;
       if (jp == 0) {
-        np = i;
+        npr = i | (colcur << 16);
         nu = ucur;
-        nr = colcur;
       } else {
         const int pl = (jp - 1) & 63, pt = (jp - 1) >> 6;
         const SlotMask<NJ> pm(pt);
-        np = sel_i<NJ>(pj, pm, pl);
+        npr = sel_i<NJ>(pr, pm, pl);
         nu = sel_d<NJ>(ucol, pm, pl);
-        nr = sel_i<NJ>(rcol, pm, pl);
       }
       const bool me = lane == ol;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
         const bool mine = me & sm.is[t];
-        pj[t] = mine ? np : pj[t];
+        pr[t] = mine ? npr : pr[t];
         ucol[t] = mine ? nu : ucol[t];
-        rcol[t] = mine ? nr : rcol[t];
       }
       j0 = jp;
     }
@@ -653,7 +665,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
   if (ok) {
 #pragma unroll
     for (int t = 0; t < NJ; ++t)
-      if (valid[t] && pj[t] > 0) asg[lane + 64 * t] = pj[t] - 1;
+      if (valid[t] && (pr[t] & 0xFFFF) > 0) asg[lane + 64 * t] = (pr[t] & 0xFFFF) - 1;
   }
   wave_sync();
   return ok;

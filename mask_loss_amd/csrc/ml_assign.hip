@@ -108,8 +108,11 @@ __device__ __forceinline__ bool cost_ok(double c, double thr) { return isfinite(
 // count, schedule entries of every class, class logits, the output columns'
 // slots and targets), then the K-split partials together with the class
 // logits of the targets, then the stores.
-constexpr int kFinCls = 3;      // class logits held per lane (C <= 192)
-constexpr int kFinCols = 2;     // output columns held per lane (GT_out <= 128)
+// Register forms of finalize: (class logits, output columns) held per lane
+constexpr int kFinCls = 3;       // C <= 192
+constexpr int kFinCols = 2;      // GT_out <= 128
+constexpr int kFinColsWide = 4;  // GT_out <= 256, class logits streamed (NC = 0)
+constexpr int kFinClsBatch = 8;  // streamed class logits loaded per lane and batch
 constexpr int kFinSplits = 12;  // K-splits loaded per lane and batch
 
 // Sum the K-split partials k0, k0 + step, ... of slot s in split order.  The
@@ -144,10 +147,12 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
 
 // Latency-bound: at least four waves per SIMD (at most 128 registers).
 // CDT: dtype of the class logits.  FAST (chosen on the host): class logits
-// present, 1 <= C <= 192 and 1 <= GT_out <= 128, so the row's class logits and
-// the output columns' slots and targets fit in registers and every load of
-// the first two round trips is unconditional (indices clamped into range).
-template <int CDT, bool FAST>
+// present and 1 <= GT_out <= 64 NG, so the output columns' slots and targets
+// fit in registers and every load of the first two round trips is
+// unconditional (indices clamped into range); with NC > 0 (C <= 64 NC) the
+// row's class logits are held in registers too, else they are streamed in
+// batches of kFinClsBatch loads per lane.
+template <int CDT, bool FAST, int NC = kFinCls, int NG = kFinCols>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void finalize_kernel(AssignArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's finish count
     if (a.done) *a.done = 0;
@@ -166,6 +171,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   const int64_t row = row32, lb = lb32, q = row32 - lb32 * (uint32_t)a.Q, b = lb32 % (uint32_t)a.B;
   const int64_t GTo = a.GT_out, C = a.C;
   const bool labels = FAST || a.cls_logits != nullptr;
+  constexpr bool kClsRegs = FAST && NC > 0;
   const int64_t zb = row * C;
   const int64_t void_idx = a.void_idx;
   const bool has_void = void_idx >= 0;
@@ -183,16 +189,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
     ksc[c] = a.sched[kClasses + c];
     nc[c] = a.sched[c];
   }
-  float zc[kFinCls] = {};
-  int oslot[kFinCols] = {};
-  int64_t oy[kFinCols] = {};
-  float zy[kFinCols] = {};
+  float zc[NC > 0 ? NC : 1] = {};
+  int oslot[NG] = {};
+  int64_t oy[NG] = {};
+  float zy[NG] = {};
   float zv = 0.f;
   if constexpr (FAST) {
+    if constexpr (kClsRegs) {
 #pragma unroll
-    for (int j = 0; j < kFinCls; ++j) zc[j] = cls_at<CDT>(a.cls_logits, zb + min((int64_t)lane + 64 * j, C - 1));
+      for (int j = 0; j < NC; ++j) zc[j] = cls_at<CDT>(a.cls_logits, zb + min((int64_t)lane + 64 * j, C - 1));
+    }
 #pragma unroll
-    for (int j = 0; j < kFinCols; ++j) {
+    for (int j = 0; j < NG; ++j) {
       const int64_t cc = min((int64_t)lane + 64 * j, GTo - 1);
       oslot[j] = a.slot_of_col[b * GTo + cc];
       oy[j] = a.cls_targets[b * a.GT_total + cc + (cc >= a.bg ? 1 : 0)];
@@ -216,7 +224,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   const RowPartials rp = row_partials_at(a.partials, a.plan, ci, tidx, KS, n_ci, qin, a.rows);
   if constexpr (FAST) {
 #pragma unroll
-    for (int j = 0; j < kFinCols; ++j) zy[j] = cls_at<CDT>(a.cls_logits, zb + min(max(oy[j], (int64_t)0), C - 1));
+    for (int j = 0; j < NG; ++j) zy[j] = cls_at<CDT>(a.cls_logits, zb + min(max(oy[j], (int64_t)0), C - 1));
   }
   const int nsl = G + 1;  // GT columns + the ones column
   if (nsl <= 32) {
@@ -246,12 +254,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   // the standalone pairwise BCE / dice operators)
   // f(c, z) over this lane's classes c = lane, lane + 64, ... in that order
   auto for_cls = [&](auto&& f) {
-    if constexpr (FAST) {
+    if constexpr (kClsRegs) {
 #pragma unroll
-      for (int j = 0; j < kFinCls; ++j)
+      for (int j = 0; j < NC; ++j)
         if (lane + 64 * j < C) f((int64_t)lane + 64 * j, zc[j]);
     } else {
-      for (int64_t c = lane; c < C; c += 64) f(c, cls_at<CDT>(a.cls_logits, zb + c));
+      for (int64_t c0 = lane; c0 < C; c0 += 64 * kFinClsBatch) {
+        float z[kFinClsBatch];  // the batch's loads in flight together
+#pragma unroll
+        for (int u = 0; u < kFinClsBatch; ++u) z[u] = cls_at<CDT>(a.cls_logits, zb + min(c0 + 64 * u, C - 1));
+#pragma unroll
+        for (int u = 0; u < kFinClsBatch; ++u)
+          if (c0 + 64 * u < C) f(c0 + 64 * u, z[u]);
+      }
     }
   };
   float rowv = 0.f, pen = 0.f;
@@ -336,7 +351,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void f
   };
   if constexpr (FAST) {
 #pragma unroll
-    for (int j = 0; j < kFinCols; ++j) {
+    for (int j = 0; j < NG; ++j) {
       const int64_t c = lane + 64 * j;
       if (c < GTo) emit(c, oslot[j], oy[j], zy[j]);
     }
@@ -1193,11 +1208,17 @@ int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const dim3 grid((unsigned)(ceil_div(rows, 4) + a.fin_fill.blocks));
   const bool fast = a.cls_logits && a.C >= 1 && a.C <= 64 * kFinCls && a.GT_out >= 1 &&
                     a.GT_out <= 64 * kFinCols;
+  const bool wide = !fast && a.cls_logits && a.C >= 1 && a.GT_out >= 1 && a.GT_out <= 64 * kFinColsWide;
   const int dt = a.cls_logits ? a.cls_dtype : ML_BF16;
   if (fast) {
     if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, true>), grid, dim3(256), 0, st, a);
     else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((finalize_kernel<ML_BF16, true>), grid, dim3(256), 0, st, a);
+  } else if (wide) {
+    constexpr int NC = 0, NG = kFinColsWide;
+    if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, true, NC, NG>), grid, dim3(256), 0, st, a);
+    else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, true, NC, NG>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((finalize_kernel<ML_BF16, true, NC, NG>), grid, dim3(256), 0, st, a);
   } else {
     if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, false>), grid, dim3(256), 0, st, a);
     else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, false>), grid, dim3(256), 0, st, a);

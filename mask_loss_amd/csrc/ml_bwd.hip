@@ -312,7 +312,24 @@ __device__ __forceinline__ void cls_out(void* p, int dt, int64_t i, float v) {
 }
 
 // Class-logit gradient of one (l,b,q) row, on one wave.
-constexpr int kClsRegs = 4;  // class rows of up to 256 logits are held in registers
+constexpr int kClsRegs = 4;   // class rows of up to 256 logits are held in registers
+constexpr int kClsBatch = 8;  // longer rows are streamed, kClsBatch loads per lane in flight
+
+// f(c, z) for this lane's classes c = c0, c0 + 64, ... of a row streamed in
+// batches (indices clamped into the row, so every load of a batch is issued
+// at once)
+template <typename F>
+__device__ __forceinline__ void for_cls_batched(const BwdArgs& a, int64_t base, int64_t C, F&& f) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t c0 = lane; c0 < C; c0 += 64 * kClsBatch) {
+    float z[kClsBatch];
+#pragma unroll
+    for (int u = 0; u < kClsBatch; ++u) z[u] = cls_in(a.cls_logits, a.cls_dtype, base + min(c0 + 64 * u, C - 1));
+#pragma unroll
+    for (int u = 0; u < kClsBatch; ++u)
+      if (c0 + 64 * u < C) f(c0 + 64 * u, z[u]);
+  }
+}
 
 __device__ void cls_row(const BwdArgs& a, int64_t row) {
   const int lane = threadIdx.x & 63;
@@ -364,17 +381,17 @@ __device__ void cls_row(const BwdArgs& a, int64_t row) {
         return;
       }
       float m = -INFINITY;
-      for (int64_t c = lane; c < C; c += 64) m = fmaxf(m, cls_in(a.cls_logits, a.cls_dtype, base + c));
+      for_cls_batched(a, base, C, [&](int64_t, float z) { m = fmaxf(m, z); });
       m = wave_max(m);
       float se = 0.f;
-      for (int64_t c = lane; c < C; c += 64) se += __expf(cls_in(a.cls_logits, a.cls_dtype, base + c) - m);
+      for_cls_batched(a, base, C, [&](int64_t, float z) { se += __expf(z - m); });
       se = wave_sum(se);
       const float inv = se > 0.f ? 1.f / se : 0.f;
-      for (int64_t c = lane; c < C; c += 64) {
-        float gv = __expf(cls_in(a.cls_logits, a.cls_dtype, base + c) - m) * inv;
+      for_cls_batched(a, base, C, [&](int64_t c, float z) {
+        float gv = __expf(z - m) * inv;
         if (c == tgt) gv -= 1.f;
         cls_out(a.grad_cls, a.cls_dtype, base + c, coeff * gv);
-      }
+      });
     } else {  // has_void only
       for (int64_t c = lane; c < C; c += 64) {
         float gv = 0.f;
@@ -390,8 +407,7 @@ __device__ void cls_row(const BwdArgs& a, int64_t row) {
   const ElemParams ep = a.cls_ep;
   const float g = a.cls_gamma;
   const float invC = C > 0 ? 1.f / (float)C : 0.f;
-  for (int64_t c = lane; c < C; c += 64) {
-    const float z = cls_in(a.cls_logits, a.cls_dtype, base + c);
+  for_cls_batched(a, base, C, [&](int64_t c, float z) {
     const Sig s = sig_terms(z);
     float mn, mp;
     focal_mods(s, ep, mn, mp);
@@ -407,7 +423,7 @@ __device__ void cls_row(const BwdArgs& a, int64_t row) {
       gv = is_void ? coeff * posg : 0.f;
     }
     cls_out(a.grad_cls, a.cls_dtype, base + c, gv);
-  }
+  });
 }
 
 // one wave per (l,b,q) row; 4 rows per workgroup

@@ -113,6 +113,7 @@ constexpr int kFinCls = 3;       // C <= 192
 constexpr int kFinCols = 2;      // GT_out <= 128
 constexpr int kFinColsWide = 4;  // GT_out <= 256, class logits streamed (NC = 0)
 constexpr int kFinClsBatch = 8;  // streamed class logits loaded per lane and batch
+constexpr int kFinClsWide = 20;  // C <= 1280 in registers with up to 64 kFinColsWide output columns
 constexpr int kFinSplits = 12;  // K-splits loaded per lane and batch
 
 // Sum the K-split partials k0, k0 + step, ... of slot s in split order.  The
@@ -153,7 +154,7 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
 // row's class logits are held in registers too, else they are streamed in
 // batches of kFinClsBatch loads per lane.
 template <int CDT, bool FAST, int NC = kFinCls, int NG = kFinCols>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void finalize_kernel(AssignArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC > 8 ? 3 : 4))) void finalize_kernel(AssignArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's finish count
     if (a.done) *a.done = 0;
   }
@@ -1209,8 +1210,14 @@ int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const bool fast = a.cls_logits && a.C >= 1 && a.C <= 64 * kFinCls && a.GT_out >= 1 &&
                     a.GT_out <= 64 * kFinCols;
   const bool wide = !fast && a.cls_logits && a.C >= 1 && a.GT_out >= 1 && a.GT_out <= 64 * kFinColsWide;
+  const bool wide_regs = wide && a.C <= 64 * kFinClsWide;
   const int dt = a.cls_logits ? a.cls_dtype : ML_BF16;
-  if (fast) {
+  if (wide_regs) {
+    constexpr int NC = kFinClsWide, NG = kFinColsWide;
+    if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, true, NC, NG>), grid, dim3(256), 0, st, a);
+    else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, true, NC, NG>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((finalize_kernel<ML_BF16, true, NC, NG>), grid, dim3(256), 0, st, a);
+  } else if (fast) {
     if (dt == ML_F32) hipLaunchKernelGGL((finalize_kernel<ML_F32, true>), grid, dim3(256), 0, st, a);
     else if (dt == ML_F16) hipLaunchKernelGGL((finalize_kernel<ML_F16, true>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((finalize_kernel<ML_BF16, true>), grid, dim3(256), 0, st, a);

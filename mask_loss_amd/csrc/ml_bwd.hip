@@ -295,13 +295,15 @@ __global__ __launch_bounds__(256) void bwd_mask_list_kernel(BwdArgs a, int64_t n
   }
 }
 
-__device__ __forceinline__ float cls_in(const void* p, int dt, int64_t i) {
+template <typename I>
+__device__ __forceinline__ float cls_in(const void* p, int dt, I i) {
   if (dt == ML_F32) return ((const float*)p)[i];
   const uint16_t h = ((const uint16_t*)p)[i];
   if (dt == ML_BF16) return __uint_as_float(((uint32_t)h) << 16);
   return (float)__builtin_bit_cast(_Float16, h);
 }
-__device__ __forceinline__ void cls_out(void* p, int dt, int64_t i, float v) {
+template <typename I>
+__device__ __forceinline__ void cls_out(void* p, int dt, I i, float v) {
   if (dt == ML_F32) {
     ((float*)p)[i] = v;
   } else if (dt == ML_BF16) {
@@ -331,6 +333,46 @@ __device__ __forceinline__ void for_cls_batched(const BwdArgs& a, int64_t base, 
   }
 }
 
+// Softmax-CE gradient of one class row held in registers (NR logits per
+// lane, 1 <= C <= 64 NR): every load of the row is issued before the first
+// use, then the wave's max, the exp sum and the gradient follow without
+// further memory round trips.
+template <int NR>
+__device__ __forceinline__ void cls_softmax_regs(const BwdArgs& a, int64_t base, int64_t C,
+                                                 int64_t tgt, float coeff) {
+  const int lane = threadIdx.x & 63;
+  // the row's start is wave-uniform, so each access takes a 32-bit offset
+  const int es = a.cls_dtype == ML_F32 ? 4 : 2;
+  const char* rowp = (const char*)a.cls_logits + base * es;
+  char* rowg = (char*)a.grad_cls + base * es;
+  const uint32_t last = (uint32_t)C - 1u;
+  float zv[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k)
+    zv[k] = cls_in(rowp, a.cls_dtype, min((uint32_t)(lane + 64 * k), last));  // clamped into the row
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < NR; ++k)
+    if (lane + 64 * k < C) m = fmaxf(m, zv[k]);
+  m = wave_max(m);
+  float se = 0.f;
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    zv[k] = lane + 64 * k < C ? __expf(zv[k] - m) : 0.f;
+    se += zv[k];
+  }
+  se = wave_sum(se);
+  const float inv = se > 0.f ? 1.f / se : 0.f;
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const uint32_t c = (uint32_t)(lane + 64 * k);
+    if (c <= last) cls_out(rowg, a.cls_dtype, c, coeff * (zv[k] * inv - ((int64_t)c == tgt ? 1.f : 0.f)));
+  }
+}
+
+// MAXR: the largest register form (logits per lane) this caller holds; the
+// persistent mask kernel keeps it small so its own registers are not squeezed
+template <int MAXR>
 __device__ void cls_row(const BwdArgs& a, int64_t row) {
   const int lane = threadIdx.x & 63;
   const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
@@ -355,30 +397,12 @@ __device__ void cls_row(const BwdArgs& a, int64_t row) {
   if (a.use_softmax) {
     if (matched || (a.force_cls && has_void)) {
       const int64_t tgt = matched ? y : a.void_idx;
-      if (C <= 64 * kClsRegs) {  // the row's logits stay in registers: one load
-        float zv[kClsRegs];
-        float m = -INFINITY;
-#pragma unroll
-        for (int k = 0; k < kClsRegs; ++k) {
-          const int64_t c = lane + 64 * k;
-          zv[k] = c < C ? cls_in(a.cls_logits, a.cls_dtype, base + c) : -INFINITY;
-          m = fmaxf(m, zv[k]);
-        }
-        m = wave_max(m);
-        float se = 0.f;
-#pragma unroll
-        for (int k = 0; k < kClsRegs; ++k) {
-          zv[k] = lane + 64 * k < C ? __expf(zv[k] - m) : 0.f;
-          se += zv[k];
-        }
-        se = wave_sum(se);
-        const float inv = se > 0.f ? 1.f / se : 0.f;
-#pragma unroll
-        for (int k = 0; k < kClsRegs; ++k) {
-          const int64_t c = lane + 64 * k;
-          if (c < C) cls_out(a.grad_cls, a.cls_dtype, base + c, coeff * (zv[k] * inv - (c == tgt ? 1.f : 0.f)));
-        }
-        return;
+      // rows of up to 64 MAXR logits stay in registers: one round of loads
+      if (C <= 64 * kClsRegs) return cls_softmax_regs<kClsRegs>(a, base, C, tgt, coeff);
+      if constexpr (MAXR >= 24) {
+        if (C <= 64 * 8) return cls_softmax_regs<8>(a, base, C, tgt, coeff);
+        if (C <= 64 * 16) return cls_softmax_regs<16>(a, base, C, tgt, coeff);
+        if (C <= 64 * 24) return cls_softmax_regs<24>(a, base, C, tgt, coeff);
       }
       float m = -INFINITY;
       for_cls_batched(a, base, C, [&](int64_t, float z) { m = fmaxf(m, z); });
@@ -429,7 +453,7 @@ __device__ void cls_row(const BwdArgs& a, int64_t row) {
 // one wave per (l,b,q) row; 4 rows per workgroup
 __global__ __launch_bounds__(256) void bwd_cls_kernel(BwdArgs a) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row < a.L * a.B * a.Q) cls_row(a, row);
+  if (row < a.L * a.B * a.Q) cls_row<24>(a, row);
 }
 
 // ---- bf16 logits: the per-logit gradient terms from an LDS table ------------
@@ -698,7 +722,7 @@ __global__ __launch_bounds__(kLutThreads) void bwd_mask_lut_kernel(BwdArgs a, in
     const int64_t rank = (int64_t)blockIdx.x - (G - nlight);
     if (rank >= 0)
       for (int64_t r0 = rank * kWaves; r0 < rows; r0 += nlight * kWaves)
-        if (r0 + wave < rows) cls_row(a, r0 + wave);
+        if (r0 + wave < rows) cls_row<kClsRegs>(a, r0 + wave);
   }
 }
 

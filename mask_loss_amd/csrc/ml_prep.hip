@@ -178,9 +178,12 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
         slots = a.plan.slots[c];
       }
     // row-tile pairs (class 0): the K-split is chosen for the pair count and
-    // stored as the number of 4-split quads (what reaches the partial sums)
+    // stored as the number of 4-split quads (what reaches the partial sums).
+    // A workgroup holds 4 pairs, so the pairs count in whole quads: with a
+    // partly filled last quad, np pairs would let ceil(np / 4) x KSq
+    // workgroups exceed the one-per-CU residency and run a second round.
     const bool pairs = lane == 0 && a.plan.pair0;
-    const int64_t units = pairs ? (n / a.rtiles) * ((a.rtiles + 1) >> 1) : (int64_t)n;
+    const int64_t units = pairs ? 4 * (((n / a.rtiles) * ((a.rtiles + 1) >> 1) + 3) >> 2) : (int64_t)n;
     int64_t ks = units > 0 ? slots / units : 1;
     ks = ks < 1 ? 1 : (ks > a.plan.ks_max ? a.plan.ks_max : ks);
     if (pairs) ks = ks >= 8 ? ks >> 2 : 1;

@@ -573,7 +573,14 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     predj[t] = valid[t] ? preds[j - 1] : 0;
   }
   bool ok = true;
+  // the cost row of the row being inserted is read before that row starts:
+  // the first row's here, every later one's during the previous row's
+  // augmentation walk, whose latency then hides the read
+  int colcur = __builtin_amdgcn_readfirstlane(hrows[0]);
+  float rawf[NJ];
+  read_cost_row<NJ, CM>(cost, colcur, predj, rawf);
   for (int i = 1; i <= M && ok; ++i) {
+    const int colnext = i < M ? hrows[i] : colcur;  // no dependence: loaded early
     // minv: a quiet NaN marks a column in the tree (and an unused slot);
     // f: 1.0 for a column in the tree, else 0.0 (its low word stays 0)
     double minv[NJ], f[NJ];
@@ -585,11 +592,8 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       wy[t] = 0;
     }
     double ucur = 0.0;  // potential of row i (column 0 of the reference)
-    const int colcur = __builtin_amdgcn_readfirstlane(hrows[i - 1]);
     int j0 = 0;
     double ui0 = ucur;
-    float rawf[NJ];
-    read_cost_row<NJ, CM>(cost, colcur, predj, rawf);
     for (;;) {
       // relax every column outside the tree (no branches: the NJ chains
       // interleave) and keep this lane's minimum
@@ -650,6 +654,8 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       read_cost_row<NJ, CM>(cost, pr1 >> 16, predj, rawf);
     }
     if (!ok) break;
+    const int cn = __builtin_amdgcn_readfirstlane(colnext);
+    if (i < M) read_cost_row<NJ, CM>(cost, cn, predj, rawf);  // row i + 1's first step
     // augment along way[] from the free column j0 back to column 0: each
     // column on the path takes the row (and that row's potential and cost
     // row) of the column it was reached from; column 0 holds row i.
@@ -677,6 +683,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       }
       j0 = jp;
     }
+    colcur = cn;
   }
   if (ok) {
 #pragma unroll

@@ -37,8 +37,8 @@ constexpr int kFillBlocks = 64;
 // the finalize launch, as extra workgroups beside their own work: both are
 // short, latency-bound launches that leave HBM nearly idle, so these bytes
 // come off the assignment launch, where the fill outlasts a short assignment.
-constexpr int64_t kPrepFillBytes = (int64_t)24 << 20;
-constexpr int64_t kFinFillBytes = (int64_t)48 << 20;
+constexpr int64_t kPrepFillBytes = (int64_t)56 << 20;
+constexpr int64_t kFinFillBytes = (int64_t)16 << 20;
 
 // Column-tile classes of the cost contraction: an image with G non-empty GT
 // columns (+ the ones column) is handled by the kernel instance whose tile

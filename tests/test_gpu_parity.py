@@ -371,6 +371,40 @@ def test_matching_backward(ml, case, mode):
         assert (gzn[unmatched] == 0).all()
 
 
+@pytest.mark.parametrize("G,class1_empty", [(31, True), (40, False)])
+def test_prefilled_fill_shares(ml, G, class1_empty):
+    """The prefilled gradient's zero fill is shared by three launches (the
+    column pass, finalize and the assignment). With a 7.0 sentinel in the
+    buffer, the prefilled backward must equal the saved-state backward (which
+    writes every row itself) bit for bit, at a size where every share is used
+    (105 MB of gradient) and with GT_out + 1 > 32 columns, so the NT = 7
+    column-tile class is launched: empty (every image has at most 31
+    non-empty GTs) or not."""
+    x = make_case(47, B=4, Q=200, H=256, W=256, G=G, dtype="bfloat16", sigma=3.0)
+    present = [int((np.unique(x["tgt_np"][b]) > 0).sum()) for b in range(4)]
+    assert (max(present) <= 31) == class1_empty, present  # the case's premise
+    P, M = params(dict(use_softmax=True)), mparams(dict(force_cls=True, void=8))
+    prefill = torch.full_like(x["z"], 7.0)
+    outs = matching_call(ml, x, P, M, prefill)
+    p2g, saved = outs[0], outs[5]
+    gm = torch.tensor([0.7], device="cuda")
+    gd = torch.tensor([1.3], device="cuda")
+    gc = torch.tensor([0.9], device="cuda")
+    ss, ds, cs = P["scales"]
+    args = (gm, gd, gc, x["z"], x["tgt"], x["zc"], x["ct"], p2g, P["smooth"], ss, ds, cs, P["bg"],
+            P["ug"], P["ug_min"], M["num_masks"], M["force_cls"], M["force_masks"], P["mask_gamma"],
+            P["mask_alpha"], P["cls_gamma"], P["cls_alpha"], M["void"], P["use_softmax"],
+            P["normalize"])
+    gz_pre, _ = ml.mask_matching_backward_fused(*args, saved, prefill)
+    gz_all, _ = ml.mask_matching_backward_fused(*args, saved)
+    torch.cuda.synchronize()
+    assert gz_pre.data_ptr() == prefill.data_ptr()
+    assert not (gz_pre == 7.0).any()
+    unmatched = (p2g < 0).reshape(-1)
+    assert (gz_pre.reshape(-1, 256 * 256)[unmatched] == 0).all()
+    assert torch.equal(gz_pre, gz_all)
+
+
 def test_function_autograd_bf16(ml):
     from mask_loss_amd.functions import MaskMatchingFunction
     x = make_case(44, dtype="bfloat16", sigma=3.0, Q=40, G=12)

@@ -190,6 +190,10 @@ MATCH_CASES = [
     dict(name="split_lds_round_K2", kw=dict(Q=300, H=8, W=8, G=160), p={}, m=dict(K=2, strategy=1)),
     dict(name="split_lds_pseudo_greedy_K2", kw=dict(Q=300, H=8, W=8, G=200), p={},
          m=dict(K=2, strategy=3)),
+    # finalize's wide form: more than 192 classes held in registers (20 per lane)
+    dict(name="softmax_C700", kw=dict(C=700, Q=24), p=dict(use_softmax=True),
+         m=dict(force_cls=True, void=699)),
+    dict(name="sigmoid_C1280", kw=dict(C=1280, Q=24), p={}, m=dict(force_cls=True, void=1279)),
 ]
 
 
@@ -324,6 +328,14 @@ BWD_CASES = [
     dict(name="bf16_softmax", kw=dict(dtype="bfloat16", sigma=3.0), p=dict(use_softmax=True),
          m=dict(force_cls=True, void=8)),
     dict(name="f32_odd", kw=dict(Q=37, H=7, W=5, B=3), p={}, m=dict(void=8)),
+    # class rows longer than 256 logits: the class-gradient launch holds 8 or
+    # 16 logits per lane (f32 masks), the bf16 table kernel streams them
+    dict(name="f32_softmax_C300", kw=dict(C=300, Q=24), p=dict(use_softmax=True),
+         m=dict(force_cls=True, void=299)),
+    dict(name="f32_softmax_C700", kw=dict(C=700, Q=24), p=dict(use_softmax=True),
+         m=dict(force_cls=True, void=699)),
+    dict(name="bf16_softmax_C700", kw=dict(C=700, Q=24, dtype="bfloat16", sigma=3.0),
+         p=dict(use_softmax=True), m=dict(force_cls=True, void=699)),
 ]
 
 

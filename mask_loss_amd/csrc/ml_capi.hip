@@ -126,8 +126,9 @@ bool make_dims(const ml_shape* s, int64_t background_index, int dtype, Dims& d,
   d.nslot = 16 * d.NT;
   d.rtiles = ceil_div(d.Q, d.rows);
   // a wave covers at least 4 K-steps of its task (small maps then split
-  // further and fill more of the GPU: cfg1's 64x64 contraction 24.5 -> 15.8 us
-  // against 8; large maps are bound by the resident slots, not by this)
+  // further and fill more of the GPU: a 64 x 64 map with 14 row tiles takes
+  // 15.8 us instead of 24.5 with 8; large maps are bound by the resident
+  // slots, not by this)
   const int64_t nsteps = ceil_div(d.HW, kStep);
   d.ks_max = nsteps / 4 > 1 ? nsteps / 4 : 1;
   d.counts_mode = d.s > 1;

@@ -198,14 +198,11 @@ __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
   const int64_t b = blockIdx.y;
   const int64_t HW = a.H * a.W;
   const bool mark = a.pbits != nullptr;
-  if (mark) {
-    pres_clear(pres);
-    void_check(a, b);  // ends with a barrier
-    __syncthreads();
-  }
+  // the labels are loaded first, so that their latency and the void check's
+  // (first workgroup of each image) overlap
   const int64_t cell0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  int64_t lab[8];
   if (cell0 < a.HWp) {
-    int64_t lab[8];
     const int64_t* src = a.targets + b * HW + cell0;
     if (HW % 8 == 0 && cell0 + 8 <= HW) {  // 64-byte aligned run of 8 labels
 #pragma unroll
@@ -218,6 +215,13 @@ __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) lab[k] = cell0 + k < HW ? src[k] : -1;
     }
+  }
+  if (mark) {
+    pres_clear(pres);
+    void_check(a, b);  // ends with a barrier
+    __syncthreads();
+  }
+  if (cell0 < a.HWp) {
     uint32_t wv[4];
     int64_t prev = -1;
     const int64_t lane0 = __shfl(lab[0], 0, 64);

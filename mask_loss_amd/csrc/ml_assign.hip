@@ -502,11 +502,11 @@ __device__ __forceinline__ double sel_d(const double (&x)[NJ], const SlotMask<NJ
 // comparison or sum can see), so the assignment is the reference's bit for
 // bit.
 // ---------------------------------------------------------------------------
-// Cost rows of one image, [column][query] with row stride ldq: rows c < nl
-// in LDS, the others read in place from finalize's total-cost plane (L2).
+// Cost rows of one image, [column][query] with row stride ldq: all in LDS,
+// or all read in place from finalize's total-cost plane (L2).
 // CM, a compile-time choice so that each read is a ds_read or a global load:
-// kCostLds (every row in LDS), kCostGlobal (none), kCostSplit (the first nl).
-enum { kCostGlobal = 0, kCostLds = 1, kCostSplit = 2 };
+// kCostLds (every row in LDS) or kCostGlobal (none).
+enum { kCostGlobal = 0, kCostLds = 1 };
 typedef __attribute__((address_space(3))) const float lds_f32;     // LDS
 typedef __attribute__((address_space(1))) const float global_f32;  // device memory
 template <int CM>
@@ -516,24 +516,18 @@ struct CostRows {
   const lds_f32* lds;
   const global_f32* glb;
   int ldq;  // c * ldq fits 31 bits: Q <= 1024, and the column arrays fit the LDS
-  int nl;
-  __device__ __forceinline__ bool in_lds(int c) const {
-    return CM == kCostLds || (CM == kCostSplit && c < nl);
-  }
-  // one element (per-lane column): split mode reads the plane in place, where
-  // every row is (the LDS rows are copies), so no read goes through a flat
-  // pointer
+  // one element (per-lane column)
   __device__ __forceinline__ float at(int64_t c, int64_t q) const {
     return CM == kCostLds ? lds[c * ldq + q] : glb[c * ldq + q];
   }
 };
 
-// The row of column col, at the slots' query indices: a wave-uniform branch
-// between a ds_read row and an in-place global row.
+// The row of column col, at the slots' query indices: a ds_read row or an
+// in-place global row.
 template <int NJ, int CM>
 __device__ __forceinline__ void read_cost_row(const CostRows<CM>& cost, int col,
                                               const int (&predj)[NJ], float (&rawf)[NJ]) {
-  if (cost.in_lds(col)) {
+  if (CM == kCostLds) {
     const lds_f32* crow = cost.lds + col * cost.ldq;
 #pragma unroll
     for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
@@ -809,8 +803,7 @@ __device__ void layer_pass(const LayerArgs& a, int* sbuf, int nsbuf) {
 }
 
 // CM: where the image's cost rows live (CostRows): all in LDS when the
-// matrix fits, else the first lds_rows columns' rows in LDS and the rest read
-// in place from finalize's total-cost plane.
+// matrix fits, else read in place from finalize's total-cost plane.
 // Workgroups L*B .. L*B + fill_blocks - 1 zero-fill the gradient buffer:
 // the assignment keeps one CU per image busy with a serial chain and leaves
 // HBM idle, so the fill runs beside it in the same launch, from its start
@@ -854,7 +847,7 @@ __device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int6
       for (int k = 0; k < KW; ++k) {
         const int j = lane + 64 * k;
         if (j >= W) continue;
-        if (CM == kCostLds || (CM == kCostSplit && col[r] < lds_rows))
+        if (CM == kCostLds)
           ((word_t*)costL)[(int64_t)col[r] * W + j] = v[r][k];
         const float* e = (const float*)&v[r][k];
 #pragma unroll
@@ -895,7 +888,6 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   crows.lds = (const lds_f32*)costL;
   crows.glb = (const global_f32*)(a.tot + lb * a.tot_stride);
   crows.ldq = (int)Q;
-  crows.nl = (int)a.lds_rows;
   const int64_t term = a.L * a.B * Q * GTo;
   const float* sep = a.sep + lb * Q * GTo;
 
@@ -1205,7 +1197,6 @@ static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
 template <int NJ>
 static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
   if (a.lds_rows >= a.GT_out) return launch_nj_l<NJ, kCostLds>(a, d, st);
-  if (a.lds_rows > 0) return launch_nj_l<NJ, kCostSplit>(a, d, st);
   return launch_nj_l<NJ, kCostGlobal>(a, d, st);
 }
 int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {

@@ -229,16 +229,13 @@ static bool check_assign_dims(const Dims& d, std::string& err) {
 }
 
 // Cost rows (by column) the assignment keeps in LDS: all GT_out of them when
-// they fit, else as many as fit (the others are read in place from L2).
+// they fit, else none (every row is then read in place from L2: on the
+// widest images that beats keeping only the first rows in LDS, whose staging
+// writes cost more than the L2 reads they replace, since each Dijkstra step
+// is bound by its own instruction chain and not by the row read).
 // 1 KB stays free for the assignment kernel's static LDS.
 static int64_t cost_lds_rows(const Dims& d) {
-  const size_t budget = kMaxLds - 1024;
-  if (assign_smem_bytes(d.Q, d.GT_out, d.GT_out) <= budget) return d.GT_out;
-  const size_t base = assign_smem_bytes(d.Q, d.GT_out, 0);
-  if (d.Q <= 0 || base + 16 > budget) return 0;
-  int64_t n = (int64_t)((budget - base - 16) / ((size_t)d.Q * 4));
-  while (n > 0 && assign_smem_bytes(d.Q, d.GT_out, n) > budget) --n;
-  return n;
+  return assign_smem_bytes(d.Q, d.GT_out, d.GT_out) <= kMaxLds - 1024 ? d.GT_out : 0;
 }
 
 static int check_focal(float gamma, float alpha, const char* who) {

@@ -307,7 +307,7 @@ struct AssignArgs {
   int64_t topk;
   int strategy;
   int costs_only;
-  int64_t lds_rows;  // cost rows (columns 0 .. lds_rows - 1) the assignment keeps in LDS
+  int64_t lds_rows;  // GT_out when the assignment keeps every cost row in LDS, else 0
 };
 
 

@@ -184,11 +184,11 @@ MATCH_CASES = [
     dict(name="counts_s17_force", kw=dict(s=17, H=4, W=4), p={}, m=dict(force_masks=True, force_cls=True)),
     dict(name="empty_image", kw=dict(empty_image=True), p={}, m=dict(force_cls=True, void=8)),
     dict(name="q_tail_1024", kw=dict(Q=130, H=8, W=8, G=20), p={}, m={}),
-    # cost matrices too large for LDS (300 x 250 floats): the first columns'
-    # rows in LDS, the others read in place
-    dict(name="split_lds_global", kw=dict(Q=300, H=8, W=8, G=250), p={}, m={}),
-    dict(name="split_lds_round_K2", kw=dict(Q=300, H=8, W=8, G=160), p={}, m=dict(K=2, strategy=1)),
-    dict(name="split_lds_pseudo_greedy_K2", kw=dict(Q=300, H=8, W=8, G=200), p={},
+    # cost matrices too large for LDS (300 x 250 floats): every row read in
+    # place from the total-cost plane
+    dict(name="global_rows", kw=dict(Q=300, H=8, W=8, G=250), p={}, m={}),
+    dict(name="global_rows_round_K2", kw=dict(Q=300, H=8, W=8, G=160), p={}, m=dict(K=2, strategy=1)),
+    dict(name="global_rows_pseudo_greedy_K2", kw=dict(Q=300, H=8, W=8, G=200), p={},
          m=dict(K=2, strategy=3)),
     # finalize's wide form: more than 192 classes held in registers (20 per lane)
     dict(name="softmax_C700", kw=dict(C=700, Q=24), p=dict(use_softmax=True),

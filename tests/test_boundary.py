@@ -216,3 +216,21 @@ def test_function_validation_errors():
         call(mask_alpha=2.0)
     with pytest.raises(RuntimeError, match="CUDA tensor"):
         call()
+
+
+def test_losses_dispatcher_argument_errors():
+    """functions/losses.py:8-67: the branches whose operators the reference's
+    sources lack, and malformed arguments, raise before any GPU work."""
+    import torch
+    from mask_loss_amd.functions import losses
+    z = torch.zeros(2, 3, 4, 4)
+    t = torch.zeros(2, 8, 8, dtype=torch.long)
+    for fn in (losses.sigmoid_cross_entropy_loss, losses.dice_loss):
+        with pytest.raises(NotImplementedError, match="multi-class"):
+            fn(z, t, class_mapping=torch.arange(256))
+        with pytest.raises(NotImplementedError, match="pure-PyTorch"):
+            fn(z, t, implementation="python")
+        with pytest.raises(ValueError, match="implementation"):
+            fn(z, t, implementation="triton")
+        with pytest.raises(ValueError, match="logits must be"):
+            fn(z[0], t)

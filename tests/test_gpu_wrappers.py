@@ -152,3 +152,39 @@ def test_wrapper_validation(F):
                                          None, 0, None, None, None, None, None, None, None, "sigmoid")
     with pytest.raises(AssertionError, match="Batch size mismatch"):
         F.PairwiseDiceLossFunction.apply(x["z"], x["tgt"][:1], None, None, None)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_losses_dispatchers(F, dtype):
+    """functions/losses.py:8-67: (B, C, h, w) logits give a scalar, (L, B, C,
+    h, w) one loss per layer; both against the float64 oracle."""
+    x = inputs(31, L=2, B=2, Q=12, H=8, W=8, G=5, dtype=dtype)
+    B, C = 2, 12
+    z4 = x["z"][0]
+    tg = torch.from_numpy(np.kron(x["tgt_np"], np.ones((1, 2, 2), np.int64))).cuda()  # s = 2
+    ce = F.sigmoid_cross_entropy_loss(z4, tg, scale=1.5)
+    dl = F.dice_loss(z4, tg, smooth=1.0, scale=0.7)
+    assert ce.dim() == 0 and dl.dim() == 0
+    tgn = tg.cpu().numpy()
+    close(ce.item(), O.sigmoid_ce_loss(x["z64"][:1], tgn, B * C, scale=1.5)[0], RTOL[dtype])
+    close(dl.item(), O.dice_loss(x["z64"][:1], tgn, 1.0, B * C, scale=0.7)[0][0], RTOL[dtype])
+    ce5 = F.sigmoid_cross_entropy_loss(x["z"], tg, num_masks=10.0)
+    dl5 = F.dice_loss(x["z"], tg, num_masks=10.0)
+    assert tuple(ce5.shape) == (2,) and tuple(dl5.shape) == (2,)
+    close(ce5.cpu().numpy(), O.sigmoid_ce_loss(x["z64"], tgn, 10.0), RTOL[dtype])
+    close(dl5.cpu().numpy(), O.dice_loss(x["z64"], tgn, 1e-6, 10.0)[0], RTOL[dtype])
+
+
+def test_losses_dispatcher_errors(F):
+    x = inputs(32, L=1, B=2, Q=4, H=8, W=8, G=3)
+    z4 = x["z"][0]
+    cm = torch.arange(256, device=z4.device)
+    for fn in (F.sigmoid_cross_entropy_loss, F.dice_loss):
+        with pytest.raises(NotImplementedError, match="multi-class"):
+            fn(z4, x["tgt"], class_mapping=cm)
+        with pytest.raises(NotImplementedError, match="pure-PyTorch"):
+            fn(z4, x["tgt"], implementation="python")
+        with pytest.raises(ValueError, match="implementation"):
+            fn(z4, x["tgt"], implementation="triton")
+        with pytest.raises(ValueError, match="logits must be"):
+            fn(z4[0], x["tgt"])

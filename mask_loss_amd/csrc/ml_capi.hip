@@ -238,6 +238,19 @@ static int64_t cost_lds_rows(const Dims& d) {
   return assign_smem_bytes(d.Q, d.GT_out, d.GT_out) <= kMaxLds - 1024 ? d.GT_out : 0;
 }
 
+// The matching forward's required device pointers: every input and the three
+// outputs (a shape with no query rows reads and writes none of them).
+static int check_matching_pointers(const ml_shape* s, const void* mask_logits,
+                                   const int64_t* mask_targets, const void* cls_logits,
+                                   const int64_t* cls_targets, const int64_t* pred_to_gt,
+                                   const int64_t* pred_round, const float* layer_means) {
+  if (s->L <= 0 || s->B <= 0 || s->Q <= 0) return ML_OK;
+  if (!mask_logits || !mask_targets || !cls_logits || !cls_targets || !pred_to_gt || !pred_round ||
+      !layer_means)
+    return fail(ML_EINVAL, "matching forward: a required input or output pointer is null");
+  return ML_OK;
+}
+
 static int check_focal(float gamma, float alpha, const char* who) {
   if (!(gamma >= 0.f)) return fail(ML_EINVAL, std::string(who) + " focal_gamma must be non-negative");
   if (!(alpha < 0.f || (alpha >= 0.f && alpha <= 1.f)))
@@ -280,11 +293,15 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                  bool packed) {
   if (!dtype_ok(mask_dtype) || (cls_logits && !dtype_ok(cls_dtype)))
     return fail(ML_EINVAL, "unsupported dtype");
-  if (!cls_logits && !costs_only) return fail(ML_EINVAL, "matching needs class logits");
   Dims d;
   std::string err;
   if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
   if (!costs_only && !check_assign_dims(d, err)) return fail(ML_EUNSUPPORTED, err);
+  if (!costs_only) {
+    const int rc = check_matching_pointers(s, mask_logits, mask_targets, cls_logits, cls_targets,
+                                           pred_to_gt, pred_round, layer_means);
+    if (rc) return rc;
+  }
   const bool force_masks = !costs_only && p->force_unmatched_masks_to_empty;
   if (prefill && (force_masks || costs_only || !saved))
     return fail(ML_EINVAL, "gradient prefill needs a saved state and unforced unmatched masks");
@@ -475,17 +492,24 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
 }
 
 // Workspace bytes of the matching forward with the packed cost plan (what
-// forward_impl with packed = true needs), or 0 with `err` set.
-size_t forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype,
-                            std::string& err) {
+// forward_impl with packed = true needs) in `bytes`; the shape errors are
+// those of ml_mask_matching_forward (ML_EINVAL for malformed shapes,
+// ML_EUNSUPPORTED for shapes the assignment does not take).
+int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t& bytes) {
   Dims d;
-  if (!make_dims(s, p->background_index, mask_dtype, d, err) || !check_assign_dims(d, err)) return 0;
+  std::string err;
+  bytes = 0;
+  if (!make_dims(s, p->background_index, mask_dtype, d, err)) return fail(ML_EINVAL, err);
+  if (!check_assign_dims(d, err)) return fail(ML_EUNSUPPORTED, err);
   const bool force_masks = p->force_unmatched_masks_to_empty != 0;
   const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
   CostPlan plan = make_cost_plan(d, mask_dtype, tab);
   pack_cost_plan(plan, d);
-  return make_layout(d, force_masks, plan).total;
+  bytes = make_layout(d, force_masks, plan).total;
+  return ML_OK;
 }
+
+
 
 }  // namespace ml
 

@@ -371,7 +371,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype, const vo
                  hipEvent_t void_ready, void* ws, size_t ws_bytes, hipStream_t st, bool costs_only,
                  float* bce_out, float* dice_out, const float* pt_coords, int64_t pt_Hs,
                  int64_t pt_Ws, bool packed);
-size_t forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, std::string& err);
+int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t& bytes);
 int check_matching_params(const ml_params* p, int64_t C);
 
 // ---- instrumentation: bracket a launch with events when profiling is on ------

@@ -63,9 +63,8 @@ extern "C" int ml_mask_matching_forward_noalloc(
     ml_stream_t stream) {
   int rc = check_matching_params(p, s->C);
   if (rc) return rc;
-  std::string err;
-  const size_t need = forward_packed_bytes(s, p, mask_dtype, err);
-  if (!err.empty()) return fail(ML_EINVAL, err);
+  size_t need = 0;
+  if ((rc = forward_packed_bytes(s, p, mask_dtype, need))) return rc;
   if (need > kScratchBytes)
     return fail(ML_EUNSUPPORTED, "no-allocation forward: this shape needs " + std::to_string(need) +
                                      " bytes of scratch, more than the " +

@@ -220,7 +220,8 @@ def test_function_validation_errors():
 
 def test_losses_dispatcher_argument_errors():
     """functions/losses.py:8-67: the branches whose operators the reference's
-    sources lack, and malformed arguments, raise before any GPU work."""
+    sources lack, and malformed arguments, raise before any GPU work; every
+    implementation value but "python" goes to the GPU operator."""
     import torch
     from mask_loss_amd.functions import losses
     z = torch.zeros(2, 3, 4, 4)
@@ -230,7 +231,9 @@ def test_losses_dispatcher_argument_errors():
             fn(z, t, class_mapping=torch.arange(256))
         with pytest.raises(NotImplementedError, match="pure-PyTorch"):
             fn(z, t, implementation="python")
-        with pytest.raises(ValueError, match="implementation"):
+        # any other value selects the GPU operator, as in the reference, so
+        # host tensors are rejected by it
+        with pytest.raises(RuntimeError, match="CUDA tensor"):
             fn(z, t, implementation="triton")
         with pytest.raises(ValueError, match="logits must be"):
             fn(z[0], t)

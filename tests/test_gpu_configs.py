@@ -7,6 +7,11 @@ the sum of the layer means -- at its full size, and is checked:
 * the assignment and pred_round of every image, bit for bit, against the C
   restatement of the reference solver on the GPU's own float32 cost matrix
   (reference src/cpu/matching.cpp:95-186, :476-571);
+* the assignment of every image against the same solver on the float64
+  oracle's costs of that image (all queries, all columns): equal, or not
+  separated from the float64 optimum by more than rt * sum |matched costs|
+  (the north star's index rule; at bfloat16 this covers the cost table's
+  rounding of the four planes);
 * the bce / dice / label costs of two full images (the ones with the most and
   the fewest non-empty GTs) against the float64 oracle (reference
   src/cuda/pw_mask.cu:52-308, src/cuda/pw_softmax_label_loss.cu:12-103);
@@ -38,6 +43,7 @@ torch = pytest.importorskip("torch")
 from oracle import assign as OA  # noqa: E402
 from oracle import mask_oracle as O  # noqa: E402
 from oracle import points_oracle as PO  # noqa: E402
+from assign_rule import check_f64_assignment_total  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -106,6 +112,30 @@ def present_columns(tgt_np, GT_total, bg):
     return pres, acts
 
 
+def oracle_image_costs(cfg, z, t, zc, ct):
+    """The float64 oracle's separate costs (3, L, B, Q, G) of every image,
+    one image per host thread (one BLAS thread each)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+    a = kw_args(cfg)
+    B = t.shape[0]
+    tgt_np = t.cpu().numpy()
+    ct_np = ct.cpu().numpy()
+    zc64 = zc.detach().double().cpu().numpy()
+
+    def one(b):
+        z64 = z.detach()[:, b:b + 1].double().cpu().numpy()
+        return O.pairwise_mask_loss_forward(z64, tgt_np[b:b + 1], zc64[:, b:b + 1], ct_np[b:b + 1],
+                                            a["smooth"], a["ss"], a["ds"], a["cs"], a["bg"], a["ug"],
+                                            a["ug_min"], 0.0, -1.0, 0.0, -1.0, a["softmax"], True)
+
+    with threadpool_limits(limits=1):
+        with ThreadPoolExecutor(min(B, 16)) as ex:
+            parts = list(ex.map(one, range(B)))
+    return np.concatenate(parts, axis=2)
+
+
 def check_step(ml, cfg, z, t, zc, ct, p2g, pr, means, gz, gzc, dtype, full_oracle=False,
                grad_map=None):
     """All checks of the module docstring on one step's results.  grad_map(b,
@@ -127,6 +157,14 @@ def check_step(ml, cfg, z, t, zc, ct, p2g, pr, means, gz, gzc, dtype, full_oracl
     rp2g, rpr = OA.assign_batch(total, a["inf_thresh"], a["K"], 0, nthreads=8)
     assert np.array_equal(p2g_np.reshape(L * B, Q), rp2g), "assignment differs from the reference solver"
     assert np.array_equal(pr.cpu().numpy().reshape(L * B, Q), rpr), "pred_round differs"
+    # 1b. the north star's index rule on every image: the float64 oracle's
+    # costs of all images, the reference solver on them, the GPU's indices
+    # equal or within the cost tolerance of that optimum
+    ref_all = oracle_image_costs(cfg, z, t, zc, ct)
+    tot64 = ((ref_all[0] + ref_all[1]) + ref_all[2]).reshape(L * B, Q, G)
+    _, ndiff = check_f64_assignment_total(tot64, p2g_np, rt, a["inf_thresh"], a["K"], 0,
+                                          nthreads=8)
+    print(f"{cfg.name}: {ndiff} of {L * B} slices differ from the float64 optimum (within tolerance)")
     # 2. properties on every row
     pres, acts = present_columns(tgt_np, GT_total, a["bg"])
     ycls = ct_np[:, acts]
@@ -168,9 +206,7 @@ def check_step(ml, cfg, z, t, zc, ct, p2g, pr, means, gz, gzc, dtype, full_oracl
     for b in imgs:
         z64 = z.detach()[:, b:b + 1].double().cpu().numpy()
         tb, cb = tgt_np[b:b + 1], ct_np[b:b + 1]
-        ref = O.pairwise_mask_loss_forward(z64, tb, zc64[:, b:b + 1], cb, a["smooth"], a["ss"],
-                                           a["ds"], a["cs"], a["bg"], a["ug"], a["ug_min"], 0.0,
-                                           -1.0, 0.0, -1.0, a["softmax"], True)
+        ref = ref_all[:, :, b:b + 1]
         close(sep[0][:, b:b + 1], ref[0], rt, 1e-2, f"bce image {b}")
         close(sep[1][:, b:b + 1], ref[1], rt, 1e-2, f"dice image {b}")
         close(sep[2][:, b:b + 1], ref[2], 1e-5, 1e-2, f"label cost image {b}")

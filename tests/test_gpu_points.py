@@ -248,6 +248,23 @@ def test_point_sample_backward(ml, dt, H, W, P, C):
     close(got.double().cpu().numpy(), ref, SAMPLE_RTOL[dt], np.abs(ref).max())
 
 
+@pytest.mark.parametrize("H,W,P,C", [(37, 29, 1025, 8), (128, 128, 12544, 8), (9, 13, 777, 9)])
+def test_point_sample_backward_align_corners(ml, H, W, P, C):
+    """align_corners=True on the grouped path (C >= 8 planes per coordinate
+    set: corner entries bucketed by base cell, then gathered per plane), with
+    coordinates outside [0, 1] (coords_with_edges), against the oracle's
+    adjoint of grid_sample with align_corners=True."""
+    rng = np.random.default_rng(57 + H + P + C)
+    c = coords_with_edges(rng, 3, P)
+    g64, g = as_dtype(rng.normal(0, 1, size=(3, C, P)), "float32")
+    g64[2, 1] = 0.0  # an all-zero row (an unmatched query)
+    g[2, 1] = 0
+    got = ml.point_sample_backward(g, torch.from_numpy(c).cuda(), H, W, True)
+    ref = PO.point_sample_backward(g64, c, H, W, True)
+    assert (got[2, 1] == 0).all()
+    close(got.double().cpu().numpy(), ref, SAMPLE_RTOL["float32"], np.abs(ref).max())
+
+
 def test_point_sample_autograd_4d_grid(ml):
     from mask_loss_amd.functions import point_sample
     rng = np.random.default_rng(4)

@@ -184,7 +184,10 @@ def test_losses_dispatcher_errors(F):
             fn(z4, x["tgt"], class_mapping=cm)
         with pytest.raises(NotImplementedError, match="pure-PyTorch"):
             fn(z4, x["tgt"], implementation="python")
-        with pytest.raises(ValueError, match="implementation"):
-            fn(z4, x["tgt"], implementation="triton")
+        # every value other than "python" runs the GPU operator
+        # (functions/losses.py:24-33, 57-67)
+        a = fn(z4, x["tgt"], num_masks=3.0, implementation="triton")
+        b = fn(z4, x["tgt"], num_masks=3.0)
+        assert torch.equal(a, b)
         with pytest.raises(ValueError, match="logits must be"):
             fn(z4[0], x["tgt"])

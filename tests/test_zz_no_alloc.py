@@ -141,9 +141,17 @@ def test_noalloc_forward_matches_workspace_forward(lib):
               rt, f"call {i} saved statistics")
 
 
+SCRATCH_BYTES = 128 << 20  # ML_NOALLOC_SCRATCH_BYTES (include/mask_loss_hip.h)
+
+
 def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
-    # 64 label maps of 1024 x 1024: their compact labels alone fill the 128 MiB
-    s = Shape(1, 64, 100, 1024, 1024, 1024, 1024, 9, 250)
+    # 128 label maps of 1024 x 1024: the forward's compact label map alone
+    # ([B][H W] 16-bit labels, the cost contraction's column operand) is
+    # twice the scratch array, checked here on the host before the call.
+    # Null device pointers: the call must fail before any launch (and the
+    # forward rejects null pointers itself if a shape ever passes the size check).
+    s = Shape(1, 128, 100, 1024, 1024, 1024, 1024, 9, 250)
+    assert s.B * s.Ht * s.Wt * 2 >= 2 * SCRATCH_BYTES
     p = params(9)
     dummy = ctypes.c_void_p(0)
     rc = lib.ml_mask_matching_forward_noalloc(ctypes.byref(s), ctypes.byref(p), ML_BF16, dummy, dummy,
@@ -151,3 +159,21 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
                                               None, None, None, None)
     assert rc == 4, rc  # ML_EUNSUPPORTED, before anything is launched
     assert b"scratch" in lib.ml_last_error()
+
+
+def test_noalloc_unsupported_shape_codes_match(lib):
+    """A shape the assignment does not take (Q = 1025) gives ML_EUNSUPPORTED
+    from both forwards, before any launch (null pointers throughout)."""
+    s = Shape(1, 2, 1025, 16, 16, 16, 16, 9, 7)
+    p = params(9)
+    dummy = ctypes.c_void_p(0)
+    rc_na = lib.ml_mask_matching_forward_noalloc(ctypes.byref(s), ctypes.byref(p), ML_F32, dummy,
+                                                 dummy, ML_F32, dummy, dummy, dummy, dummy, dummy,
+                                                 None, None, None, None, None, None)
+    err_na = lib.ml_last_error()
+    rc_ws = lib.ml_mask_matching_forward(ctypes.byref(s), ctypes.byref(p), ML_F32, dummy, dummy,
+                                         ML_F32, dummy, dummy, dummy, dummy, dummy, None, None, None,
+                                         None, None, dummy, 1 << 20, None)
+    err_ws = lib.ml_last_error()
+    assert rc_na == rc_ws == 4, (rc_na, rc_ws)
+    assert err_na == err_ws and b"1024 queries" in err_na

@@ -7,9 +7,11 @@
 // host tensors raise, as in the reference (src/cuda/utils.h:4-6,
 // src/cpu/matching.cpp:618).
 #include <ATen/hip/HIPContext.h>
+#include <torch/csrc/autograd/custom_function.h>
 #include <torch/extension.h>
 
 #include <chrono>
+#include <cstring>
 #include <thread>
 #include <vector>
 
@@ -390,6 +392,89 @@ std::vector<torch::Tensor> mask_matching_backward_fused(
                                   use_softmax, normalize);
   return backward_impl(g_mask, g_dice, g_cls, mask_logits, mask_targets, cls_logits, cls_targets,
                        pred_to_gt, p, &saved, grad_prefill);
+}
+
+// --------------------------------------------------------------------------
+// MaskMatchingFunction's autograd node (reference functions/mask/matching.py:
+// 33-334) in C++: the forward is mask_matching_fused with the gradient buffer
+// prefilled and the void-class check, the backward mask_matching_backward_fused
+// on the saved state.  The Python class keeps the reference's argument
+// defaulting and validation and calls mask_matching_autograd; the node itself
+// keeps the per-step host work to the launches (no Python frames in either
+// direction).
+// --------------------------------------------------------------------------
+struct MatchingNode : public torch::autograd::Function<MatchingNode> {
+  static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx,
+                                                const torch::Tensor& mask_logits,
+                                                const torch::Tensor& mask_targets,
+                                                const torch::Tensor& cls_logits,
+                                                const torch::Tensor& cls_targets,
+                                                const ml_params& p, bool check_void,
+                                                bool want_prefill) {
+    const auto z = mask_logits.contiguous();
+    const auto t = mask_targets.contiguous();
+    const auto zc = cls_logits.contiguous();
+    const auto ct = cls_targets.contiguous();
+    c10::optional<torch::Tensor> prefill;
+    if (want_prefill) prefill = torch::empty_like(z, at::MemoryFormat::Contiguous);
+    auto outs = matching_impl(z, t, zc, ct, p, true, prefill, check_void);
+    // outs: pred_to_gt, pred_round, the three layer means, saved state[, void flag]
+    ctx->save_for_backward({z, t, zc, ct, outs[0], outs[5]});
+    // the parameters travel as the bytes of their C struct
+    auto pb = torch::empty({(int64_t)sizeof(ml_params)}, torch::dtype(torch::kUInt8));
+    std::memcpy(pb.data_ptr(), &p, sizeof(ml_params));
+    ctx->saved_data["params"] = pb;
+    // the zero-filled gradient buffer serves the first backward only (a
+    // second backward through a retained graph gets a fresh tensor)
+    if (prefill.has_value()) ctx->saved_data["prefill"] = *prefill;
+    if (check_void && outs[6].item<int32_t>() == 1)
+      TORCH_CHECK_VALUE(false, "cls_targets must not contain the void class index");
+    ctx->mark_non_differentiable({outs[0], outs[1]});
+    ctx->set_materialize_grads(false);  // no zero gradients for the integer outputs
+    return {outs[0], outs[1], outs[2], outs[3], outs[4]};
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list g) {
+    const auto sv = ctx->get_saved_variables();
+    const auto& z = sv[0];
+    ml_params p;
+    std::memcpy(&p, ctx->saved_data["params"].toTensor().data_ptr(), sizeof(ml_params));
+    // as mask_matching_backward_fused: the assignment's own fields do not apply
+    p.inf_thresh = 1e30;
+    p.topk_matches = 1;
+    p.strategy_id = 0;
+    c10::optional<torch::Tensor> prefill;
+    auto it = ctx->saved_data.find("prefill");
+    if (it != ctx->saved_data.end()) {
+      prefill = it->second.toTensor();
+      ctx->saved_data.erase(it);
+    }
+    auto grad_of = [&](const torch::Tensor& x) {
+      return x.defined() ? x.detach() : torch::zeros({z.size(0)}, z.options().dtype(torch::kFloat32));
+    };
+    const auto r = backward_impl(grad_of(g[2]), grad_of(g[3]), grad_of(g[4]), z, sv[1], sv[2],
+                                 sv[3], sv[4], p, &sv[5], prefill);
+    return {r[0], torch::Tensor(), r[1], torch::Tensor(), torch::Tensor(), torch::Tensor(),
+            torch::Tensor()};
+  }
+};
+
+std::vector<torch::Tensor> mask_matching_autograd(
+    const torch::Tensor& mask_logits, const torch::Tensor& mask_targets,
+    const torch::Tensor& cls_logits, const torch::Tensor& cls_targets, double smooth,
+    double sigmoid_scale, double dice_scale, double cls_scale, int64_t background_index, double ug,
+    double ug_min, double inf_thresh, double num_masks, bool force_cls, bool force_masks,
+    int64_t topk, int64_t strategy, double mask_gamma, double mask_alpha, double cls_gamma,
+    double cls_alpha, int64_t void_idx, bool use_softmax, bool normalize, bool check_void) {
+  const ml_params p = make_params(smooth, sigmoid_scale, dice_scale, cls_scale, background_index,
+                                  ug, ug_min, inf_thresh, num_masks, force_cls, force_masks, topk,
+                                  strategy, mask_gamma, mask_alpha, cls_gamma, cls_alpha, void_idx,
+                                  use_softmax, normalize);
+  const bool want_prefill =
+      torch::GradMode::is_enabled() && mask_logits.requires_grad() && !force_masks;
+  return MatchingNode::apply(mask_logits, mask_targets, cls_logits, cls_targets, p, check_void,
+                             want_prefill);
 }
 
 // --------------------------------------------------------------------------
@@ -778,6 +863,18 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("void_class_index"), py::arg("use_softmax_label_loss"),
         py::arg("normalize_uncertainty"), py::arg("grad_prefill") = py::none(),
         py::arg("check_void") = false);
+  m.def("mask_matching_autograd", &mask_matching_autograd,
+        "MaskMatchingFunction's forward as a C++ autograd node: pred_to_gt, pred_round and the "
+        "three layer means, differentiable in the mask and class logits (HIP)",
+        py::arg("mask_logits"), py::arg("mask_targets"), py::arg("cls_logits"),
+        py::arg("cls_targets"), py::arg("smooth"), py::arg("sigmoid_scale"), py::arg("dice_scale"),
+        py::arg("cls_scale"), py::arg("background_index"), py::arg("uncertainty_gamma"),
+        py::arg("uncertainty_gamma_min"), py::arg("inf_thresh"), py::arg("num_masks"),
+        py::arg("force_unmatched_class_to_background"), py::arg("force_unmatched_masks_to_empty"),
+        py::arg("topk_matches"), py::arg("strategy_id"), py::arg("mask_gamma"),
+        py::arg("mask_alpha"), py::arg("cls_gamma"), py::arg("cls_alpha"),
+        py::arg("void_class_index"), py::arg("use_softmax_label_loss"),
+        py::arg("normalize_uncertainty"), py::arg("check_void") = false);
   m.def("mask_matching_backward_fused", &mask_matching_backward_fused,
         "Mask matching backward using the forward's saved state (HIP)", py::arg("g_mask"),
         py::arg("g_dice"), py::arg("g_cls"), py::arg("mask_logits"), py::arg("mask_targets"),

@@ -193,7 +193,6 @@ Layout make_layout(const Dims& d, bool force_masks, const CostPlan& pl) {
   L.lab16 = take(d.counts_mode ? 0 : (size_t)d.B * d.HWp * 2);
   L.counts = take(d.counts_mode ? (size_t)d.B * d.GT_total * d.HWp * d.cw : 0);
   L.pbits = take((size_t)d.B * prep_blocks(d) * kPresWords * 4);
-  L.vflag = take((size_t)d.B * 4);
   L.ncols = take((size_t)d.B * 4);
   L.colmap = take((size_t)d.B * d.nslot * 4);
   L.slot_of_col = take((size_t)d.B * d.GT_out * 4);
@@ -348,7 +347,6 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.cw = d.cw;
   pa.pbits = (uint32_t*)(w + L.pbits);
   pa.nblk = prep_blocks(d);
-  pa.vflag = (int*)(w + L.vflag);
   const int64_t void_idx =
       (p->void_class_index >= 0 && p->void_class_index < d.C) ? p->void_class_index : -1;
   if (void_found) {

@@ -173,7 +173,7 @@ inline SavedLayout saved_layout(const Dims& d) {
 
 // Byte offsets inside the caller's workspace.
 struct Layout {
-  size_t lab16, counts, pbits, vflag, ncols, colmap, slot_of_col, sched, partials, rowsum,
+  size_t lab16, counts, pbits, ncols, colmap, slot_of_col, sched, partials, rowsum,
       sep, tot, rowIT, rowstat, img, mrows, layer, done, total;
 };
 // Workspace layout for the cost plan `pl` (its float_total / slot_total size
@@ -210,11 +210,10 @@ struct PrepArgs {
   uint32_t* pbits = nullptr;
   int nblk = 0;          // preparation workgroups per image (prep_blocks)
   // void-class check (reference functions/mask/matching.py:184-185): the
-  // first workgroup of image b writes vflag[b] = any(cls_targets[b][:] == void_idx);
-  // the column pass ORs them into *void_found (device or host-mapped memory)
+  // first workgroup of image 0 writes *void_found = any(cls_targets == void_idx)
+  // (device or host-mapped memory)
   const int64_t* cls_targets = nullptr;
-  int64_t void_idx = -1;  // -1: no check
-  int* vflag = nullptr;
+  int64_t void_idx = -1;  // -1: no valid void index (the check reports 0)
   int32_t* void_found = nullptr;
   int* ncols;
   int* colmap;

@@ -73,15 +73,30 @@ __device__ __forceinline__ void pres_store(const PrepArgs& a, const uint32_t* pr
     a.pbits[(b * a.nblk + blockIdx.x) * kPresWords + threadIdx.x] = pres[threadIdx.x];
 }
 
-// The void check of image b's class targets (first preparation workgroup of
-// the image; every flag rewritten on each call).
+// The void-class check of every image's class targets, made by the first
+// preparation workgroup of image 0 so that the word is written within the
+// forward's first kernel (a host may be polling it): *void_found =
+// any(cls_targets == void_idx), 0 without a valid void index, stored with
+// system scope (the word may be pinned host memory).  Ends with a barrier.
 __device__ __forceinline__ void void_check(const PrepArgs& a, int64_t b) {
-  if (a.void_idx < 0 || blockIdx.x != 0) return;
+  if (!a.void_found || blockIdx.x != 0 || b != 0) return;  // uniform over the workgroup
   int hit = 0;
-  for (int64_t i = threadIdx.x; i < a.GT_total; i += blockDim.x)
-    hit |= a.cls_targets[b * a.GT_total + i] == a.void_idx;
+  if (a.void_idx >= 0) {
+    const int64_t n = a.B * a.GT_total;
+    for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * (int64_t)blockDim.x) {
+      int64_t v[8];  // eight loads in flight per thread, then the compares
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int64_t i = i0 + k * (int64_t)blockDim.x;
+        v[k] = i < n ? a.cls_targets[i] : -1;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) hit |= v[k] == a.void_idx;
+    }
+  }
   hit = __syncthreads_or(hit);
-  if (threadIdx.x == 0) a.vflag[b] = hit ? 1 : 0;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.void_found, hit ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 constexpr int kColsLds = 1024;
@@ -97,14 +112,6 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const uint64_t below = (1ull << lane) - 1ull;
-  if (a.void_found && wave == nw - 1) {  // no valid void index: 0
-    int hit = 0;
-    if (a.void_idx >= 0)
-      for (int64_t b = lane; b < a.B; b += 64) hit |= a.vflag[b];
-    hit = __any(hit);
-    // system scope: the word may be pinned host memory that the host polls
-    if (lane == 0) __hip_atomic_store(a.void_found, hit ? 1 : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
   for (int64_t b = wave; b < a.B; b += nw) {
     // presence word j = OR over the image's preparation workgroups: lane
     // (k0, j) with j = lane & 7 ORs workgroups k0, k0 + 8, ..., then the

@@ -1,7 +1,7 @@
 """MaskMatchingFunction -- reference functions/mask/matching.py:21-334.
 
 Same positional signature, defaults and validation as the reference.  The
-differences are on the device side only:
+differences:
 
 * mask logits are consumed in their own dtype (float32, bfloat16 or float16):
   no float32 copy of the logits is made (reference: ``.contiguous().float()``,
@@ -13,12 +13,14 @@ differences are on the device side only:
   backward: mask_matching_backward.cu:110-215) and skips target preparation;
 * when the mask logits need a gradient (and unmatched masks are not forced to
   empty, so unmatched rows have zero gradient), the forward allocates the
-  gradient tensor and zero-fills it on a side stream while the assignment
-  runs; the first backward then writes only the matched rows into it.
+  gradient tensor and zero-fills it with extra workgroups of its own launches
+  while the assignment runs; the first backward then writes only the matched
+  rows into it;
+* the autograd node is a C++ one (the extension's MatchingNode): the Python
+  class applies the reference's defaults and validation only.
 """
 from __future__ import annotations
 
-import torch
 from torch.autograd import Function
 
 import mask_loss_amd  # noqa: F401  (registers the `mask_loss` module)
@@ -28,9 +30,19 @@ from .._args import STRATEGIES, focal, label_kind, uncertainty
 
 
 class MaskMatchingFunction(Function):
+    """The reference's autograd Function (functions/mask/matching.py:33-334).
+
+    ``apply`` takes the reference's positional arguments, applies its defaults
+    and validation, and runs the step as a C++ autograd node of the extension
+    (``mask_loss.mask_matching_autograd``): the forward launches the fused cost
+    -> assignment -> loss kernels (and, when the mask logits need a gradient,
+    the gradient buffer's zero fill); the node's backward writes the matched
+    rows into that buffer and the class-logit gradient.  Returns
+    (pred_to_gt, pred_round, layer mask mean, layer dice mean, layer class mean).
+    """
+
     @staticmethod
-    def forward(
-        ctx,
+    def apply(
         mask_logits,  # (L,B,Q,H,W)
         mask_targets,  # (B,H_t,W_t)
         cls_logits,  # (L,B,Q,C)
@@ -59,10 +71,6 @@ class MaskMatchingFunction(Function):
         L, B, Q, h, w = mask_logits.shape
         B_t, H_t, W_t = mask_targets.shape
         assert B == B_t, "Batch size mismatch between logits and targets"
-        mask_logits = mask_logits.contiguous()
-        mask_targets = mask_targets.contiguous()
-        cls_logits = cls_logits.contiguous()
-        cls_targets = cls_targets.contiguous()
 
         smooth_val = float(smooth if smooth is not None else 1.0)
         sigmoid_scale_val = float(sigmoid_scale if sigmoid_scale is not None else 1.0)
@@ -96,47 +104,12 @@ class MaskMatchingFunction(Function):
         if use_softmax and force_cls and void == -1:
             raise ValueError("void_class_index must be provided when using softmax label loss "
                              "and forcing unmatched predictions to background")
-
-        args = (smooth_val, sigmoid_scale_val, dice_scale_val, cls_scale_val, bg, ug, ugm)
-        prefill = None
-        if ctx.needs_input_grad[0] and not force_masks:
-            prefill = torch.empty_like(mask_logits, memory_format=torch.contiguous_format)
         # The void-class check (reference: a synchronous torch.any before any
         # work) runs in the forward's first kernels; the call returns once
-        # they are done, with the rest of the forward still queued, so the
-        # host never drains the GPU before launching it.
-        check = void != -1
-        outs = mask_loss.mask_matching_fused(
-            mask_logits, mask_targets, cls_logits, cls_targets, *args, inf_thresh_val,
-            num_masks_val, force_cls, force_masks, K_val, STRATEGIES[strategy], mg, ma, cg, ca,
-            void, use_softmax, normalize, prefill, check)
-        pred_to_gt, pred_round, m, d, c, saved = outs[:6]
-        ctx.save_for_backward(mask_logits.detach(), mask_targets.detach(), cls_logits.detach(),
-                              cls_targets.detach(), pred_to_gt.detach(), saved)
-        # the zero-filled gradient buffer serves the first backward only (a
-        # second backward through a retained graph gets a fresh tensor)
-        ctx.prefill = prefill
-        ctx.bwd_args = (smooth_val, sigmoid_scale_val, dice_scale_val, cls_scale_val, bg, ug, ugm,
-                        num_masks_val, force_cls, force_masks, mg, ma, cg, ca, void, use_softmax,
-                        normalize)
-        if check and int(outs[6][0]) == 1:
-            raise ValueError("cls_targets must not contain the void class index")
-        ctx.mark_non_differentiable(pred_to_gt, pred_round)
-        # no zero gradients for the integer outputs (or unused means)
-        ctx.set_materialize_grads(False)
-        return pred_to_gt, pred_round, m, d, c
-
-    @staticmethod
-    def backward(ctx, _, __, grad_layer_mask_mean, grad_layer_dice_mean, grad_layer_cls_mean):
-        mask_logits, mask_targets, cls_logits, cls_targets, pred_to_gt, saved = ctx.saved_tensors
-        prefill, ctx.prefill = ctx.prefill, None
-
-        def g(x):
-            return x.detach().float().contiguous() if x is not None else \
-                torch.zeros(mask_logits.shape[0], device=mask_logits.device)
-
-        grad_mask, grad_cls = mask_loss.mask_matching_backward_fused(
-            g(grad_layer_mask_mean), g(grad_layer_dice_mean), g(grad_layer_cls_mean),
-            mask_logits, mask_targets, cls_logits, cls_targets, pred_to_gt, *ctx.bwd_args, saved,
-            prefill)
-        return (grad_mask, None, grad_cls) + (None,) * 21
+        # they are done, with the rest of the forward still queued, and raises
+        # ValueError("cls_targets must not contain the void class index").
+        return tuple(mask_loss.mask_matching_autograd(
+            mask_logits, mask_targets, cls_logits, cls_targets, smooth_val, sigmoid_scale_val,
+            dice_scale_val, cls_scale_val, bg, ug, ugm, inf_thresh_val, num_masks_val, force_cls,
+            force_masks, K_val, STRATEGIES[strategy], mg, ma, cg, ca, void, use_softmax, normalize,
+            void != -1))

@@ -73,13 +73,13 @@ __device__ __forceinline__ void pres_store(const PrepArgs& a, const uint32_t* pr
     a.pbits[(b * a.nblk + blockIdx.x) * kPresWords + threadIdx.x] = pres[threadIdx.x];
 }
 
-// The void-class check of every image's class targets, made by the first
-// preparation workgroup of image 0 so that the word is written within the
-// forward's first kernel (a host may be polling it): *void_found =
-// any(cls_targets == void_idx), 0 without a valid void index, stored with
-// system scope (the word may be pinned host memory).  Ends with a barrier.
-__device__ __forceinline__ void void_check(const PrepArgs& a, int64_t b) {
-  if (!a.void_found || blockIdx.x != 0 || b != 0) return;  // uniform over the workgroup
+// The void-class check of every image's class targets, made by a workgroup
+// of its own (the preparation grid's extra column, blockIdx.x == nblk, image
+// row 0) so that the word is written early in the forward's first kernel
+// without delaying a preparation workgroup (a host may be polling it):
+// *void_found = any(cls_targets == void_idx), 0 without a valid void index,
+// stored with system scope (the word may be pinned host memory).
+__device__ __forceinline__ void void_check(const PrepArgs& a) {
   int hit = 0;
   if (a.void_idx >= 0) {
     const int64_t n = a.B * a.GT_total;
@@ -203,10 +203,12 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
 __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
   __shared__ uint32_t pres[kPresWords];
   const int64_t b = blockIdx.y;
+  if (a.void_found && blockIdx.x == (unsigned)a.nblk) {  // the void check's own column
+    if (b == 0) void_check(a);
+    return;
+  }
   const int64_t HW = a.H * a.W;
   const bool mark = a.pbits != nullptr;
-  // the labels are loaded first, so that their latency and the void check's
-  // (first workgroup of each image) overlap
   const int64_t cell0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   int64_t lab[8];
   if (cell0 < a.HWp) {
@@ -225,7 +227,6 @@ __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
   }
   if (mark) {
     pres_clear(pres);
-    void_check(a, b);  // ends with a barrier
     __syncthreads();
   }
   if (cell0 < a.HWp) {
@@ -257,11 +258,14 @@ __global__ __launch_bounds__(256) void prep_labels_kernel(PrepArgs a) {
 __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
   __shared__ uint32_t pres[kPresWords];
   const int64_t b = blockIdx.y;
+  if (a.void_found && blockIdx.x == (unsigned)a.nblk) {  // the void check's own column
+    if (b == 0) void_check(a);
+    return;
+  }
   const int64_t HW = a.H * a.W;
   const bool mark = a.pbits != nullptr;
   if (mark) {
     pres_clear(pres);
-    void_check(a, b);  // ends with a barrier
     __syncthreads();
   }
   const int64_t cell = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -314,7 +318,8 @@ int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st) {
   if (a.pbits && (a.GT_total > kPresLabels || a.nblk != prep_blocks(d)))
     return fail(ML_EINVAL, "internal: presence records do not fit the preparation grid");
   if (a.sched && a.plan.ntasks >= ((int64_t)1 << 31)) return fail(ML_EINVAL, "too many row tiles");
-  const dim3 grid((unsigned)prep_blocks(d), (unsigned)d.B);
+  // one more workgroup column for the void check
+  const dim3 grid((unsigned)prep_blocks(d) + (a.void_found ? 1u : 0u), (unsigned)d.B);
   if (!d.counts_mode) {
     hipLaunchKernelGGL(prep_labels_kernel, grid, dim3(256), 0, st, a);
   } else {
@@ -354,7 +359,8 @@ int launch_prep_points(const PrepArgs& a, const Dims& d, int64_t Hs, int64_t Ws,
   m.H = Hs;
   m.W = Ws;
   m.HWp = ceil_div(Hs * Ws, kStep) * kStep;
-  hipLaunchKernelGGL(prep_labels_kernel, dim3((unsigned)a.nblk, (unsigned)d.B), dim3(256), 0, st, m);
+  hipLaunchKernelGGL(prep_labels_kernel, dim3((unsigned)a.nblk + (a.void_found ? 1u : 0u), (unsigned)d.B),
+                     dim3(256), 0, st, m);
   int rc = check_launch("prep");
   if (rc) return rc;
   rc = launch_point_labels(a.targets, coords, d.B, Hs, Ws, d.HW, a.GT_total, nullptr, a.lab16, d.HWp, st);

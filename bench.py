@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of 512 MiB (3 launches), the reference "
                          "point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="run only the read-only HBM stream over the headline logits' size "
+                         "(ml_profile_stream_read) and print its GB/s")
     return ap.parse_args()
 
 
@@ -60,6 +63,45 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 3}), flush=True)
+
+
+READ_BYTES = 16 * 200 * 256 * 256 * 2  # the headline's bf16 logits, read once by the contraction
+
+
+def read_ceiling(reps=20):
+    """Practical HBM read ceiling: ml_profile_stream_read (16-byte loads, one
+    contiguous chunk per workgroup, eight loads in flight per thread) over
+    READ_BYTES, timed with HIP events on the launch stream; per grid size the
+    best and median of `reps` launches."""
+    import torch
+    lib = prof_lib()
+    src = torch.ones(READ_BYTES // 2, dtype=torch.bfloat16, device="cuda:0")
+    out = torch.empty(8192, dtype=torch.int32, device="cuda:0")
+    st = torch.cuda.current_stream()
+    res = {}
+    for grid in (1024, 2048, 4096):
+        for _ in range(3):
+            lib.ml_profile_stream_read(ctypes.c_void_p(src.data_ptr()), READ_BYTES,
+                                       ctypes.c_void_p(out.data_ptr()), grid, ctypes.c_void_p(st.cuda_stream))
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            rc = lib.ml_profile_stream_read(ctypes.c_void_p(src.data_ptr()), READ_BYTES,
+                                            ctypes.c_void_p(out.data_ptr()), grid,
+                                            ctypes.c_void_p(st.cuda_stream))
+            e1.record(st)
+            if rc != 0:
+                raise RuntimeError("ml_profile_stream_read failed")
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        ts.sort()
+        res[grid] = {"best_us": round(ts[0], 2), "median_us": round(ts[len(ts) // 2], 2),
+                     "best_GBs": round(READ_BYTES / (ts[0] * 1e-6) / 1e9, 1),
+                     "median_GBs": round(READ_BYTES / (ts[len(ts) // 2] * 1e-6) / 1e9, 1)}
+    best = max(res.values(), key=lambda r: r["median_GBs"])
+    return {"bytes": READ_BYTES, "grids": res, "median_GBs": best["median_GBs"],
+            "best_GBs": best["best_GBs"]}
 
 
 def load_traffic(workload, kernel):
@@ -81,6 +123,8 @@ def prof_lib():
     lib.ml_profile_enable.argtypes = [ctypes.c_int]
     lib.ml_profile_read.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64),
                                     ctypes.POINTER(ctypes.c_double)]
+    lib.ml_profile_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                           ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -361,6 +405,9 @@ def main():
     if a.copy_calibration:
         copy_calibration()
         return
+    if a.read_ceiling:
+        print(json.dumps(read_ceiling()), flush=True)
+        return
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
                                    "(the step shards over images across GPUs, which is not "
@@ -427,6 +474,12 @@ def main():
         "algorithmic_bytes": dom_bytes,
         "avg_launch_us": kernels[dom]["avg_us"],
     }
+    # the practical read ceiling of this box (a read-only 16-byte-load stream
+    # over the headline logits' size), beside the published peak
+    rc_ = read_ceiling(reps=10)
+    roofline["practical_read_ceiling_GBs"] = rc_["median_GBs"]
+    if achieved:
+        roofline["frac_of_practical_read_ceiling"] = round(achieved / rc_["median_GBs"], 4)
     step_roof = {
         "algorithmic_bytes": step_bytes,
         "hbm_floor_us": round(step_bytes / HBM_PEAK_GBS / 1e3, 1),

@@ -316,6 +316,15 @@ int ml_profile_enable(int enable);
 int ml_profile_read(const char* name, int64_t* launches, double* total_ms);
 int ml_profile_reset(void);
 
+/* Measurement aid (no counterpart in the reference): a read-only HBM stream
+ * over `bytes` bytes at `p` (16-byte aligned, bytes a multiple of 16) by
+ * `grid` workgroups of 256 threads, each reading one contiguous chunk with
+ * 16-byte loads (eight in flight per thread) and writing one word to
+ * out[blockIdx] -- the practical read ceiling that the cost contraction,
+ * which streams every logit once, is measured against. */
+int ml_profile_stream_read(const void* p, size_t bytes, uint32_t* out, int grid,
+                           ml_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -559,6 +559,12 @@ int ml_profile_read(const char* name, int64_t* launches, double* total_ms) {
 }
 int ml_version(void) { return 1; }
 
+int ml_profile_stream_read(const void* p, size_t bytes, uint32_t* out, int grid, ml_stream_t stream) {
+  if (!p || !out || bytes == 0 || bytes % 16 || ((uintptr_t)p & 15) || grid < 1 || grid > 65536)
+    return fail(ML_EINVAL, "stream_read: bad arguments");
+  return launch_stream_read(p, (int64_t)(bytes / 16), out, grid, (hipStream_t)stream);
+}
+
 int ml_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, ml_stream_t stream) {
   if (n < 0 || (n > 0 && !x) || !flag) return fail(ML_EINVAL, "any_equal: bad arguments");
   return launch_any_equal(x, n, value, flag, (hipStream_t)stream);

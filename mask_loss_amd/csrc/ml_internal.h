@@ -440,6 +440,7 @@ __device__ inline void fill_slice(const FillSlice& f, int64_t blk) {
   zero_fill_range(f.p, f.n16, nullptr, 0, blk, f.blocks);
 }
 int launch_any_equal(const int64_t* x, int64_t n, int64_t value, int32_t* flag, hipStream_t st);
+int launch_stream_read(const void* p, int64_t n16, uint32_t* out, int grid, hipStream_t st);
 
 // Counts of one label at 8 consecutive cells starting at element `idx` of the
 // count tensor: u8 (cw == 1) or u16 (cw == 2).  idx is a multiple of 8, so the

@@ -44,6 +44,38 @@ int launch_zero_fill(void* p, size_t bytes, hipStream_t st) {
   return check_launch("zero_fill");
 }
 
+// Read-only stream: workgroup g reads its contiguous chunk of the n16 16-byte
+// words, eight loads in flight per thread, and writes one word (so that no
+// load is dead code).
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4_t* p, int64_t n16, uint32_t* out) {
+  const int64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const int64_t b0 = min(n16, (int64_t)blockIdx.x * per), b1 = min(n16, b0 + per);
+  uint32_t acc = 0;
+  int64_t i = b0 + threadIdx.x;
+  for (; i + 7 * 256 < b1; i += 8 * 256) {
+    u32x4_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[i + u * 256];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+  }
+  for (; i < b1; i += 256) {
+    const u32x4_t v = p[i];
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  __shared__ uint32_t s;
+  if (threadIdx.x == 0) s = 0u;
+  __syncthreads();
+  atomicXor(&s, acc);
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
+int launch_stream_read(const void* p, int64_t n16, uint32_t* out, int grid, hipStream_t st) {
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const u32x4_t*)p, n16, out);
+  return check_launch("stream_read");
+}
+
 // flag[0] = any(x[i] == value), one workgroup.
 __global__ __launch_bounds__(256) void any_equal_kernel(const int64_t* x, int64_t n, int64_t value,
                                                         int32_t* flag) {

@@ -720,16 +720,35 @@ __device__ __forceinline__ uint4 ring_read(uint32_t addr) {
   return v;
 }
 
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2_t as_u16x2(uint32_t v) { return __builtin_bit_cast(u16x2_t, v); }
+__device__ __forceinline__ uint32_t as_u32(u16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Table byte offsets (sign block included) of the two bf16 logits packed in
+// u, as lut_lookup8 computes them, in compiler-visible packed 16-bit ops (no
+// inline assembly, so no hazard padding after each one): the clamped index
+// times 8 stays below 2^15, so the sign bit ORs in without carry.
+__device__ __forceinline__ uint32_t lut_addr_pair(uint32_t u) {
+  const u16x2_t m = as_u16x2(u & 0x7FFF7FFFu);
+  const u16x2_t idx = __builtin_elementwise_min(
+      __builtin_elementwise_sub_sat(m, (u16x2_t){(unsigned short)kLutSub, (unsigned short)kLutSub}),
+      (u16x2_t){(unsigned short)(kLutN + 1), (unsigned short)(kLutN + 1)});
+  uint32_t addr = (u & 0x80008000u) | as_u32(idx << (u16x2_t){3, 3});
+  // kept whole, so its two halves are one mask and one shift of it
+  asm("" : "+v"(addr));
+  return addr;
+}
+
 // Table entries of 8 bf16 cells (as lut_lookup8) read with assembly, and the
 // wait for them tied to their registers.  lut_base: the table's LDS address.
 __device__ __forceinline__ void lut_lookup8_asm(const uint4& x, uint32_t lut_base, uint64_t E[8]) {
   const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+  uint32_t ad[4];  // the four words' chains side by side, then the reads
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ad[i] = lut_addr_pair(u[i]);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t m = u[i] & 0x7FFF7FFFu;
-    const uint32_t idx =
-        pk_min_u16(pk_sub_sat_u16(m, kLutSub * 0x10001u), (kLutN + 1) * 0x10001u);
-    const uint32_t addr = bfi32(0x80008000u, u[i], pk_lshl3_u16(idx));
+    const uint32_t addr = ad[i];
     asm volatile("ds_read_b64 %0, %1" : "=v"(E[2 * i]) : "v"(lut_base + (addr & 0xFFFFu)) : "memory");
     asm volatile("ds_read_b64 %0, %1" : "=v"(E[2 * i + 1]) : "v"(lut_base + (addr >> 16)) : "memory");
   }

@@ -209,9 +209,9 @@ struct PrepArgs {
   // rewritten on each call, so nothing needs clearing first
   uint32_t* pbits = nullptr;
   int nblk = 0;          // preparation workgroups per image (prep_blocks)
-  // void-class check (reference functions/mask/matching.py:184-185): the
-  // first workgroup of image 0 writes *void_found = any(cls_targets == void_idx)
-  // (device or host-mapped memory)
+  // void-class check (reference functions/mask/matching.py:184-185): an extra
+  // workgroup of the preparation launch (blockIdx.x == nblk, image 0) writes
+  // *void_found = any(cls_targets == void_idx) (device or host-mapped memory)
   const int64_t* cls_targets = nullptr;
   int64_t void_idx = -1;  // -1: no valid void index (the check reports 0)
   int32_t* void_found = nullptr;

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC > 8 ? 3 
   const uint32_t rtile = (uint32_t)q / (uint32_t)a.rows;
   const int qin = (int)((uint32_t)q - rtile * (uint32_t)a.rows);
   const int64_t task = lb * a.rtiles + rtile;
-  const int64_t tidx = a.sched[2 * kClasses + kClasses * a.plan.ntasks + task];
+  const int64_t tidx = a.sched[kSchedList + kClasses * a.plan.ntasks + task];
   int ksc[kClasses], nc[kClasses];
 #pragma unroll
   for (int c = 0; c < kClasses; ++c) {

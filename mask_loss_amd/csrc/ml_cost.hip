@@ -284,6 +284,16 @@ __device__ __forceinline__ void pace(int* prog, int k) {
   else __builtin_amdgcn_s_setprio(1);
 }
 
+// In-workgroup sum of R consecutive K-splits of one task (R a power of two):
+// this wave is split r of its group grp of R waves.  buf: the workgroup's LDS
+// exchange area for its writers, 3*RT*NT float4 per lane each; rsbuf: their
+// row sums.  buf == null: no reduction.
+struct SplitRed {
+  f32x4_t* buf = nullptr;
+  float2* rsbuf = nullptr;
+  int R = 1, r = 0, grp = 0;
+};
+
 // One wave's work: 16*RT query rows of task (lb, rtile) over the K-steps of
 // split ks of KS; writes the partial sums to `out` ([3][16*RT][16*NT]) and,
 // for unweighted penalties, the row sums to `rs` ([16*RT][2]).  TAB:
@@ -292,10 +302,14 @@ __device__ __forceinline__ void pace(int* prog, int k) {
 // redoes the range with the formulas before writing.  `setup` (the
 // workgroup's table build and barrier) is called exactly once on every path,
 // after the first D K-steps of loads are issued, so their latency overlaps it.
+// With red.buf, the R waves of the group add their sums in a fixed tree order
+// (wave r takes wave r + h for h = R/2, ..., 1; 2 log2(R) barriers for every
+// wave of the workgroup) and only wave 0 of the group writes.
 template <int DT, int RT, int NT, int CNT, bool TAB, class Setup>
 __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
                                           int64_t ks, int64_t KS, const unsigned char* lut,
-                                          float* out, float* rs_out, int* prog, Setup&& setup) {
+                                          float* out, float* rs_out, int* prog, Setup&& setup,
+                                          const SplitRed& red = SplitRed()) {
   constexpr int NS = InTraits<DT>::kSplit;
   constexpr int D = TAB ? kDepth : 2;  // K-steps of logits and labels in flight
   const int lane = threadIdx.x & 63;
@@ -595,6 +609,48 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
     mma_step(A, lv, cell0);
   }
 
+  if (red.buf) {
+    constexpr int TW = 3 * RT * NT;  // float4 per lane per writer
+    for (int h = red.R >> 1; h >= 1; h >>= 1) {
+      const int64_t slot = red.grp * (red.R >> 1) + (red.r & (h - 1));
+      if (red.r >= h && red.r < 2 * h) {
+        f32x4_t* d = red.buf + slot * TW * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              if (nt < nt_used) d[((i * RT + rt) * NT + nt) * 64] = acc[i][rt][nt];
+        if (unw) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) red.rsbuf[(slot * RT + rt) * 64 + lane] = make_float2(ub[rt], up[rt]);
+        }
+      }
+      __syncthreads();
+      if (red.r < h) {
+        const f32x4_t* d = red.buf + slot * TW * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              if (nt < nt_used) acc[i][rt][nt] += d[((i * RT + rt) * NT + nt) * 64];
+        if (unw) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            const float2 v = red.rsbuf[(slot * RT + rt) * 64 + lane];
+            ub[rt] += v.x;
+            up[rt] += v.y;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (red.r != 0) return;
+  }
+
   // ---- write this wave's partial sums (only the tiles in use)
   constexpr int rows = 16 * RT, nslot = 16 * NT;
 #pragma unroll
@@ -631,36 +687,72 @@ template <int NT>
 constexpr int kClassOf = NT == 2 ? 0 : NT == 7 ? 1 : 2;
 
 // One launch per column-tile class: wave w of the grid takes work item w of
-// the class (item = task index * KS + split), with the class's tasks, count
+// the class (item = split * n + task index), with the class's tasks, count
 // and K-split read from the device schedule.  The grid has
-// max(slots, tasks) waves, so every item has a wave.
+// max(slots, tasks) waves, so every item has a wave.  Where the schedule sets
+// R > 1 (classes 1 and 2), items are groups of R waves instead: item u of the
+// grid's groups is task u % n at partial u / n, its R waves take R
+// consecutive splits of the R * KS-way split and add their sums in LDS
+// (n * KS * R <= slots, so the groups fit the grid).
 template <int DT, int RT, int NT, int CNT, bool TAB>
 __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs a) {
   constexpr int CI = kClassOf<NT>;
   constexpr int WV = cost_waves(NT, TAB);
+  constexpr bool kRed = CI > 0;  // classes whose splits the schedule may group
   __shared__ __align__(16) unsigned char lut_s[TAB ? kLutBytes : 16];
   __shared__ int prog_s[WV];
+  __shared__ f32x4_t red_s[kRed ? (WV / 2) * 3 * RT * NT * 64 : 1];
+  __shared__ float2 red_rs[kRed ? (WV / 2) * RT * 64 : 1];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n = __builtin_amdgcn_readfirstlane(a.sched[CI]);
   const int64_t KS = __builtin_amdgcn_readfirstlane(a.sched[kClasses + CI]);
+  const int R = kRed ? __builtin_amdgcn_readfirstlane(a.sched[kSchedRed + CI]) : 1;
   const int64_t total = n * KS;
-  const int64_t w0 = (int64_t)blockIdx.x * WV;
-  if (w0 >= total) return;  // the whole workgroup is idle
-  if (threadIdx.x < WV) prog_s[threadIdx.x] = 0;
   // table build + barrier: once per wave, after its first loads are in flight
   auto setup = [&]() {
     if constexpr (TAB) build_lut(lut_s, a.ep);
     __syncthreads();
   };
+  constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
+  if (kRed && R > 1) {
+    const int gpw = WV / R;  // groups per workgroup
+    const int grp = wave / R, r = wave - grp * R;
+    const int64_t u0 = (int64_t)blockIdx.x * gpw;
+    if (u0 >= total) return;  // the whole workgroup is idle
+    const int64_t u = u0 + grp;
+    if (u >= total) {  // an idle group still meets every barrier of the others
+      setup();
+      for (int h = R >> 1; h >= 1; h >>= 1) {
+        __syncthreads();
+        __syncthreads();
+      }
+      return;
+    }
+    const int64_t i = u % n, kp = u / n;
+    const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[kSchedList + CI * a.plan.ntasks + i]);
+    const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
+    float* out = a.partials + a.plan.float_base[CI] + u * tile;
+    float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + u) * (16 * RT) * 2 : nullptr;
+    SplitRed red;
+    red.buf = red_s;
+    red.rsbuf = red_rs;
+    red.R = R;
+    red.r = r;
+    red.grp = grp;
+    cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, kp * R + r, KS * R, lut_s, out, rs, nullptr, setup, red);
+    return;
+  }
+  const int64_t w0 = (int64_t)blockIdx.x * WV;
+  if (w0 >= total) return;  // the whole workgroup is idle
+  if (threadIdx.x < WV) prog_s[threadIdx.x] = 0;
   const int64_t w = w0 + wave;
   if (w >= total) {
     setup();
     return;
   }
   const int64_t i = w % n, ks = w / n;
-  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
+  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[kSchedList + CI * a.plan.ntasks + i]);
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
-  constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
   float* out = a.partials + a.plan.float_base[CI] + w * tile;
   float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + w) * (16 * RT) * 2 : nullptr;
   // pace the waves only where many share the workgroup's CU
@@ -1013,7 +1105,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void cost_dma_kernel(CostArgs a) {
     return;
   }
   const int64_t i = w % n, ks = w / n;
-  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + CI * a.plan.ntasks + i]);
+  const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[kSchedList + CI * a.plan.ntasks + i]);
   const int64_t lb = task / a.rtiles, rtile = task % a.rtiles;
   constexpr int64_t tile = 3 * 16 * 16 * NT;
   float* out = a.partials + a.plan.float_base[CI] + w * tile;
@@ -1256,7 +1348,7 @@ __global__ __launch_bounds__(64 * kDmaWaves) void cost_pair_kernel(CostArgs a) {
     // pair p = row tiles 2 (p % prt) (+ 1) of the class's (p / prt)-th image
     const int64_t j = p / prt;
     rp = p - j * prt;
-    const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[2 * kClasses + j * rt + 2 * rp]);
+    const int64_t task = __builtin_amdgcn_readfirstlane(a.sched[kSchedList + j * rt + 2 * rp]);
     lb = task / rt;
     const uint32_t ring = (uint32_t)(size_t)(lds_void_t*)lds + ring_base(wave);
     cost_wave_pair(a, lb, 32 * rp, 4 * ksq + kq, 4 * KSq, lds, ring, acc, setup);

@@ -66,8 +66,11 @@ constexpr int64_t kCostSlots = 4096;
 // kCostSlots); on the device the schedule picks the class's K-split KS_c =
 // clamp(slots / n_c, 1, ks_max) for its n_c (image, row-tile) tasks, and wave
 // w of the class takes task w / KS_c, split w % KS_c (grid-stride beyond).
-// Work item w of class c owns partial tile float_base[c] + w * tile(c) and
-// global slot slot_base[c] + w (unweighted row sums).
+// Classes 1 and 2 may instead split each task R_c times finer and add R_c
+// consecutive splits in the workgroup (see the cost kernel), so that KS_c
+// partials per task remain.  Work item w of class c (task i, partial k:
+// w = k * n_c + i) owns partial tile float_base[c] + w * tile(c) and global
+// slot slot_base[c] + w (unweighted row sums).
 struct CostPlan {
   int nclass;                    // classes with class_nt(c) <= padded NT
   int slots[kClasses];
@@ -84,10 +87,14 @@ struct CostPlan {
   // tiles ([3][2 rows][nslot]).  No row-sum records on this path.
   int pair0;
 };
-// Device schedule (ints in the workspace): n[kClasses], ks[kClasses],
-// list[kClasses][ntasks] (task ids per class, ascending), idx[ntasks]
-// (position of each task in its class list).
-__host__ __device__ inline int64_t sched_ints(int64_t ntasks) { return 2 * kClasses + (kClasses + 1) * ntasks; }
+// Device schedule (ints in the workspace): n[kClasses], ks[kClasses] (the
+// K-split partials of each task that reach the partial sums), red[kClasses]
+// (waves per partial: each partial is the sum of red consecutive K-splits,
+// added in the workgroup; 1 for class 0), list[kClasses][ntasks] (task ids per
+// class, ascending), idx[ntasks] (position of each task in its class list).
+constexpr int kSchedRed = 2 * kClasses;
+constexpr int kSchedList = 3 * kClasses;
+__host__ __device__ inline int64_t sched_ints(int64_t ntasks) { return kSchedList + (kClasses + 1) * ntasks; }
 
 // Work item w of column-tile class c (n_c tasks, KS_c splits) is task
 // i = w % n_c at K-split ks = w / n_c: consecutive waves take consecutive row

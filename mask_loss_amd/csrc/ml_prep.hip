@@ -186,7 +186,7 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
   __syncthreads();
   if (wave != 0) return;
   const int64_t nt = a.plan.ntasks;
-  int* list = a.sched + 2 * kClasses;
+  int* list = a.sched + kSchedList;
   int* idx = list + kClasses * nt;
   int cnt[kClasses] = {};
   for (int64_t t0 = 0; t0 < nt; t0 += 64) {
@@ -226,8 +226,26 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
     int64_t ks = units > 0 ? slots / units : 1;
     ks = ks < 1 ? 1 : (ks > a.plan.ks_max ? a.plan.ks_max : ks);
     if (pairs) ks = ks >= 8 ? ks >> 2 : 1;
+    // classes 1 and 2: split each task R times finer than the partials that
+    // reach memory and add each R consecutive splits in the workgroup, with
+    // R the largest power of two up to the workgroup's wave count for which
+    // R * floor(ks / R) keeps at least 95% of the waves busy.  Fewer partials
+    // mean fewer partial bytes and a shorter sum in finalize (one image of
+    // 13 row tiles otherwise takes ~150 splits per task).
+    int red = 1;
+    if (lane > 0) {
+      for (int r = cost_waves(class_nt(lane), false); r >= 2; r >>= 1) {
+        const int64_t kp = ks / r;
+        if (kp >= 1 && kp * r * 20 >= ks * 19) {
+          red = r;
+          ks = kp;
+          break;
+        }
+      }
+    }
     a.sched[lane] = n;
     a.sched[kClasses + lane] = (int)ks;
+    a.sched[kSchedRed + lane] = red;
   }
 }
 

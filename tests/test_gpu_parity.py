@@ -183,6 +183,10 @@ MATCH_CASES = [
     dict(name="counts_s2_force", kw=dict(s=2, H=12, W=12), p=dict(mask_gamma=2.0, mask_alpha=0.25),
          m=dict(force_masks=True, force_cls=True)),
     dict(name="counts_s17_force", kw=dict(s=17, H=4, W=4), p={}, m=dict(force_masks=True, force_cls=True)),
+    # wider column classes with unweighted row sums: K-splits added in the
+    # cost workgroup (8 per partial at 41 columns, 4 at 121)
+    dict(name="wide7_force", kw=dict(G=40, Q=50, H=32, W=32), p={}, m=dict(force_masks=True, force_cls=True)),
+    dict(name="wide16_force", kw=dict(G=120, Q=40, H=32, W=32), p={}, m=dict(force_masks=True)),
     dict(name="empty_image", kw=dict(empty_image=True), p={}, m=dict(force_cls=True, void=8)),
     dict(name="q_tail_1024", kw=dict(Q=130, H=8, W=8, G=20), p={}, m={}),
     # cost matrices too large for LDS (300 x 250 floats): every row read in

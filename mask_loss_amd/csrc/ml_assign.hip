@@ -115,6 +115,7 @@ constexpr int kFinColsWide = 4;  // GT_out <= 256, class logits streamed (NC = 0
 constexpr int kFinClsBatch = 8;  // streamed class logits loaded per lane and batch
 constexpr int kFinClsWide = 20;  // C <= 1280 in registers with up to 64 kFinColsWide output columns
 constexpr int kFinSplits = 12;  // K-splits loaded per lane and batch
+constexpr int kFinSplits4 = 9;  // the same for four-plane partials (same registers)
 
 // Sum the K-split partials k0, k0 + step, ... of slot s in split order.  The
 // loads of a batch are unconditional (indices clamped to the last split) so
@@ -146,6 +147,51 @@ __device__ __forceinline__ void sum_splits(const RowPartials& rp, int s, int k0,
   v2 = a2;
 }
 
+// The same for four-plane partials (slot sums of A_neg, A_pos, A_p, A_w).
+__device__ __forceinline__ void sum_splits4(const RowPartials& rp, int s, float& v0, float& v1,
+                                            float& v2, float& v3) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int base = 0; base < rp.KS; base += kFinSplits4) {
+    float x0[kFinSplits4], x1[kFinSplits4], x2[kFinSplits4], x3[kFinSplits4];
+#pragma unroll
+    for (int u = 0; u < kFinSplits4; ++u) {
+      const int ks = min(base + u, rp.KS - 1);
+      const float* P = rp.p0 + (int64_t)ks * rp.ks_stride + s;
+      x0[u] = P[0];
+      x1[u] = P[rp.plane];
+      x2[u] = P[2 * rp.plane];
+      x3[u] = P[3 * rp.plane];
+    }
+#pragma unroll
+    for (int u = 0; u < kFinSplits4; ++u) {
+      if (base + u < rp.KS) {
+        a0 += x0[u];
+        a1 += x1[u];
+        a2 += x2[u];
+        a3 += x3[u];
+      }
+    }
+  }
+  v0 = a0;
+  v1 = a1;
+  v2 = a2;
+  v3 = a3;
+}
+
+// Exclusive prefix (UP) or suffix sum of v over the wave's lanes, in a fixed
+// order.
+template <bool UP>
+__device__ __forceinline__ float wave_excl_scan(float v, int lane) {
+  float x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float y = UP ? __shfl_up(x, d, 64) : __shfl_down(x, d, 64);
+    if (UP ? lane >= d : lane + d < 64) x += y;
+  }
+  const float e = UP ? __shfl_up(x, 1, 64) : __shfl_down(x, 1, 64);
+  return (UP ? lane >= 1 : lane + 1 < 64) ? e : 0.f;
+}
+
 // Latency-bound: at least four waves per SIMD (at most 128 registers).
 // CDT: dtype of the class logits.  FAST (chosen on the host): class logits
 // present and 1 <= GT_out <= 64 NG, so the output columns' slots and targets
@@ -158,7 +204,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC > 8 ? 3 
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's finish count
     if (a.done) *a.done = 0;
   }
-  __shared__ float sl[4][3][256 + 16];
+  __shared__ float sl[4][4][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // 32-bit index arithmetic: the host checks L * B * Q < 2^31
   const uint32_t nrows = (uint32_t)(a.L * a.B * a.Q), nrow_blocks = (nrows + 3u) / 4u;
@@ -241,13 +287,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC > 8 ? 3 
       sl[wave][1][s] = v1;
       sl[wave][2][s] = v2;
     }
-  } else {
+  } else if (a.plan.planes[ci] == 3) {
     for (int s = lane; s < nsl; s += 64) {
       float v0 = 0.f, v1 = 0.f, v2 = 0.f;
       sum_splits(rp, s, 0, 1, v0, v1, v2);
       sl[wave][0][s] = v0;
       sl[wave][1][s] = v1;
       sl[wave][2][s] = v2;
+    }
+  } else {
+    // slot sums N, Pos, I, T of slots 0..G (slot G: cells of no column)
+    for (int s = lane; s < nsl; s += 64) {
+      float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+      sum_splits4(rp, s, v0, v1, v2, v3);
+      sl[wave][0][s] = v0;
+      sl[wave][3][s] = v1;
+      sl[wave][1][s] = v2;
+      sl[wave][2][s] = v3;
+    }
+    wave_sync();
+    // bce numerator of slot g: the A_neg sums of every other slot (cells
+    // outside g) plus g's A_pos sum, from an exclusive prefix and suffix of
+    // the N sums (non-negative terms, no cancellation); P and S: the I and T
+    // sums over all slots.  Lane l takes slots 4l .. 4l + 3.
+    float nv[4], iv = 0.f, tv = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int s = 4 * lane + k;
+      const bool ok = s < nsl;
+      nv[k] = ok ? sl[wave][0][s] : 0.f;
+      iv += ok ? sl[wave][1][s] : 0.f;
+      tv += ok ? sl[wave][2][s] : 0.f;
+    }
+    float in[4], sf[4];  // within the lane: inclusive prefix and suffix
+    in[0] = nv[0];
+#pragma unroll
+    for (int k = 1; k < 4; ++k) in[k] = in[k - 1] + nv[k];
+    sf[3] = nv[3];
+#pragma unroll
+    for (int k = 2; k >= 0; --k) sf[k] = nv[k] + sf[k + 1];
+    const float pre = wave_excl_scan<true>(in[3], lane), suf = wave_excl_scan<false>(sf[0], lane);
+    const float Ptot = wave_sum(iv), Stot = wave_sum(tv);
+    wave_sync();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int s = 4 * lane + k;
+      if (s < G) {
+        const float before = k > 0 ? pre + in[k - 1] : pre;
+        const float after = k < 3 ? suf + sf[k + 1] : suf;
+        sl[wave][0][s] = (before + after) + sl[wave][3][s];
+      }
+    }
+    if (lane == 0) {
+      sl[wave][1][G] = Ptot;
+      sl[wave][2][G] = Stot;
     }
   }
 

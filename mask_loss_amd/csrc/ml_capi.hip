@@ -158,7 +158,8 @@ CostPlan bound_cost_plan(const Dims& d) {
     p.float_base[c] = f;
     // row-tile pairs: up to max(slots, pairs) items of two row tiles each
     const int64_t items = c == 0 && d.pair_ok ? 2 * cap : cap;
-    if (c < p.nclass) f += items * 3 * d.rows * 16 * class_nt(c);
+    p.planes[c] = c == 0 ? 3 : 4;  // the most any plan of this shape uses
+    if (c < p.nclass) f += items * p.planes[c] * d.rows * 16 * class_nt(c);
   }
   p.float_total = f;
   p.slot_total = (int64_t)p.nclass * cap;
@@ -172,7 +173,7 @@ void pack_cost_plan(CostPlan& p, const Dims& d) {
     p.slot_base[c] = sl;
     p.float_base[c] = f;
     sl += cap;
-    f += (c == 0 && p.pair0 ? 2 * cap : cap) * 3 * d.rows * 16 * class_nt(c);
+    f += (c == 0 && p.pair0 ? 2 * cap : cap) * p.planes[c] * d.rows * 16 * class_nt(c);
   }
   p.float_total = f;
   p.slot_total = sl;

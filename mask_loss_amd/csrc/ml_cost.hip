@@ -309,8 +309,15 @@ template <int DT, int RT, int NT, int CNT, bool TAB, class Setup>
 __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t rtile,
                                           int64_t ks, int64_t KS, const unsigned char* lut,
                                           float* out, float* rs_out, int* prog, Setup&& setup,
-                                          const SplitRed& red = SplitRed()) {
+                                          const SplitRed& red = SplitRed(), uint32_t* klut = nullptr) {
   constexpr int NS = InTraits<DT>::kSplit;
+  // slot-sum form (classes 1 and 2 on label maps without the table): four
+  // planes summed per slot over the cells whose key (the slot of their label's
+  // column, or G for cells of no column) is that slot, with one-hot operands
+  // only, so each K-step runs the MFMAs of just the column tiles its cells'
+  // keys fall in.  klut: this wave's LDS label -> (key | tile bit << 16) table.
+  constexpr bool SP = CNT == 0 && !TAB && NT >= 7;
+  constexpr int NP = SP ? 4 : 3;
   constexpr int D = TAB ? kDepth : 2;  // K-steps of logits and labels in flight
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, g4 = lane >> 4;
@@ -327,22 +334,38 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
   // B' = 0; padding: both 0.
   uint32_t colL[NT], coefB[NT], baseB[NT];
   const uint32_t n2pair = pack_bf16x2(a.N2, a.N2);
+  if constexpr (!SP) {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int slot = nt * 16 + r;
-    colL[nt] = 0;
-    coefB[nt] = slot < G ? 0x3F803F80u : 0u;
-    baseB[nt] = slot < G ? 0x3F803F80u : (slot == G ? n2pair : 0u);
-    if (slot < G) {
-      const int c = a.colmap[b * a.nslot + slot];
-      const int act = c + (c >= a.bg ? 1 : 0);
-      colL[nt] = (uint32_t)act * 0x10001u;
+    for (int nt = 0; nt < NT; ++nt) {
+      const int slot = nt * 16 + r;
+      colL[nt] = 0;
+      coefB[nt] = slot < G ? 0x3F803F80u : 0u;
+      baseB[nt] = slot < G ? 0x3F803F80u : (slot == G ? n2pair : 0u);
+      if (slot < G) {
+        const int c = a.colmap[b * a.nslot + slot];
+        const int act = c + (c >= a.bg ? 1 : 0);
+        colL[nt] = (uint32_t)act * 0x10001u;
+      }
     }
+  } else {
+    // labels (u16, 0xFFFF for none; min(label, 256) indexes the table) ->
+    // key: every entry G first, then each column's label its slot (one
+    // wave's LDS writes land in issue order; the wait keeps the two rounds
+    // apart all the same)
+    const uint32_t eG = (uint32_t)G | (1u << (16 + (G >> 4)));
+    for (int l = lane; l < 257; l += 64) klut[l] = eG;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int sl = lane; sl < G; sl += 64) {
+      const int c = a.colmap[b * a.nslot + sl];
+      const int act = c + (c >= a.bg ? 1 : 0);
+      if (act >= 0 && act < 256) klut[act] = (uint32_t)sl | (1u << (16 + (sl >> 4)));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
 
-  f32x4_t acc[3][RT][NT];
+  f32x4_t acc[NP][RT][NT];
 #pragma unroll
-  for (int i = 0; i < 3; ++i)
+  for (int i = 0; i < NP; ++i)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -432,6 +455,61 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
     }
   };
 
+  // slot-sum form: keys of the lane's 8 cells as u16 pairs, and the column
+  // tiles any of the K-step's 32 cells falls in (the four lane groups hold
+  // different cells; every lane ends with the same mask)
+  auto keys_of = [&](const uint4& lv, uint32_t (&kp)[4]) -> uint32_t {
+    const uint32_t L2[4] = {lv.x, lv.y, lv.z, lv.w};
+    uint32_t e[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e[2 * i] = klut[min(L2[i] & 0xFFFFu, 256u)];
+      e[2 * i + 1] = klut[min(L2[i] >> 16, 256u)];
+    }
+    uint32_t t = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kp[i] = __builtin_amdgcn_perm(e[2 * i + 1], e[2 * i], 0x0C040C00u);
+      t |= e[2 * i] | e[2 * i + 1];
+    }
+    t >>= 16;
+    return __builtin_amdgcn_readlane(t, 0) | __builtin_amdgcn_readlane(t, 16) |
+           __builtin_amdgcn_readlane(t, 32) | __builtin_amdgcn_readlane(t, 48);
+  };
+  auto mma_step_sp = [&](bf16x8_t (&A)[4][RT][NS], const uint32_t (&kp)[4], uint32_t tmask) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if (nt >= nt_used || !((tmask >> nt) & 1u)) continue;
+      const uint32_t s2 = (uint32_t)(nt * 16 + r) * 0x10001u;
+      u32x4_t bv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t m = pk_min_u16(kp[i] ^ s2, 0x00010001u);
+        bv[i] = pk_sub_u16(0x3F803F80u, pk_mul_lo_u16(m, 0x3F803F80u));
+      }
+      const bf16x8_t Bv = __builtin_bit_cast(bf16x8_t, bv);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) {
+#pragma unroll
+          for (int pl = 0; pl < 4; ++pl)
+            acc[pl][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[pl][rt][sp], Bv, acc[pl][rt][nt], 0, 0, 0);
+        }
+      }
+    }
+  };
+  // one K-step of either form
+  auto mma_any = [&](bf16x8_t (&A)[4][RT][NS], const uint4& lv, int64_t cell0) {
+    if constexpr (SP) {
+      uint32_t kp[4];
+      const uint32_t tm = keys_of(lv, kp);
+      mma_step_sp(A, kp, tm);
+    } else {
+      mma_step(A, lv, cell0);
+    }
+  };
+
   // Software pipeline over this wave's nst steps: D steps of logits and
   // labels in flight.  Slot j holds step k + j; it is turned into A operands
   // first and then refilled with step k + j + D (clamped to the last step, so
@@ -515,13 +593,17 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
         if (prog && (k & (2 * D - 1)) == 0) pace(prog, k);
 #pragma unroll
         for (int j = 0; j < D; ++j) {
+          // slot-sum form: the key table reads go out before the plane work
+          uint32_t kp[4] = {0u, 0u, 0u, 0u}, tm = 0;
+          if constexpr (SP) tm = keys_of(lbuf[j], kp);
           bf16x8_t A[4][RT][NS];
           planes(buf[j], A);
           // keep each refill below the last read of its slot, so that it reuses
           // the slot's registers instead of rotating the whole pipeline
           __builtin_amdgcn_sched_barrier(0);
           fetch_z(j, k + j + D);
-          mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+          if constexpr (SP) mma_step_sp(A, kp, tm);
+          else mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
           __builtin_amdgcn_sched_barrier(0);
           fetch_l(j, k + j + D);
         }
@@ -531,7 +613,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
         if (k + j < nst) {
           bf16x8_t A[4][RT][NS];
           planes(buf[j], A);
-          mma_step(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
+          mma_any(A, lbuf[j], (s0 + k + j) * kStep + g4 * 8);
         }
       }
     }
@@ -606,17 +688,17 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
         for (int sp = 0; sp < NS; ++sp) A[pl][rt][sp] = T[pl][sp];
     }
     const uint4 lv = *(const uint4*)(labp + st * kStep);
-    mma_step(A, lv, cell0);
+    mma_any(A, lv, cell0);
   }
 
   if (red.buf) {
-    constexpr int TW = 3 * RT * NT;  // float4 per lane per writer
+    constexpr int TW = NP * RT * NT;  // float4 per lane per writer
     for (int h = red.R >> 1; h >= 1; h >>= 1) {
       const int64_t slot = red.grp * (red.R >> 1) + (red.r & (h - 1));
       if (red.r >= h && red.r < 2 * h) {
         f32x4_t* d = red.buf + slot * TW * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < 3; ++i)
+        for (int i = 0; i < NP; ++i)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -631,7 +713,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
       if (red.r < h) {
         const f32x4_t* d = red.buf + slot * TW * 64 + lane;
 #pragma unroll
-        for (int i = 0; i < 3; ++i)
+        for (int i = 0; i < NP; ++i)
 #pragma unroll
           for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -654,7 +736,7 @@ __device__ __forceinline__ void cost_wave(const CostArgs& a, int64_t lb, int64_t
   // ---- write this wave's partial sums (only the tiles in use)
   constexpr int rows = 16 * RT, nslot = 16 * NT;
 #pragma unroll
-  for (int i = 0; i < 3; ++i)
+  for (int i = 0; i < NP; ++i)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -699,9 +781,12 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
   constexpr int CI = kClassOf<NT>;
   constexpr int WV = cost_waves(NT, TAB);
   constexpr bool kRed = CI > 0;  // classes whose splits the schedule may group
+  constexpr bool SP = CNT == 0 && !TAB && NT >= 7;  // slot-sum form (see cost_wave)
+  constexpr int NP = SP ? 4 : 3;                    // planes per partial tile
   __shared__ __align__(16) unsigned char lut_s[TAB ? kLutBytes : 16];
   __shared__ int prog_s[WV];
-  __shared__ f32x4_t red_s[kRed ? (WV / 2) * 3 * RT * NT * 64 : 1];
+  __shared__ f32x4_t red_s[kRed ? (WV / 2) * NP * RT * NT * 64 : 1];
+  __shared__ uint32_t klut_s[SP ? WV : 1][SP ? 260 : 1];
   __shared__ float2 red_rs[kRed ? (WV / 2) * RT * 64 : 1];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t n = __builtin_amdgcn_readfirstlane(a.sched[CI]);
@@ -713,7 +798,8 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
     if constexpr (TAB) build_lut(lut_s, a.ep);
     __syncthreads();
   };
-  constexpr int64_t tile = 3 * 16 * RT * 16 * NT;
+  constexpr int64_t tile = NP * 16 * RT * 16 * NT;
+  uint32_t* klut = SP ? &klut_s[SP ? wave : 0][0] : nullptr;
   if (kRed && R > 1) {
     const int gpw = WV / R;  // groups per workgroup
     const int grp = wave / R, r = wave - grp * R;
@@ -739,7 +825,8 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
     red.R = R;
     red.r = r;
     red.grp = grp;
-    cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, kp * R + r, KS * R, lut_s, out, rs, nullptr, setup, red);
+    cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, kp * R + r, KS * R, lut_s, out, rs, nullptr, setup, red,
+                                    klut);
     return;
   }
   const int64_t w0 = (int64_t)blockIdx.x * WV;
@@ -757,7 +844,7 @@ __global__ __launch_bounds__(64 * cost_waves(NT, TAB)) void cost_kernel(CostArgs
   float* rs = a.rowsum ? a.rowsum + (a.plan.slot_base[CI] + w) * (16 * RT) * 2 : nullptr;
   // pace the waves only where many share the workgroup's CU
   cost_wave<DT, RT, NT, CNT, TAB>(a, lb, rtile, ks, KS, lut_s, out, rs, WV >= 16 ? prog_s : nullptr,
-                                  setup);
+                                  setup, SplitRed(), klut);
 }
 
 // ---- bf16 table path with LDS-staged logits (16-row tiles, <= 32 columns) ------
@@ -1480,6 +1567,8 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
   CostPlan p = bound_cost_plan(d);
   const int cnt = d.counts_mode ? d.cw : 0;
   p.pair0 = dtype == ML_BF16 && tab && d.pair_ok ? 1 : 0;
+  // the wide classes' slot-sum form runs on label maps without the table
+  for (int c = 0; c < kClasses; ++c) p.planes[c] = c > 0 && !d.counts_mode && !(dtype == ML_BF16 && tab) ? 4 : 3;
   switch (dtype) {
     case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false, false); break;
     case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab, dma_ok(d)); break;

@@ -86,6 +86,13 @@ struct CostPlan {
   // the class's images at one K-split, and its partial tile holds both row
   // tiles ([3][2 rows][nslot]).  No row-sum records on this path.
   int pair0;
+  // Planes per partial tile of each class: 3 (bce numerator, I, T) or 4 for
+  // classes 1 and 2 on label maps without the bf16 table (per-slot sums of
+  // A_neg, A_pos, A_p, A_w over the cells whose label is that slot's column;
+  // slot G holds the cells of no column).  Finalize rebuilds the bce
+  // numerator of slot g as the sum of the other slots' A_neg sums plus g's
+  // A_pos sum, and P, S as the sums over all slots.
+  int planes[kClasses];
 };
 // Device schedule (ints in the workspace): n[kClasses], ks[kClasses] (the
 // K-split partials of each task that reach the partial sums), red[kClasses]
@@ -117,7 +124,7 @@ struct RowPartials {
 __device__ inline RowPartials row_partials_at(const float* partials, const CostPlan& plan, int ci,
                                               int64_t i, int KS, int64_t n, int qin, int64_t rows) {
   const int64_t nslot_c = 16 * class_nt(ci);
-  const int64_t tile = 3 * rows * nslot_c;
+  const int64_t tile = plan.planes[ci] * rows * nslot_c;
   RowPartials r;
   r.KS = KS;
   if (ci == 0 && plan.pair0) {
@@ -240,7 +247,7 @@ struct CostArgs {
   const int* ncols;
   const int* colmap;
   const int* sched;  // device schedule (see CostPlan)
-  float* partials;   // per work item: [3][rows][16 * NT_class]
+  float* partials;   // per work item: [planes][rows][16 * NT_class] (CostPlan::planes)
   float* rowsum;     // per work item: [rows][2] unweighted (force_masks) or null
   CostPlan plan;
   int64_t L, B, Q, HW, HWp, rtiles, GT_total, bg, rows;

@@ -146,6 +146,34 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
                              int32_t* void_found, ml_event_t void_ready,
                              void* workspace, size_t workspace_bytes, ml_stream_t stream);
 
+/* ---- matching forward that skips empty column classes --------------------------
+ * No counterpart in the reference: for a host thread that can wait while its
+ * kernels run (the library's own PyTorch binding uses it).  The forward of
+ * ml_mask_matching_forward, same arguments and results, plus the device and
+ * host addresses of three int32 words of pinned, coherent host memory mapped
+ * for the device.  The cost contraction runs one launch per column-tile class
+ * (images with up to 31, 111 and 255 non-empty GTs), and which classes have
+ * images is known on the device only, so ml_mask_matching_forward launches
+ * every class that the shape allows; an empty launch still costs the GPU a
+ * few microseconds.  Here the forward's column pass stores each class's task
+ * count into the words (system-scope stores); the call queues one class
+ * unconditionally (the narrowest when the shape allows two classes, the
+ * widest when it allows three), waits for the counts (polling; after 2 s it
+ * synchronizes the stream) while that class runs, queues only the other
+ * classes that have tasks, then the rest of the forward, and returns while
+ * that runs.  Not for graph capture (the wait
+ * needs the kernels to run), and one call at a time per set of words.
+ * ML_EINVAL if either address is null. */
+int ml_mask_matching_forward_polled(const ml_shape* s, const ml_params* p, int mask_dtype,
+                                    const void* mask_logits, const int64_t* mask_targets,
+                                    int cls_dtype, const void* cls_logits,
+                                    const int64_t* cls_targets, int64_t* pred_to_gt,
+                                    int64_t* pred_round, float* layer_means, float* separate_costs,
+                                    void* saved, void* grad_mask_prefill, int32_t* void_found,
+                                    ml_event_t void_ready, void* workspace, size_t workspace_bytes,
+                                    ml_stream_t stream, int32_t* class_counts_dev,
+                                    volatile int32_t* class_counts_host);
+
 /* ---- matching forward without allocation -------------------------------------
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

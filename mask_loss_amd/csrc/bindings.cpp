@@ -40,12 +40,15 @@ ml_stream_t cur_stream() { return (ml_stream_t)at::hip::getCurrentHIPStream().st
 // The forward's void-class check writes its answer into a pinned, coherent
 // host word (mapped for the device) with a system-scope store; the host
 // polls the word rather than recording an event in the stream (an event's
-// system-scope release would stall the next kernel).  One word per host
+// system-scope release would stall the next kernel).  Words 4 .. 6 of the
+// same block receive the column-tile classes' task counts, so that the
+// forward launches only the classes that have images.  One block per host
 // thread and device, kept for the life of the process.
 struct VoidSlot {
   volatile int32_t* host = nullptr;
   int32_t* dev = nullptr;
 };
+constexpr int kClassWords = 4;  // offset of the class-count words in the block
 
 VoidSlot& void_slot() {
   constexpr int kMaxDevices = 64;
@@ -224,20 +227,22 @@ std::vector<torch::Tensor> matching_impl(const torch::Tensor& mask_logits,
   const size_t wsb = ml_mask_matching_workspace_size(&s, &p, mdt);
   TORCH_CHECK(wsb > 0 || s.B == 0 || s.L == 0, ml_last_error());
   auto ws = workspace(wsb, mask_logits);
-  VoidSlot* vs = check_void ? &void_slot() : nullptr;
+  VoidSlot& words = void_slot();
+  VoidSlot* vs = check_void ? &words : nullptr;
   if (vs) *vs->host = -1;
-  const int rc = ml_mask_matching_forward(
+  const int rc = ml_mask_matching_forward_polled(
       &s, &p, mdt, mask_logits.data_ptr(), mask_targets.data_ptr<int64_t>(), cdt,
       cls_logits.data_ptr(), cls_targets.data_ptr<int64_t>(), pred_to_gt.data_ptr<int64_t>(),
       pred_round.data_ptr<int64_t>(), means.data_ptr<float>(), nullptr,
       want_saved ? saved.data_ptr() : nullptr, prefill, vs ? vs->dev : nullptr,
-      nullptr, ws.data_ptr(), ws.numel(), cur_stream());
+      nullptr, ws.data_ptr(), ws.numel(), cur_stream(), words.dev + kClassWords,
+      words.host + kClassWords);
   if (rc != ML_OK) {
     // a failure after the first launch leaves kernels queued that may still
-    // write this thread's void word: let them finish before the next call
-    // re-arms it
+    // write this thread's void and class-count words: let them finish before
+    // the next call re-arms them
     const std::string msg = ml_last_error();
-    if (vs) (void)hipStreamSynchronize((hipStream_t)cur_stream());
+    (void)hipStreamSynchronize((hipStream_t)cur_stream());
     TORCH_CHECK(false, msg);
   }
   int32_t void_hit = -1;

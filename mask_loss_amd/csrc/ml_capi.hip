@@ -6,8 +6,10 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "ml_internal.h"
@@ -282,6 +284,29 @@ int check_matching_params(const ml_params* p, int64_t C) { return check_params(p
 
 static bool dtype_ok(int dt) { return dt == ML_F32 || dt == ML_BF16 || dt == ML_F16; }
 
+// The task counts of the column-tile classes below nclass other than `skip`
+// from the pinned words the column pass stores with system scope (preset to
+// -1): polled, and after 2 s the stream is drained, after which they are
+// written.
+static int wait_class_counts(volatile int32_t* w, int nclass, int skip, hipStream_t st, int32_t* n) {
+  const auto t0 = std::chrono::steady_clock::now();
+  auto ready = [&]() {
+    for (int c = 0; c < nclass; ++c)
+      if (c != skip && w[c] == -1) return false;
+    return true;
+  };
+  while (!ready()) {
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
+      if (hipStreamSynchronize(st) != hipSuccess) return fail(ML_ELAUNCH, "class counts: stream failed");
+      if (!ready()) return fail(ML_ELAUNCH, "class counts: the column pass did not write them");
+      break;
+    }
+    std::this_thread::yield();
+  }
+  for (int c = 0; c < kClasses; ++c) n[c] = c < nclass && c != skip ? w[c] : 0;
+  return ML_OK;
+}
+
 // Shared forward: prep -> cost -> assign (-> layer).
 int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                  const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
@@ -290,7 +315,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                  void* prefill, int32_t* void_found, hipEvent_t void_ready, void* ws,
                  size_t ws_bytes, hipStream_t st, bool costs_only, float* bce_out,
                  float* dice_out, const float* pt_coords, int64_t pt_Hs, int64_t pt_Ws,
-                 bool packed) {
+                 bool packed, int32_t* cc_dev, volatile int32_t* cc_host) {
   if (!dtype_ok(mask_dtype) || (cls_logits && !dtype_ok(cls_dtype)))
     return fail(ML_EINVAL, "unsupported dtype");
   Dims d;
@@ -362,6 +387,13 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
   pa.sched = (int*)(w + L.sched);
   pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = plan;
+  // the wider classes' launches wait for the device's task counts (only when
+  // there are wider classes and a host that can wait)
+  const bool poll_classes = cc_dev && cc_host && !pt_coords && plan.nclass > 1;
+  if (poll_classes) {
+    for (int c = 0; c < kClasses; ++c) cc_host[c] = -1;
+    pa.class_counts = cc_dev;
+  }
   if (pt_coords) {
     pa.pbits = (uint32_t*)(w + pt_pbits);
     pa.nblk = pt_nblk;
@@ -390,7 +422,26 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.rows = d.rows;
   ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;
   ca.use_lut = g_use_lut;
-  if (d.LB > 0 && d.rtiles > 0 && (rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
+  if (d.LB > 0 && d.rtiles > 0) {
+    if (!poll_classes) {
+      if ((rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
+    } else {
+      // one class first, unconditionally: class 0 when the shape allows two
+      // classes, else the widest; while it runs, the column pass's counts
+      // reach the host, which then launches only the other classes that have
+      // tasks (an empty class launch costs the GPU ~4.5 us, and waiting
+      // before the first class would leave the GPU idle instead)
+      ProfScope ps_("pair_cost", st);
+      const int first = plan.nclass > 2 ? plan.nclass - 1 : 0;
+      if ((rc = launch_cost(ca, d, mask_dtype, force_masks, st, 1u << first, false))) return rc;
+      int32_t n[kClasses];
+      if ((rc = wait_class_counts(cc_host, plan.nclass, first, st, n))) return rc;
+      unsigned rest = 0;
+      for (int c = 0; c < plan.nclass; ++c)
+        if (c != first && n[c] != 0) rest |= 1u << c;
+      if (rest && (rc = launch_cost(ca, d, mask_dtype, force_masks, st, rest, false))) return rc;
+    }
+  }
 
   const bool use_softmax = p->use_softmax_label_loss != 0;
   AssignArgs aa;
@@ -608,6 +659,26 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
                       grad_mask_prefill, void_found, (hipEvent_t)void_ready, workspace,
                       workspace_bytes, (hipStream_t)stream, false, nullptr, nullptr, nullptr, 0,
                       0, false);
+}
+
+int ml_mask_matching_forward_polled(const ml_shape* s, const ml_params* p, int mask_dtype,
+                                    const void* mask_logits, const int64_t* mask_targets,
+                                    int cls_dtype, const void* cls_logits,
+                                    const int64_t* cls_targets, int64_t* pred_to_gt,
+                                    int64_t* pred_round, float* layer_means, float* separate_costs,
+                                    void* saved, void* grad_mask_prefill, int32_t* void_found,
+                                    ml_event_t void_ready, void* workspace, size_t workspace_bytes,
+                                    ml_stream_t stream, int32_t* class_counts_dev,
+                                    volatile int32_t* class_counts_host) {
+  int rc = check_params(p, s->C, true);
+  if (rc) return rc;
+  if (!class_counts_dev || !class_counts_host)
+    return fail(ML_EINVAL, "the class count words must not be null");
+  return forward_impl(s, p, mask_dtype, mask_logits, mask_targets, cls_dtype, cls_logits,
+                      cls_targets, pred_to_gt, pred_round, layer_means, separate_costs, saved,
+                      grad_mask_prefill, void_found, (hipEvent_t)void_ready, workspace,
+                      workspace_bytes, (hipStream_t)stream, false, nullptr, nullptr, nullptr, 0,
+                      0, false, class_counts_dev, class_counts_host);
 }
 
 int ml_pairwise_mask_loss_forward(const ml_shape* s, const ml_params* p, int mask_dtype,

@@ -1615,23 +1615,25 @@ static int launch_one(const CostArgs& a, const Dims& d, bool tab, hipStream_t st
 // One launch per column-tile class up to the padded width; each image is
 // processed by exactly one of them.
 template <int DT, int RT>
-static int launch_classes(const CostArgs& a, const Dims& d, bool tab, hipStream_t st) {
-  int rc = launch_one<DT, RT, 2>(a, d, tab, st);
-  if (!rc && a.plan.nclass > 1) rc = launch_one<DT, RT, 7>(a, d, tab, st);
-  if (!rc && a.plan.nclass > 2) rc = launch_one<DT, RT, 16>(a, d, tab, st);
+static int launch_classes(const CostArgs& a, const Dims& d, bool tab, unsigned classes, hipStream_t st) {
+  int rc = 0;
+  if (classes & 1u) rc = launch_one<DT, RT, 2>(a, d, tab, st);
+  if (!rc && a.plan.nclass > 1 && (classes & 2u)) rc = launch_one<DT, RT, 7>(a, d, tab, st);
+  if (!rc && a.plan.nclass > 2 && (classes & 4u)) rc = launch_one<DT, RT, 16>(a, d, tab, st);
   return rc;
 }
 
 int cost_rt_for(int, int) { return 1; }
 
-int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool, hipStream_t st) {
-  ProfScope ps_("pair_cost", st);
+int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool, hipStream_t st, unsigned classes,
+                bool prof) {
+  ProfScope ps_(prof ? "pair_cost" : nullptr, st);
   // bf16 with label maps and no unweighted row sums: table path
   const bool tab = dtype == ML_BF16 && !d.counts_mode && a.use_lut && a.rowsum == nullptr;
   switch (dtype) {
-    case ML_F32: return launch_classes<ML_F32, 1>(a, d, false, st);
-    case ML_BF16: return launch_classes<ML_BF16, 1>(a, d, tab, st);
-    case ML_F16: return launch_classes<ML_F16, 1>(a, d, false, st);
+    case ML_F32: return launch_classes<ML_F32, 1>(a, d, false, classes, st);
+    case ML_BF16: return launch_classes<ML_BF16, 1>(a, d, tab, classes, st);
+    case ML_F16: return launch_classes<ML_F16, 1>(a, d, false, classes, st);
   }
   return fail(ML_EINVAL, "unsupported mask logits dtype");
 }

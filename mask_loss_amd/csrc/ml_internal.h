@@ -229,6 +229,10 @@ struct PrepArgs {
   const int64_t* cls_targets = nullptr;
   int64_t void_idx = -1;  // -1: no valid void index (the check reports 0)
   int32_t* void_found = nullptr;
+  // null, or kClasses int32 the device can write (pinned host memory mapped
+  // for the device): the column pass stores each class's task count there
+  // with system-scope stores, for a host that launches only non-empty classes
+  int32_t* class_counts = nullptr;
   int* ncols;
   int* colmap;
   int* slot_of_col;
@@ -377,13 +381,18 @@ struct DenseArgs {
 // prep -> cost -> finalize -> assignment (costs_only: no assignment) on `st`,
 // scratch from `ws` (ws_bytes).  packed: the cost plan's regions are packed
 // for its own slot counts (pack_cost_plan) instead of the kCostSlots bound.
+// cc_dev / cc_host: null, or the device and host addresses of kClasses pinned
+// int32 words: the column pass stores the classes' task counts there, and the
+// host launches column-tile class 0, waits for the counts, then launches only
+// the wider classes that have tasks.
 int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype, const void* mask_logits,
                  const int64_t* mask_targets, int cls_dtype, const void* cls_logits,
                  const int64_t* cls_targets, int64_t* pred_to_gt, int64_t* pred_round,
                  float* layer_means, float* sep, void* saved, void* prefill, int32_t* void_found,
                  hipEvent_t void_ready, void* ws, size_t ws_bytes, hipStream_t st, bool costs_only,
                  float* bce_out, float* dice_out, const float* pt_coords, int64_t pt_Hs,
-                 int64_t pt_Ws, bool packed);
+                 int64_t pt_Ws, bool packed, int32_t* cc_dev = nullptr,
+                 volatile int32_t* cc_host = nullptr);
 int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t& bytes);
 int check_matching_params(const ml_params* p, int64_t C);
 
@@ -393,13 +402,21 @@ void prof_end(const char* name, hipStream_t st);
 struct ProfScope {
   const char* n;
   hipStream_t s;
-  ProfScope(const char* name, hipStream_t st) : n(name), s(st) { prof_begin(n, s); }
-  ~ProfScope() { prof_end(n, s); }
+  // name == null: no bracket
+  ProfScope(const char* name, hipStream_t st) : n(name), s(st) {
+    if (n) prof_begin(n, s);
+  }
+  ~ProfScope() {
+    if (n) prof_end(n, s);
+  }
 };
 
 // ---- launchers (defined in the kernels' translation units) ---------------------
 int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st);
-int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool force_masks, hipStream_t st);
+// classes: bit c launches column-tile class c (all by default); prof: bracket
+// the launches with the profiling events
+int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool force_masks, hipStream_t st,
+                unsigned classes = ~0u, bool prof = true);
 int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st);
 int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st);
 int launch_layer(const LayerArgs& a, hipStream_t st);

@@ -246,6 +246,7 @@ __device__ void columns_and_schedule(const PrepArgs& a) {
     a.sched[lane] = n;
     a.sched[kClasses + lane] = (int)ks;
     a.sched[kSchedRed + lane] = red;
+    if (a.class_counts) __hip_atomic_store(a.class_counts + lane, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 

@@ -161,3 +161,96 @@ def test_capi_matching_forward(lib, case):
     # 3. the void-class flag (reference functions/mask/matching.py:184-185)
     want_void = int(d["void"] >= 0 and (x["ct_np"] == d["void"]).any())
     assert int(out["void"].item()) == want_void
+
+
+# ---- the forward that launches only the column-tile classes with images ----
+def hip_runtime():
+    """The HIP runtime the process has loaded (torch's), for pinned memory."""
+    for line in open("/proc/self/maps"):
+        path = line.split()[-1]
+        if "libamdhip64.so" in path:
+            rt = ctypes.CDLL(path)
+            rt.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+            rt.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p,
+                                                   ctypes.c_uint]
+            rt.hipHostFree.argtypes = [ctypes.c_void_p]
+            return rt
+    pytest.skip("HIP runtime not found in the process")
+
+
+def polled_forward(lib, x, p, words):
+    """ml_mask_matching_forward_polled with the host/device words `words`."""
+    s = x["shape"]
+    L, B, Q, G = s.L, s.B, s.Q, s.GT_total - 1
+    dev = "cuda"
+    out = dict(p2g=torch.full((L, B, Q), -7, dtype=torch.int64, device=dev),
+               pr=torch.full((L, B, Q), -7, dtype=torch.int64, device=dev),
+               means=torch.full((3, L), float("nan"), device=dev),
+               sep=torch.full((3, L, B, Q, G), float("nan"), device=dev),
+               saved=torch.zeros(lib.ml_saved_bytes(s, p, x["dtype"]), dtype=torch.uint8, device=dev),
+               void=torch.full((1,), -1, dtype=torch.int32, device=dev))
+    wsb = lib.ml_mask_matching_workspace_size(s, p, x["dtype"])
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    hdev, hhost = words
+    rc = lib.ml_mask_matching_forward_polled(
+        ctypes.byref(s), ctypes.byref(p), x["dtype"], ptr(x["z"]), ptr(x["tgt"]), ML_F32, ptr(x["zc"]),
+        ptr(x["ct"]), ptr(out["p2g"]), ptr(out["pr"]), ptr(out["means"]), ptr(out["sep"]),
+        ptr(out["saved"]), None, ptr(out["void"]), None, ptr(ws), wsb, stream, hdev, hhost)
+    assert rc == 0, lib.ml_last_error().decode()
+    torch.cuda.synchronize()
+    return {k: v.cpu() for k, v in out.items()}
+
+
+def two_size_case(seed, dtype, big_gts):
+    """Images 0, 1 with at most 12 and 20 GTs and image 2 with exactly
+    `big_gts` non-empty GTs (disjoint 3 x 3 squares), so that column-tile
+    class 1 has image 2 when big_gts >= 32 and no image otherwise; GT_total
+    is 41 in every case."""
+    x = make(seed, B=3, Q=40, H=32, W=32, G=40, C=9, dtype=dtype)
+    tgt = x["tgt_np"].copy()
+    tgt[0][tgt[0] > 12] = 0
+    tgt[1][tgt[1] > 20] = 0
+    tgt[2] = 0
+    for g in range(1, big_gts + 1):
+        y0, x0 = ((g - 1) // 8) * 6, ((g - 1) % 8) * 4
+        tgt[2, y0:y0 + 3, x0:x0 + 3] = g
+    x["tgt_np"] = tgt
+    x["tgt"] = torch.from_numpy(tgt).cuda()
+    return x
+
+
+@pytest.mark.parametrize("dtype", [ML_F32, ML_BF16])
+@pytest.mark.parametrize("big_gts", [20, 40])
+def test_capi_polled_forward_same_results(lib, dtype, big_gts):
+    """The polled forward skips the empty wider class (big_gts = 20: class 1
+    has no image) or launches it (40), and returns exactly what
+    ml_mask_matching_forward returns; its words hold the classes' task
+    counts."""
+    rt = hip_runtime()
+    P = ctypes.c_void_p
+    lib.ml_mask_matching_forward_polled.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(Params), ctypes.c_int,
+                                                    P, P, ctypes.c_int, P, P, P, P, P, P, P, P, P, P, P,
+                                                    ctypes.c_size_t, P, P, P]
+    h = ctypes.c_void_p()
+    assert rt.hipHostMalloc(ctypes.byref(h), 64, 0x2 | 0x40000000) == 0  # mapped | coherent
+    try:
+        d = ctypes.c_void_p()
+        assert rt.hipHostGetDevicePointer(ctypes.byref(d), h, 0) == 0
+        words = (ctypes.c_int32 * 16).from_address(h.value)
+        x = two_size_case(77, dtype, big_gts)
+        p = Params(1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, 1e30, -1.0, 1, 0, 1, 0, 0.0, -1.0, 0.0, -1.0, 8, 1, 1)
+        want = forward(lib, x, p)
+        for _ in range(2):  # twice: the words are re-armed by each call
+            got = polled_forward(lib, x, p, (d, h))
+            for k in ("p2g", "pr", "means", "sep", "saved", "void"):
+                assert torch.equal(got[k], want[k]), k
+            rtiles = (x["shape"].Q + 15) // 16
+            present = [len(np.setdiff1d(np.unique(x["tgt_np"][b]), [0])) for b in range(3)]
+            cls = [0 if g + 1 <= 32 else 1 for g in present]
+            n = [words[i] for i in range(3)]
+            assert n == [cls.count(0) * rtiles, cls.count(1) * rtiles, 0], (n, present)
+            assert n[1] == (rtiles if big_gts == 40 else 0)
+    finally:
+        rt.hipHostFree(h)

@@ -3,7 +3,9 @@
  * matched-loss library (libmask_loss_hip.so).
  *
  * Plain pointers, sizes and a hipStream_t; no framework types.  Every entry
- * point enqueues work on `stream` and returns without synchronising.  All
+ * point enqueues work on `stream` and returns without synchronising (except
+ * ml_mask_matching_forward_polled, which waits for its forward's second
+ * kernel before it queues the rest).  All
  * device pointers must be device-accessible, contiguous, row-major.
  * Return value: ML_OK (0) or an ML_E* code; ml_last_error() returns the
  * message of the last failure on the calling thread.
@@ -195,6 +197,12 @@ int ml_mask_matching_forward_noalloc(const ml_shape* s, const ml_params* p, int 
                                      float* separate_costs, void* saved, void* grad_mask_prefill,
                                      int32_t* void_found, ml_event_t void_ready,
                                      ml_stream_t stream);
+/* Scratch bytes ml_mask_matching_forward_noalloc needs for this shape on the
+ * current device (its cost plan is sized for the device's resident waves),
+ * to compare with ML_NOALLOC_SCRATCH_BYTES before a call; 0 on an invalid
+ * or unsupported shape (ml_last_error() says why).  No counterpart in the
+ * reference; allocates nothing and launches nothing. */
+size_t ml_mask_matching_forward_noalloc_bytes(const ml_shape* s, const ml_params* p, int mask_dtype);
 
 /* ---- matching backward ------------------------------------------------------
  * grad_{mask,dice,cls}: (L,) float upstream gradients of the layer means.

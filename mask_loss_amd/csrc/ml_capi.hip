@@ -181,6 +181,29 @@ void pack_cost_plan(CostPlan& p, const Dims& d) {
   p.slot_total = sl;
 }
 
+// The packed plan within `budget` workspace bytes: while the layout exceeds
+// it, halve the slots of the class whose partial-sum region is largest (a
+// smaller K-split and grid for that class: slower, same results to the cost
+// tolerance), down to the class's task count.  For the allocation-free
+// forward, whose scratch is fixed.
+void fit_cost_plan(CostPlan& p, const Dims& d, bool force_masks, size_t budget) {
+  pack_cost_plan(p, d);
+  while (make_layout(d, force_masks, p).total > budget) {
+    int best = -1;
+    int64_t best_f = 0;
+    for (int c = 0; c < p.nclass; ++c) {
+      const int64_t f = (c + 1 < kClasses ? p.float_base[c + 1] : p.float_total) - p.float_base[c];
+      if (p.slots[c] > 8 && p.slots[c] > p.ntasks && f > best_f) {
+        best = c;
+        best_f = f;
+      }
+    }
+    if (best < 0) return;
+    p.slots[best] = std::max<int>(8, p.slots[best] / 2);
+    pack_cost_plan(p, d);
+  }
+}
+
 Layout make_layout(const Dims& d, bool force_masks) {
   return make_layout(d, force_masks, bound_cost_plan(d));
 }
@@ -338,7 +361,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   float* stats = saved ? (float*)(sv + SL.stats) : nullptr;
   const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
   CostPlan plan = make_cost_plan(d, mask_dtype, tab);
-  if (packed) pack_cost_plan(plan, d);
+  if (packed) fit_cost_plan(plan, d, force_masks, ws_bytes);
   const Layout L = packed ? make_layout(d, force_masks, plan) : make_layout(d, force_masks);
   // point-sampling front end: presence records of the full label map after the layout
   const size_t pt_pbits = align256(L.total);
@@ -541,11 +564,13 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   return ML_OK;
 }
 
-// Workspace bytes of the matching forward with the packed cost plan (what
-// forward_impl with packed = true needs) in `bytes`; the shape errors are
+// Workspace bytes of the matching forward with the packed cost plan fitted
+// to `budget` (what forward_impl with packed = true and ws_bytes = budget
+// needs) in `bytes`; the shape errors are
 // those of ml_mask_matching_forward (ML_EINVAL for malformed shapes,
 // ML_EUNSUPPORTED for shapes the assignment does not take).
-int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t& bytes) {
+int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t budget,
+                         size_t& bytes) {
   Dims d;
   std::string err;
   bytes = 0;
@@ -554,7 +579,7 @@ int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, 
   const bool force_masks = p->force_unmatched_masks_to_empty != 0;
   const bool tab = mask_dtype == ML_BF16 && !d.counts_mode && g_use_lut && !force_masks;
   CostPlan plan = make_cost_plan(d, mask_dtype, tab);
-  pack_cost_plan(plan, d);
+  fit_cost_plan(plan, d, force_masks, budget);
   bytes = make_layout(d, force_masks, plan).total;
   return ML_OK;
 }

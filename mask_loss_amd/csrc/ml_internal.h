@@ -202,6 +202,9 @@ CostPlan bound_cost_plan(const Dims& d);
 // max(slots[c], ntasks) work items): the smallest layout that gives the same
 // K-splits, and so the same results, as the bound layout.
 void pack_cost_plan(CostPlan& p, const Dims& d);
+// pack_cost_plan, with fewer slots for the classes with the largest partial
+// regions until the layout fits `budget` bytes (or no class can shrink)
+void fit_cost_plan(CostPlan& p, const Dims& d, bool force_masks, size_t budget);
 
 // ---- kernel argument blocks ------------------------------------------------
 // Part of the gradient's zero fill done by `blocks` extra workgroups of a
@@ -380,11 +383,12 @@ struct DenseArgs {
 // ---- the shared forward (ml_capi.hip) ---------------------------------------
 // prep -> cost -> finalize -> assignment (costs_only: no assignment) on `st`,
 // scratch from `ws` (ws_bytes).  packed: the cost plan's regions are packed
-// for its own slot counts (pack_cost_plan) instead of the kCostSlots bound.
+// for its own slot counts (pack_cost_plan) instead of the kCostSlots bound,
+// with fewer slots where that does not fit ws_bytes (fit_cost_plan).
 // cc_dev / cc_host: null, or the device and host addresses of kClasses pinned
 // int32 words: the column pass stores the classes' task counts there, and the
-// host launches column-tile class 0, waits for the counts, then launches only
-// the wider classes that have tasks.
+// host launches one class (class 0 of two, the widest of three), waits for
+// the counts, then launches only the other classes that have tasks.
 int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype, const void* mask_logits,
                  const int64_t* mask_targets, int cls_dtype, const void* cls_logits,
                  const int64_t* cls_targets, int64_t* pred_to_gt, int64_t* pred_round,
@@ -393,7 +397,11 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype, const vo
                  float* bce_out, float* dice_out, const float* pt_coords, int64_t pt_Hs,
                  int64_t pt_Ws, bool packed, int32_t* cc_dev = nullptr,
                  volatile int32_t* cc_host = nullptr);
-int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t& bytes);
+// Workspace bytes of the packed forward whose cost plan is fitted to `budget`
+// (fit_cost_plan), what forward_impl with packed = true and ws_bytes = budget
+// uses.
+int forward_packed_bytes(const ml_shape* s, const ml_params* p, int mask_dtype, size_t budget,
+                         size_t& bytes);
 int check_matching_params(const ml_params* p, int64_t C);
 
 // ---- instrumentation: bracket a launch with events when profiling is on ------

@@ -55,6 +55,14 @@ int scratch_address(void** out) {
 
 using namespace ml;
 
+extern "C" size_t ml_mask_matching_forward_noalloc_bytes(const ml_shape* s, const ml_params* p,
+                                                         int mask_dtype) {
+  if (check_matching_params(p, s->C)) return 0;
+  size_t need = 0;
+  if (forward_packed_bytes(s, p, mask_dtype, kScratchBytes, need)) return 0;
+  return need;
+}
+
 extern "C" int ml_mask_matching_forward_noalloc(
     const ml_shape* s, const ml_params* p, int mask_dtype, const void* mask_logits,
     const int64_t* mask_targets, int cls_dtype, const void* cls_logits, const int64_t* cls_targets,
@@ -64,7 +72,7 @@ extern "C" int ml_mask_matching_forward_noalloc(
   int rc = check_matching_params(p, s->C);
   if (rc) return rc;
   size_t need = 0;
-  if ((rc = forward_packed_bytes(s, p, mask_dtype, need))) return rc;
+  if ((rc = forward_packed_bytes(s, p, mask_dtype, kScratchBytes, need))) return rc;
   if (need > kScratchBytes)
     return fail(ML_EUNSUPPORTED, "no-allocation forward: this shape needs " + std::to_string(need) +
                                      " bytes of scratch, more than the " +

@@ -55,6 +55,9 @@ def lib():
     lib.ml_mask_matching_workspace_size.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(Params), ctypes.c_int]
     lib.ml_saved_bytes.restype = ctypes.c_size_t
     lib.ml_saved_bytes.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(Params), ctypes.c_int]
+    lib.ml_mask_matching_forward_noalloc_bytes.restype = ctypes.c_size_t
+    lib.ml_mask_matching_forward_noalloc_bytes.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(Params),
+                                                          ctypes.c_int]
     lib.ml_last_error.restype = ctypes.c_char_p
     return lib
 
@@ -153,6 +156,7 @@ def test_noalloc_rejects_shapes_beyond_its_scratch(lib):
     s = Shape(1, 128, 100, 1024, 1024, 1024, 1024, 9, 250)
     assert s.B * s.Ht * s.Wt * 2 >= 2 * SCRATCH_BYTES
     p = params(9)
+    assert lib.ml_mask_matching_forward_noalloc_bytes(ctypes.byref(s), ctypes.byref(p), ML_BF16) > SCRATCH_BYTES
     dummy = ctypes.c_void_p(0)
     rc = lib.ml_mask_matching_forward_noalloc(ctypes.byref(s), ctypes.byref(p), ML_BF16, dummy, dummy,
                                               ML_F32, dummy, dummy, dummy, dummy, dummy, None, None,
@@ -177,3 +181,40 @@ def test_noalloc_unsupported_shape_codes_match(lib):
     err_ws = lib.ml_last_error()
     assert rc_na == rc_ws == 4, (rc_na, rc_ws)
     assert err_na == err_ws and b"1024 queries" in err_na
+
+
+def test_noalloc_scratch_query(lib):
+    """ml_mask_matching_forward_noalloc_bytes: the headline shape (B=16,
+    Q=200, 256 x 256 bf16, 100 GT columns) fits the scratch array, a shape the
+    assignment does not take reports 0, and the size grows with the batch."""
+    p = params(133)
+    q = lambda s, dt: lib.ml_mask_matching_forward_noalloc_bytes(ctypes.byref(s), ctypes.byref(p), dt)
+    head = q(Shape(1, 16, 200, 256, 256, 256, 256, 134, 101), ML_BF16)
+    assert 0 < head <= SCRATCH_BYTES, head
+    assert q(Shape(1, 32, 200, 256, 256, 256, 256, 134, 101), ML_BF16) > head
+    assert q(Shape(1, 2, 1025, 16, 16, 16, 16, 134, 7), ML_F32) == 0
+    assert b"1024 queries" in lib.ml_last_error()
+
+
+def test_noalloc_fitted_plan_large_shape(lib):
+    """A cfg5-sized shape (8 images x 300 queries, 128 x 128 float32 logits,
+    250 GT columns, 1,204 classes): with the device's full cost plan it needs
+    more than the scratch array (146 MiB on MI355X), so the allocation-free
+    forward sizes its plan for fewer resident slots (a smaller K-split).  Its
+    costs agree with the workspace forward's to the float32 tolerance, and its
+    assignment is the reference solver's on its own costs."""
+    from oracle import assign as OA
+
+    x = make_inputs(5, B=8, Q=300, H=128, W=128, G=250, C=1204, dtype=ML_F32)
+    s, p = x["shape"], params(x["shape"].C)
+    need = lib.ml_mask_matching_forward_noalloc_bytes(ctypes.byref(s), ctypes.byref(p), ML_F32)
+    assert 0 < need <= SCRATCH_BYTES, need
+    got = forward(lib, x, noalloc=True)
+    ref = forward(lib, x, noalloc=False)
+    close(got["sep"], ref["sep"], RTOL[ML_F32], "costs")
+    close(got["means"], ref["means"], RTOL[ML_F32], "means")
+    total = ((got["sep"][0] + got["sep"][1]) + got["sep"][2]).double().cpu().numpy().reshape(8, 300, 250)
+    rp2g, rpr = OA.assign_batch(total, 1e30, 1, 0)
+    assert np.array_equal(got["p2g"].cpu().numpy().reshape(8, 300), rp2g)
+    assert np.array_equal(got["pr"].cpu().numpy().reshape(8, 300), rpr)
+    assert (rp2g >= 0).any()

@@ -53,7 +53,7 @@ def rounded(z, dtype):
 
 
 def make_case(seed, L=1, B=2, Q=20, H=16, W=16, s=1, G=6, C=9, dtype="float32", sigma=2.0,
-              empty_image=False, extreme=False):
+              empty_image=False, extreme=False, grid=False):
     rng = np.random.default_rng(seed)
     z = rng.normal(0, sigma, size=(L, B, Q, H, W)).astype(np.float32)
     if extreme:  # |z| >= 64 in a few rows: outside the bf16 table, formulas redo those waves
@@ -65,6 +65,16 @@ def make_case(seed, L=1, B=2, Q=20, H=16, W=16, s=1, G=6, C=9, dtype="float32", 
     tgt = np.zeros((B, H * s, W * s), dtype=np.int64)
     for b in range(B):
         if empty_image and b == 0:
+            continue
+        if grid:  # G disjoint blocks, labels shuffled: exactly G non-empty GTs
+            r = int(math.ceil(math.sqrt(G)))
+            c = int(math.ceil(G / r))
+            hb, wb = (H * s) // r, (W * s) // c
+            assert hb > 0 and wb > 0, "grid case: blocks need a cell each"
+            perm = rng.permutation(G) + 1
+            for i in range(G):
+                y0, x0 = (i // c) * hb, (i % c) * wb
+                tgt[b, y0:y0 + hb, x0:x0 + wb] = perm[i]
             continue
         for g in range(1, G + 1):
             cy, cx = rng.uniform(0, H * s), rng.uniform(0, W * s)
@@ -105,6 +115,20 @@ COST_CASES = [
     dict(name="bf16_extreme", kw=dict(Q=40, H=32, W=32, dtype="bfloat16", sigma=3.0, extreme=True), p={}),
     dict(name="bf16_extreme_many_gt",
          kw=dict(G=70, Q=40, H=32, W=32, dtype="bfloat16", sigma=3.0, extreme=True), p={}),
+    # the wide classes: slot sums with a 2-term split (f16), a background
+    # label inside the GT range (the label -> slot table), focal terms in the
+    # 16-tile class, and count operands (grouped K-splits, complement form)
+    # (grid: exactly G non-empty GTs, 40 in the 7-tile class, 120 in the
+    # 16-tile one)
+    dict(name="f32_grid40", kw=dict(G=40, Q=50, H=32, W=32, grid=True), p={}),
+    dict(name="f32_grid120_focal", kw=dict(G=120, Q=40, H=32, W=32, grid=True),
+         p=dict(mask_gamma=2.0, mask_alpha=0.25, ug=2.0, ug_min=0.1)),
+    dict(name="f16_grid40", kw=dict(G=40, Q=50, H=32, W=32, dtype="float16", grid=True), p={}),
+    dict(name="f16_grid120", kw=dict(G=120, Q=40, H=32, W=32, dtype="float16", grid=True), p={}),
+    dict(name="bf16_grid40", kw=dict(G=40, Q=64, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True), p={}),
+    dict(name="bf16_grid120", kw=dict(G=120, Q=40, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True), p={}),
+    dict(name="f32_grid40_bg_mid", kw=dict(G=40, Q=50, H=32, W=32, grid=True), p=dict(bg=3)),
+    dict(name="f32_counts_s2_grid40", kw=dict(s=2, G=40, Q=40, H=32, W=32, grid=True), p={}),
     dict(name="f32_empty_image", kw=dict(empty_image=True), p={}),
     dict(name="f32_L2", kw=dict(L=2), p=dict(scales=(1.3, 0.7, 2.0), smooth=0.5)),
 ]
@@ -185,8 +209,13 @@ MATCH_CASES = [
     dict(name="counts_s17_force", kw=dict(s=17, H=4, W=4), p={}, m=dict(force_masks=True, force_cls=True)),
     # wider column classes with unweighted row sums: K-splits added in the
     # cost workgroup (8 per partial at 41 columns, 4 at 121)
-    dict(name="wide7_force", kw=dict(G=40, Q=50, H=32, W=32), p={}, m=dict(force_masks=True, force_cls=True)),
-    dict(name="wide16_force", kw=dict(G=120, Q=40, H=32, W=32), p={}, m=dict(force_masks=True)),
+    dict(name="wide7_force", kw=dict(G=40, Q=50, H=32, W=32, grid=True), p={},
+         m=dict(force_masks=True, force_cls=True)),
+    dict(name="wide16_force", kw=dict(G=120, Q=40, H=32, W=32, grid=True), p={}, m=dict(force_masks=True)),
+    dict(name="wide16", kw=dict(G=120, Q=130, H=32, W=32, grid=True), p={}, m={}),
+    # bf16 with forced-empty masks runs without the table: slot sums in bf16
+    dict(name="bf16_wide7_force", kw=dict(G=40, Q=50, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True),
+         p={}, m=dict(force_masks=True, force_cls=True)),
     dict(name="empty_image", kw=dict(empty_image=True), p={}, m=dict(force_cls=True, void=8)),
     dict(name="q_tail_1024", kw=dict(Q=130, H=8, W=8, G=20), p={}, m={}),
     # cost matrices too large for LDS (300 x 250 floats): every row read in
@@ -325,6 +354,12 @@ BWD_CASES = [
          m=dict(force_cls=True, void=699)),
     dict(name="bf16_softmax_C700", kw=dict(C=700, Q=24, dtype="bfloat16", sigma=3.0),
          p=dict(use_softmax=True), m=dict(force_cls=True, void=699)),
+    # the wide classes' statistics (slot sums for f32, the table for bf16)
+    dict(name="f32_grid40", kw=dict(G=40, Q=50, H=32, W=32, grid=True), p={}, m=dict(force_cls=True, void=8)),
+    dict(name="bf16_grid120", kw=dict(G=120, Q=130, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True),
+         p={}, m=dict(force_cls=True, void=8)),
+    dict(name="f32_grid120_forcemasks", kw=dict(G=120, Q=40, H=32, W=32, grid=True), p={},
+         m=dict(force_masks=True)),
 ]
 
 

@@ -608,6 +608,9 @@ struct CostRows {
   // and never a flat load through a pointer chosen at run time
   const lds_f32* lds;
   const global_f32* glb;
+  // kCostGlobal: the staging pass's float64 copies of the rows, [column][query]
+  // with row stride ldq, the invalid cost already replaced by BIG
+  const double* glb64;
   int ldq;  // c * ldq fits 31 bits: Q <= 1024, and the column arrays fit the LDS
   // one element (per-lane column)
   __device__ __forceinline__ float at(int64_t c, int64_t q) const {
@@ -617,17 +620,33 @@ struct CostRows {
 
 // The row of column col, at the slots' query indices: a ds_read row or an
 // in-place global row.
+// Row entries as the solver reads them: float32 from the LDS (the invalid
+// cost replaced in each step), float64 c(i, j) for rows read in place.
+template <int CM>
+using RowElem = typename std::conditional<CM == kCostLds, float, double>::type;
 template <int NJ, int CM>
 __device__ __forceinline__ void read_cost_row(const CostRows<CM>& cost, int col,
-                                              const int (&predj)[NJ], float (&rawf)[NJ]) {
-  if (CM == kCostLds) {
+                                              const int (&predj)[NJ], RowElem<CM> (&raw)[NJ]) {
+  if constexpr (CM == kCostLds) {
     const lds_f32* crow = cost.lds + col * cost.ldq;
 #pragma unroll
-    for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+    for (int t = 0; t < NJ; ++t) raw[t] = crow[predj[t]];
   } else {
-    const global_f32* crow = cost.glb + (uint32_t)(col * cost.ldq);
+    const double* crow = cost.glb64 + (uint32_t)(col * cost.ldq);
 #pragma unroll
-    for (int t = 0; t < NJ; ++t) rawf[t] = crow[predj[t]];
+    for (int t = 0; t < NJ; ++t) raw[t] = crow[predj[t]];
+  }
+}
+// c(i, j) of the reference (src/cpu/matching.cpp:497-511): the cost, or BIG
+// for an invalid one (the plane holds a NaN for every non-finite cost, so
+// raw < thr is cost_ok(raw)); rows read in place carry it already.
+template <int CM>
+__device__ __forceinline__ double cij_of(RowElem<CM> raw, double thr, double BIG) {
+  if constexpr (CM == kCostLds) {
+    const double r = (double)raw;
+    return r < thr ? r : BIG;
+  } else {
+    return raw;
   }
 }
 
@@ -664,7 +683,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
   // the first row's here, every later one's during the previous row's
   // augmentation walk, whose latency then hides the read
   int colcur = __builtin_amdgcn_readfirstlane(hrows[0]);
-  float rawf[NJ];
+  RowElem<CM> rawf[NJ];
   read_cost_row<NJ, CM>(cost, colcur, predj, rawf);
   for (int i = 1; i <= M && ok; ++i) {
     const int colnext = i < M ? hrows[i] : colcur;  // no dependence: loaded early
@@ -687,8 +706,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       double lmin = INFINITY;
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
-        const double raw = (double)rawf[t];
-        const double cij = raw < thr ? raw : BIG;
+        const double cij = cij_of<CM>(rawf[t], thr, BIG);
         const double cur = cij - ui0 - v[t];
         const bool upd = cur < minv[t];
         minv[t] = upd ? cur : minv[t];
@@ -905,7 +923,8 @@ __device__ void layer_pass(const LayerArgs& a, int* sbuf, int nsbuf) {
 // the staging).
 
 // Copy the cost rows of image b's non-empty GT columns (colmap order) from
-// finalize's plane into LDS (those CM keeps there) and mark the valid ones (a cost that is
+// finalize's plane into LDS (kCostLds) or, as float64 c(i, j) with BIG for an
+// invalid cost, into tot64 (kCostGlobal), and mark the valid columns (one cost
 // finite and below the threshold, cost_ok).  One wave per row, V floats per
 // load (V = 4 when rows start on 16-byte boundaries), R rows per wave in
 // flight; Q <= 64 * NJ, so a lane holds at most KW words of a row.
@@ -943,8 +962,18 @@ __device__ __forceinline__ void stage_rows(const AssignArgs& a, int64_t lb, int6
         if (CM == kCostLds)
           ((word_t*)costL)[(int64_t)col[r] * W + j] = v[r][k];
         const float* e = (const float*)&v[r][k];
+        double c64[V];
 #pragma unroll
-        for (int h = 0; h < V; ++h) ok |= cost_ok((double)e[h], a.inf_thresh);
+        for (int h = 0; h < V; ++h) {
+          const bool okh = cost_ok((double)e[h], a.inf_thresh);
+          ok |= okh;
+          c64[h] = okh ? (double)e[h] : a.big;
+        }
+        if (CM == kCostGlobal) {
+          double* dst = a.tot64 + (lb * a.GT_out + col[r]) * a.Q + (int64_t)j * V;
+#pragma unroll
+          for (int h = 0; h < V; ++h) dst[h] = c64[h];
+        }
       }
       if (__ballot(ok) != 0ull && lane == 0) colok[col[r]] = 1;
     }
@@ -980,6 +1009,7 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   CostRows<CM> crows;
   crows.lds = (const lds_f32*)costL;
   crows.glb = (const global_f32*)(a.tot + lb * a.tot_stride);
+  crows.glb64 = CM == kCostGlobal ? a.tot64 + lb * a.GT_out * a.Q : nullptr;
   crows.ldq = (int)Q;
   const int64_t term = a.L * a.B * Q * GTo;
   const float* sep = a.sep + lb * Q * GTo;

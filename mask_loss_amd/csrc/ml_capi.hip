@@ -204,6 +204,8 @@ void fit_cost_plan(CostPlan& p, const Dims& d, bool force_masks, size_t budget) 
   }
 }
 
+static int64_t cost_lds_rows(const Dims& d);
+
 Layout make_layout(const Dims& d, bool force_masks) {
   return make_layout(d, force_masks, bound_cost_plan(d));
 }
@@ -227,6 +229,8 @@ Layout make_layout(const Dims& d, bool force_masks, const CostPlan& pl) {
   L.rowsum = take(force_masks ? (size_t)pl.slot_total * d.rows * 2 * 4 : 0);
   L.sep = take((size_t)3 * d.LB * d.Q * d.GT_out * 4);
   L.tot = take((size_t)d.LB * ceil_div(d.Q * d.GT_out, 4) * 16);
+  // float64 cost rows for an assignment that reads them in place
+  L.tot64 = take(cost_lds_rows(d) == 0 ? (size_t)d.LB * d.GT_out * d.Q * 8 : 0);
   L.rowIT = take((size_t)d.LB * d.Q * d.nslot * 8);
   L.rowstat = take((size_t)d.LB * d.Q * 8 * 4);
   L.img = take((size_t)d.LB * 4 * 4);
@@ -488,6 +492,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   }
   aa.rowstat = (float*)(w + L.rowstat);
   aa.tot = costs_only ? nullptr : (float*)(w + L.tot);
+  aa.tot64 = costs_only || lds_rows > 0 ? nullptr : (double*)(w + L.tot64);
   aa.tot_stride = ceil_div(d.Q * d.GT_out, 4) * 4;
   aa.rowIT = costs_only || !stats ? nullptr : (float*)(w + L.rowIT);
   aa.pred_to_gt = pred_to_gt;

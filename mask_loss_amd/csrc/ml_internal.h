@@ -188,7 +188,7 @@ inline SavedLayout saved_layout(const Dims& d) {
 // Byte offsets inside the caller's workspace.
 struct Layout {
   size_t lab16, counts, pbits, ncols, colmap, slot_of_col, sched, partials, rowsum,
-      sep, tot, rowIT, rowstat, img, mrows, layer, done, total;
+      sep, tot, tot64, rowIT, rowstat, img, mrows, layer, done, total;
 };
 // Workspace layout for the cost plan `pl` (its float_total / slot_total size
 // the partial-sum regions).
@@ -295,6 +295,11 @@ struct AssignArgs {
   float* out_dice;       // first two planes, or a standalone operator's outputs, or null)
   float* tot;            // [LB][tot_stride] total cost (bce + dice) + label, [c][q], or null
   int64_t tot_stride;    // Q * GT_out rounded up to whole 16-byte words
+  // [LB][GT_out][Q] float64 copies of the staged cost rows with the invalid
+  // cost replaced by `big` (the Hungarian's c(i, j)), written by the
+  // assignment's staging pass when the rows are read in place (they do not
+  // fit the LDS), or null
+  double* tot64 = nullptr;
   float* rowIT;          // [LB*Q][nslot][2] summed I, T per column slot, or null
   int64_t* pred_to_gt;   // (L,B,Q) or null (costs-only mode)
   int64_t* pred_round;

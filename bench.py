@@ -438,8 +438,12 @@ def main():
     lib.ml_profile_enable(0)
 
     kernels = {}
-    for name in ["prep", "pair_cost", "finalize", "assign", "prefill", "layer", "bwd_mask",
-                 "bwd_cls"]:
+    # finalize_early / assign_early / cost_rest: with images in the widest
+    # column-tile class and another, the widest class's finalize and
+    # assignment (on the side stream), and the other classes' contraction
+    # (finalize and assign then cover the other images)
+    for name in ["prep", "pair_cost", "cost_rest", "finalize", "assign", "finalize_early",
+                 "assign_early", "prefill", "layer", "bwd_mask", "bwd_cls"]:
         n, t = read_prof(lib, name)
         if n:
             kernels[name] = {"launches": n, "avg_us": round(1e3 * t / n, 2)}
@@ -459,6 +463,7 @@ def main():
         # workgroups of the same launch
         "assign": 4 * LBQ * Cp + e * K * LBQ,
     }
+
     step_bytes = step_bytes_of(cfg, e, M)
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
     dom_bytes = bytes_alg.get(dom)

@@ -163,7 +163,11 @@ int ml_mask_matching_forward(const ml_shape* s, const ml_params* p, int mask_dty
  * widest when it allows three), waits for the counts (polling; after 2 s it
  * synchronizes the stream) while that class runs, queues only the other
  * classes that have tasks, then the rest of the forward, and returns while
- * that runs.  Not for graph capture (the wait
+ * that runs.  When the widest class and another class both have images, the
+ * widest class's assignment runs on a second stream of the library's own
+ * (default priority, forked from and joined back into `stream` by events),
+ * beside the other classes' contraction; work queued on `stream` after the
+ * call follows it.  Not for graph capture (the wait
  * needs the kernels to run), and one call at a time per set of words.
  * ML_EINVAL if either address is null. */
 int ml_mask_matching_forward_polled(const ml_shape* s, const ml_params* p, int mask_dtype,

@@ -202,7 +202,7 @@ __device__ __forceinline__ float wave_excl_scan(float v, int lane) {
 template <int CDT, bool FAST, int NC = kFinCls, int NG = kFinCols>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC > 8 ? 3 : 4))) void finalize_kernel(AssignArgs a) {
   if (blockIdx.x == 0 && threadIdx.x == 0) {  // the assignment's finish count
-    if (a.done) *a.done = 0;
+    if (a.done && a.reset_done) *a.done = 0;
   }
   __shared__ float sl[4][4][256 + 16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -260,6 +260,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NC > 8 ? 3 
   const bool need_zv = labels && a.use_softmax && has_void;
 
   // round trip 2: the partials (need the column class) and the targets' logits
+  if (!in_phase(a.phase_class, a.phase_in, G)) return;  // another launch's image
   const int ci = class_of(G + 1);
   int KS = ksc[0], n_ci = nc[0];
 #pragma unroll
@@ -1003,6 +1004,8 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   // fill workgroups should they share the CU.
   __builtin_amdgcn_s_setprio(3);
   const int64_t lb = blockIdx.x, b = lb % a.B;
+  // another launch's image: no work, no count
+  if (!in_phase(a.phase_class, a.phase_in, __builtin_amdgcn_readfirstlane(a.ncols[b]))) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t Q = a.Q, GTo = a.GT_out;
   float* costL = (float*)(smem + L.costL);
@@ -1284,7 +1287,7 @@ size_t assign_smem_bytes(int64_t Q, int64_t GTo, int64_t lds_rows) {
 }
 
 template <int NJ, int CM>
-static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
+static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st, const char* prof) {
   const size_t sm = smem_layout(a.Q, a.GT_out, CM == kCostGlobal ? 0 : a.lds_rows).total;
   // 160 KB of LDS less the kernel's static part, raised once per device (the
   // attribute is set with that device current); the lock makes the first
@@ -1311,22 +1314,22 @@ static int launch_nj_l(const AssignArgs& a, const Dims& d, hipStream_t st) {
   const size_t max_dyn_dev = max_dyn[dev].load(std::memory_order_acquire);
   if (sm > max_dyn_dev) return fail(ML_EUNSUPPORTED, "assign: cost matrix exceeds the LDS budget");
   {
-    ProfScope ps_("assign", st);
+    ProfScope ps_(prof, st);
     hipLaunchKernelGGL((assign_kernel<NJ, CM>), dim3((unsigned)(d.LB + a.fill_blocks)),
                        dim3(256), sm, st, a);
   }
   return check_launch("assign");
 }
 template <int NJ>
-static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st) {
-  if (a.lds_rows >= a.GT_out) return launch_nj_l<NJ, kCostLds>(a, d, st);
-  return launch_nj_l<NJ, kCostGlobal>(a, d, st);
+static int launch_nj(const AssignArgs& a, const Dims& d, hipStream_t st, const char* prof) {
+  if (a.lds_rows >= a.GT_out) return launch_nj_l<NJ, kCostLds>(a, d, st, prof);
+  return launch_nj_l<NJ, kCostGlobal>(a, d, st, prof);
 }
-int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
+int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st, const char* prof) {
   const int64_t rows = d.LB * d.Q;
   if (rows == 0) return ML_OK;
   if (rows >= ((int64_t)1 << 31)) return fail(ML_EINVAL, "L * B * Q must be below 2^31");
-  ProfScope ps_("finalize", st);
+  ProfScope ps_(prof, st);
   const dim3 grid((unsigned)(ceil_div(rows, 4) + a.fin_fill.blocks));
   const bool fast = a.cls_logits && a.C >= 1 && a.C <= 64 * kFinCls && a.GT_out >= 1 &&
                     a.GT_out <= 64 * kFinCols;
@@ -1355,18 +1358,18 @@ int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st) {
   return check_launch("finalize");
 }
 
-int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st) {
+int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st, const char* prof) {
   const int64_t nj = ceil_div(a.Q, 64);
   // one instance per column count up to 6 per lane: the Dijkstra step's work
   // is proportional to NJ
-  if (nj <= 1) return launch_nj<1>(a, d, st);
-  if (nj <= 2) return launch_nj<2>(a, d, st);
-  if (nj <= 3) return launch_nj<3>(a, d, st);
-  if (nj <= 4) return launch_nj<4>(a, d, st);
-  if (nj <= 5) return launch_nj<5>(a, d, st);
-  if (nj <= 6) return launch_nj<6>(a, d, st);
-  if (nj <= 8) return launch_nj<8>(a, d, st);
-  if (nj <= 16) return launch_nj<16>(a, d, st);
+  if (nj <= 1) return launch_nj<1>(a, d, st, prof);
+  if (nj <= 2) return launch_nj<2>(a, d, st, prof);
+  if (nj <= 3) return launch_nj<3>(a, d, st, prof);
+  if (nj <= 4) return launch_nj<4>(a, d, st, prof);
+  if (nj <= 5) return launch_nj<5>(a, d, st, prof);
+  if (nj <= 6) return launch_nj<6>(a, d, st, prof);
+  if (nj <= 8) return launch_nj<8>(a, d, st, prof);
+  if (nj <= 16) return launch_nj<16>(a, d, st, prof);
   return fail(ML_EUNSUPPORTED, "more than 1024 queries per image are not supported");
 }
 

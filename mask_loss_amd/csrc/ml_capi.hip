@@ -334,6 +334,49 @@ static int wait_class_counts(volatile int32_t* w, int nclass, int skip, hipStrea
   return ML_OK;
 }
 
+// A second stream of the current device with a fork and a join event, taken
+// from a pool for the span of one forward's enqueueing.  The stream has the
+// default priority and does not synchronise with the null stream; an event
+// may be recorded again once the wait on it is enqueued, so an entry goes
+// back to the pool right after the join wait.
+struct SideStream {
+  int dev = -1;
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::mutex g_side_mu;
+static std::vector<SideStream> g_side_free;
+
+static int side_acquire(SideStream& out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(ML_ELAUNCH, "no current device");
+  {
+    std::lock_guard<std::mutex> g(g_side_mu);
+    for (size_t i = 0; i < g_side_free.size(); ++i)
+      if (g_side_free[i].dev == dev) {
+        out = g_side_free[i];
+        g_side_free.erase(g_side_free.begin() + (long)i);
+        return ML_OK;
+      }
+  }
+  SideStream n;
+  n.dev = dev;
+  if (hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking) != hipSuccess)
+    return fail(ML_ELAUNCH, "cannot create the side stream");
+  if (hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&n.join, hipEventDisableTiming) != hipSuccess) {
+    if (n.fork) (void)hipEventDestroy(n.fork);
+    (void)hipStreamDestroy(n.s);
+    return fail(ML_ELAUNCH, "cannot create the side stream's events");
+  }
+  out = n;
+  return ML_OK;
+}
+static void side_release(const SideStream& ss) {
+  std::lock_guard<std::mutex> g(g_side_mu);
+  g_side_free.push_back(ss);
+}
+
 // Shared forward: prep -> cost -> assign (-> layer).
 int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
                  const void* mask_logits, const int64_t* mask_targets, int cls_dtype,
@@ -413,6 +456,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   pa.B = d.B; pa.H = d.H; pa.W = d.W; pa.Ht = d.Ht; pa.Wt = d.Wt; pa.s = d.s; pa.HWp = d.HWp;
   pa.GT_total = d.GT_total; pa.GT_out = d.GT_out; pa.bg = d.bg; pa.nslot = d.nslot;
   pa.sched = (int*)(w + L.sched);
+  pa.done = costs_only ? nullptr : (int*)(w + L.done);
   pa.L = d.L; pa.rtiles = d.rtiles; pa.plan = plan;
   // the wider classes' launches wait for the device's task counts (only when
   // there are wider classes and a host that can wait)
@@ -449,6 +493,17 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   ca.rtiles = d.rtiles; ca.GT_total = d.GT_total; ca.bg = d.bg; ca.rows = d.rows;
   ca.nslot = d.nslot; ca.N2 = (float)d.N2; ca.ep = mask_ep;
   ca.use_lut = g_use_lut;
+  // Two image subsets when the widest class (more than 111 non-empty GTs:
+  // the longest solver chains) is the first and the polled counts show
+  // another non-empty class: the widest class's finalize runs right after
+  // its contraction and its assignment on a side stream, beside the other
+  // classes' contraction, finalize and assignment here.  The other classes'
+  // launches leave kSideCUs CUs free for it (CostPlan::slots), and each
+  // subset's rows and images are computed exactly as in one launch, so the
+  // results are the same.
+  int phase_first = -1;
+  unsigned rest_classes = 0;
+  SideStream side;
   if (d.LB > 0 && d.rtiles > 0) {
     if (!poll_classes) {
       if ((rc = launch_cost(ca, d, mask_dtype, force_masks, st))) return rc;
@@ -466,7 +521,14 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
       unsigned rest = 0;
       for (int c = 0; c < plan.nclass; ++c)
         if (c != first && n[c] != 0) rest |= 1u << c;
-      if (rest && (rc = launch_cost(ca, d, mask_dtype, force_masks, st, rest, false))) return rc;
+      // (the first class's own count: written with the others, read once;
+      // not yet visible means no side stream)
+      if (rest && !costs_only && first == kClasses - 1 && cc_host[first] > 0) {
+        phase_first = first;
+        rest_classes = rest;  // launched after the first class's finalize
+      } else if (rest && (rc = launch_cost(ca, d, mask_dtype, force_masks, st, rest, false))) {
+        return rc;
+      }
     }
   }
 
@@ -541,7 +603,7 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   aa.strategy = (int)p->strategy_id;
   aa.costs_only = costs_only;
   aa.lds_rows = lds_rows;
-  if (d.LB > 0 && (rc = launch_finalize(aa, d, st))) return rc;
+  if (phase_first < 0 && d.LB > 0 && (rc = launch_finalize(aa, d, st))) return rc;
   if (costs_only) return ML_OK;
   // per-layer means and the matched-row list, after the assignment
   LayerArgs la;
@@ -557,7 +619,42 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
   la.force_cls = p->force_unmatched_class_to_background;
   la.has_void = void_idx >= 0;
   aa.layer_args = la;  // run by the last assignment workgroup
-  if (d.LB > 0) {
+  if (phase_first >= 0) {
+    // here: the first class's finalize, the other classes' contraction,
+    // finalize (with its share of the gradient fill) and assignment (with
+    // the assignment's share); side stream: the first class's assignment
+    AssignArgs a1 = aa, a2 = aa;
+    a1.reset_done = a2.reset_done = 0;  // zeroed by the column pass
+    a1.phase_class = a2.phase_class = phase_first;
+    a1.phase_in = 1;
+    a2.phase_in = 0;
+    a1.fin_fill = FillSlice();
+    a1.fill_blocks = 0;
+    a1.fill_n16 = a1.fill_ntail = 0;
+    if ((rc = launch_finalize(a1, d, st, "finalize_early"))) return rc;
+    if ((rc = side_acquire(side))) return rc;
+    int rc1 = ML_OK, rc2 = ML_OK;
+    if (hipEventRecord(side.fork, st) != hipSuccess || hipStreamWaitEvent(side.s, side.fork, 0) != hipSuccess)
+      rc1 = fail(ML_ELAUNCH, "cannot fork the side stream");
+    if (!rc1) rc1 = launch_assign(a1, d, side.s, "assign_early");
+    {
+      ProfScope ps_("cost_rest", st);
+      rc2 = launch_cost(ca, d, mask_dtype, force_masks, st, rest_classes, false);
+    }
+    if (!rc2) rc2 = launch_finalize(a2, d, st);
+    if (!rc2) rc2 = launch_assign(a2, d, st);
+    // the join is enqueued whatever failed, so this stream's later work
+    // (and the caller's frees) follow the side stream's
+    const bool joined = hipEventRecord(side.join, side.s) == hipSuccess &&
+                        hipStreamWaitEvent(st, side.join, 0) == hipSuccess;
+    if (joined) side_release(side);
+    if (rc1) return rc1;
+    if (rc2) return rc2;
+    if (!joined) {
+      (void)hipStreamSynchronize(side.s);
+      return fail(ML_ELAUNCH, "cannot join the side stream");
+    }
+  } else if (d.LB > 0) {
     if ((rc = launch_assign(aa, d, st))) return rc;
   } else {
     if (prefill_bytes) {

@@ -1546,8 +1546,25 @@ static int occ_slots_for(int cnt, bool tab) {
   return occ_slots<DT, RT, NT, 0, false>();
 }
 
+static int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+// With three classes the narrower ones leave `side` CUs' worth of waves free:
+// their launches may run beside the widest class's assignment (one
+// workgroup per image on the forward's side stream).
 template <int DT, int RT>
-static void plan_slots(CostPlan& p, int cnt, bool tab, bool dma) {
+static void plan_slots(CostPlan& p, int cnt, bool tab, bool dma, int64_t side) {
+  const int cus = cu_count();
+  side = std::min<int64_t>(side, cus / 8);
   for (int ci = 0; ci < p.nclass; ++ci) {
     int v = 0;
     switch (ci) {
@@ -1559,6 +1576,7 @@ static void plan_slots(CostPlan& p, int cnt, bool tab, bool dma) {
       case 1: v = occ_slots_for<DT, RT, 7>(cnt, tab); break;
       default: v = occ_slots_for<DT, RT, 16>(cnt, tab); break;
     }
+    if (p.nclass == kClasses && ci < kClasses - 1) v -= (int)((int64_t)v * side / cus);
     p.slots[ci] = (int)std::min<int64_t>(std::max(v, 8), kCostSlots);
   }
 }
@@ -1569,10 +1587,11 @@ CostPlan make_cost_plan(const Dims& d, int dtype, bool tab) {
   p.pair0 = dtype == ML_BF16 && tab && d.pair_ok ? 1 : 0;
   // the wide classes' slot-sum form runs on label maps without the table
   for (int c = 0; c < kClasses; ++c) p.planes[c] = c > 0 && !d.counts_mode && !(dtype == ML_BF16 && tab) ? 4 : 3;
+  const int64_t side = std::min<int64_t>(d.LB, kSideCUs);
   switch (dtype) {
-    case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false, false); break;
-    case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab, dma_ok(d)); break;
-    case ML_F16: plan_slots<ML_F16, 1>(p, cnt, false, false); break;
+    case ML_F32: plan_slots<ML_F32, 1>(p, cnt, false, false, side); break;
+    case ML_BF16: plan_slots<ML_BF16, 1>(p, cnt, tab, dma_ok(d), side); break;
+    case ML_F16: plan_slots<ML_F16, 1>(p, cnt, false, false, side); break;
   }
   return p;
 }

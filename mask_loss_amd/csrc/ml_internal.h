@@ -58,8 +58,16 @@ __host__ __device__ inline int class_of(int ncols_plus_one) {
   const int need = (ncols_plus_one + 15) >> 4;
   return need <= 2 ? 0 : need <= 7 ? 1 : 2;
 }
+// Whether an image with G non-empty columns belongs to a launch restricted to
+// the image subset (phase_class, phase_in) (see AssignArgs).
+__host__ __device__ inline bool in_phase(int phase_class, int phase_in, int G) {
+  return phase_class < 0 || ((class_of(G + 1) == phase_class) == (phase_in != 0));
+}
 // Upper bound of resident cost waves the workspace is sized for (256 CUs x 16).
 constexpr int64_t kCostSlots = 4096;
+// CUs the narrower classes' cost launches leave free, with three classes, for
+// the widest class's assignment (at most one per image, at most 1/8 of them)
+constexpr int kSideCUs = 16;
 
 // Host-side plan of the cost launches.  Each class launch has `slots[c]`
 // waves (what the GPU holds resident at that kernel's occupancy, at most
@@ -236,6 +244,9 @@ struct PrepArgs {
   // for the device): the column pass stores each class's task count there
   // with system-scope stores, for a host that launches only non-empty classes
   int32_t* class_counts = nullptr;
+  // the assignment's finished-image count (see AssignArgs::done), zeroed by
+  // the column pass, or null
+  int* done = nullptr;
   int* ncols;
   int* colmap;
   int* slot_of_col;
@@ -314,9 +325,18 @@ struct AssignArgs {
   unsigned char* fill_tail;
   int64_t fill_ntail;
   int fill_blocks;
-  // finished-image count (zeroed by finalize): the assignment workgroup that
-  // finishes last runs the per-layer pass `layer_args`, or done == null
+  // finished-image count (zeroed by finalize when reset_done is set, else
+  // by the column pass): the assignment workgroup that finishes last runs
+  // the per-layer pass `layer_args`, or done == null
   int* done;
+  int reset_done = 1;
+  // image subset of this finalize / assignment launch: every image when
+  // phase_class < 0, else the images whose column-tile class (class_of(G +
+  // 1)) is phase_class (phase_in = 1) or is not (phase_in = 0).  Each row's
+  // and image's work is its own, so two complementary launches give the
+  // results of one launch over every image.
+  int phase_class = -1;
+  int phase_in = 1;
   LayerArgs layer_args;
   // dims / params
   int64_t L, B, Q, C, HW, Ht, Wt, GT_total, GT_out, bg, rtiles;
@@ -430,8 +450,9 @@ int launch_prep(const PrepArgs& a, const Dims& d, hipStream_t st);
 // the launches with the profiling events
 int launch_cost(const CostArgs& a, const Dims& d, int dtype, bool force_masks, hipStream_t st,
                 unsigned classes = ~0u, bool prof = true);
-int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st);
-int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st);
+int launch_finalize(const AssignArgs& a, const Dims& d, hipStream_t st,
+                    const char* prof = "finalize");
+int launch_assign(const AssignArgs& a, const Dims& d, hipStream_t st, const char* prof = "assign");
 int launch_layer(const LayerArgs& a, hipStream_t st);
 int launch_layer_from_p2g(const int64_t* p2g, float* layer, int64_t L, int64_t B, int64_t Q,
                           double num_masks, int force_masks, int force_cls, int has_void,

@@ -349,8 +349,10 @@ __global__ __launch_bounds__(256) void prep_counts_kernel(PrepArgs a) {
 }
 
 // Workgroup 0: runs once every presence record of the preparation grid is
-// in.  Workgroups 1 .. a.fill.blocks: a slice of the gradient's zero fill.
+// in (and zeroes the assignment's finished-image count).  Workgroups 1 ..
+// a.fill.blocks: a slice of the gradient's zero fill.
 __global__ __launch_bounds__(1024) void prep_columns_kernel(PrepArgs a) {
+  if (a.done && blockIdx.x == 0 && threadIdx.x == 0) *a.done = 0;
   if (blockIdx.x > 0) {
     fill_slice(a.fill, blockIdx.x - 1);
     return;

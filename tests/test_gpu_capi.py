@@ -178,8 +178,10 @@ def hip_runtime():
     pytest.skip("HIP runtime not found in the process")
 
 
-def polled_forward(lib, x, p, words):
-    """ml_mask_matching_forward_polled with the host/device words `words`."""
+def polled_forward(lib, x, p, words, prefill=False):
+    """ml_mask_matching_forward_polled with the host/device words `words`
+    (with prefill: a gradient-sized buffer of nonzero bytes to zero-fill,
+    returned as "prefill")."""
     s = x["shape"]
     L, B, Q, G = s.L, s.B, s.Q, s.GT_total - 1
     dev = "cuda"
@@ -189,6 +191,9 @@ def polled_forward(lib, x, p, words):
                sep=torch.full((3, L, B, Q, G), float("nan"), device=dev),
                saved=torch.zeros(lib.ml_saved_bytes(s, p, x["dtype"]), dtype=torch.uint8, device=dev),
                void=torch.full((1,), -1, dtype=torch.int32, device=dev))
+    if prefill:
+        out["prefill"] = torch.full((x["z"].numel() * x["z"].element_size(),), 0x5A, dtype=torch.uint8,
+                                    device=dev)
     wsb = lib.ml_mask_matching_workspace_size(s, p, x["dtype"])
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -197,24 +202,35 @@ def polled_forward(lib, x, p, words):
     rc = lib.ml_mask_matching_forward_polled(
         ctypes.byref(s), ctypes.byref(p), x["dtype"], ptr(x["z"]), ptr(x["tgt"]), ML_F32, ptr(x["zc"]),
         ptr(x["ct"]), ptr(out["p2g"]), ptr(out["pr"]), ptr(out["means"]), ptr(out["sep"]),
-        ptr(out["saved"]), None, ptr(out["void"]), None, ptr(ws), wsb, stream, hdev, hhost)
+        ptr(out["saved"]), ptr(out["prefill"]) if prefill else None, ptr(out["void"]), None, ptr(ws), wsb,
+        stream, hdev, hhost)
     assert rc == 0, lib.ml_last_error().decode()
     torch.cuda.synchronize()
     return {k: v.cpu() for k, v in out.items()}
 
 
+def class_of(g):
+    """Column-tile class of an image with g non-empty GTs (g + 1 slots in
+    tiles of 16: at most 2 tiles, at most 7, more)."""
+    need = (g + 1 + 15) // 16
+    return 0 if need <= 2 else 1 if need <= 7 else 2
+
+
 def two_size_case(seed, dtype, big_gts):
     """Images 0, 1 with at most 12 and 20 GTs and image 2 with exactly
-    `big_gts` non-empty GTs (disjoint 3 x 3 squares), so that column-tile
-    class 1 has image 2 when big_gts >= 32 and no image otherwise; GT_total
-    is 41 in every case."""
-    x = make(seed, B=3, Q=40, H=32, W=32, G=40, C=9, dtype=dtype)
+    `big_gts` non-empty GTs (disjoint 3 x 3 squares), so that image 2 is in
+    column-tile class class_of(big_gts) and images 0, 1 in class 0; GT_total
+    is 41 (64 x 64 cells and GT_total 121 for big_gts > 40)."""
+    wide = big_gts > 40
+    G = 120 if wide else 40
+    x = make(seed, B=3, Q=40, H=64 if wide else 32, W=64 if wide else 32, G=G, C=9, dtype=dtype)
+    per = 16 if wide else 8
     tgt = x["tgt_np"].copy()
     tgt[0][tgt[0] > 12] = 0
     tgt[1][tgt[1] > 20] = 0
     tgt[2] = 0
     for g in range(1, big_gts + 1):
-        y0, x0 = ((g - 1) // 8) * 6, ((g - 1) % 8) * 4
+        y0, x0 = ((g - 1) // per) * 6, ((g - 1) % per) * 4
         tgt[2, y0:y0 + 3, x0:x0 + 3] = g
     x["tgt_np"] = tgt
     x["tgt"] = torch.from_numpy(tgt).cuda()
@@ -222,11 +238,14 @@ def two_size_case(seed, dtype, big_gts):
 
 
 @pytest.mark.parametrize("dtype", [ML_F32, ML_BF16])
-@pytest.mark.parametrize("big_gts", [20, 40])
+@pytest.mark.parametrize("big_gts", [20, 40, 120])
 def test_capi_polled_forward_same_results(lib, dtype, big_gts):
-    """The polled forward skips the empty wider class (big_gts = 20: class 1
-    has no image) or launches it (40), and returns exactly what
-    ml_mask_matching_forward returns; its words hold the classes' task
+    """The polled forward skips the empty wider classes (big_gts = 20: only
+    class 0 has images) or launches them (40: class 1, 120: class 2), and
+    returns exactly what ml_mask_matching_forward returns, with the gradient
+    buffer zero-filled.  With two non-empty classes the first class's
+    finalize and assignment run on the side stream (class 0 first for 40,
+    the widest class first for 120).  Its words hold the classes' task
     counts."""
     rt = hip_runtime()
     P = ctypes.c_void_p
@@ -243,14 +262,16 @@ def test_capi_polled_forward_same_results(lib, dtype, big_gts):
         p = Params(1.0, 1.0, 1.0, 1.0, 0, 1.0, 0.05, 1e30, -1.0, 1, 0, 1, 0, 0.0, -1.0, 0.0, -1.0, 8, 1, 1)
         want = forward(lib, x, p)
         for _ in range(2):  # twice: the words are re-armed by each call
-            got = polled_forward(lib, x, p, (d, h))
+            got = polled_forward(lib, x, p, (d, h), prefill=True)
             for k in ("p2g", "pr", "means", "sep", "saved", "void"):
                 assert torch.equal(got[k], want[k]), k
+            assert not got["prefill"].any()
             rtiles = (x["shape"].Q + 15) // 16
             present = [len(np.setdiff1d(np.unique(x["tgt_np"][b]), [0])) for b in range(3)]
-            cls = [0 if g + 1 <= 32 else 1 for g in present]
+            assert present[2] == big_gts
+            cls = [class_of(g) for g in present]
             n = [words[i] for i in range(3)]
-            assert n == [cls.count(0) * rtiles, cls.count(1) * rtiles, 0], (n, present)
-            assert n[1] == (rtiles if big_gts == 40 else 0)
+            assert n == [cls.count(c) * rtiles for c in range(3)], (n, present)
+            assert n[class_of(big_gts)] >= rtiles
     finally:
         rt.hipHostFree(h)

@@ -53,7 +53,7 @@ def rounded(z, dtype):
 
 
 def make_case(seed, L=1, B=2, Q=20, H=16, W=16, s=1, G=6, C=9, dtype="float32", sigma=2.0,
-              empty_image=False, extreme=False, grid=False):
+              empty_image=False, extreme=False, grid=False, grid_sizes=None):
     rng = np.random.default_rng(seed)
     z = rng.normal(0, sigma, size=(L, B, Q, H, W)).astype(np.float32)
     if extreme:  # |z| >= 64 in a few rows: outside the bf16 table, formulas redo those waves
@@ -66,13 +66,14 @@ def make_case(seed, L=1, B=2, Q=20, H=16, W=16, s=1, G=6, C=9, dtype="float32", 
     for b in range(B):
         if empty_image and b == 0:
             continue
-        if grid:  # G disjoint blocks, labels shuffled: exactly G non-empty GTs
-            r = int(math.ceil(math.sqrt(G)))
-            c = int(math.ceil(G / r))
+        if grid:  # Gb disjoint blocks, labels shuffled: exactly Gb non-empty GTs
+            Gb = G if grid_sizes is None else grid_sizes[b]
+            r = int(math.ceil(math.sqrt(Gb)))
+            c = int(math.ceil(Gb / r))
             hb, wb = (H * s) // r, (W * s) // c
             assert hb > 0 and wb > 0, "grid case: blocks need a cell each"
-            perm = rng.permutation(G) + 1
-            for i in range(G):
+            perm = rng.permutation(G)[:Gb] + 1
+            for i in range(Gb):
                 y0, x0 = (i // c) * hb, (i % c) * wb
                 tgt[b, y0:y0 + hb, x0:x0 + wb] = perm[i]
             continue
@@ -213,6 +214,13 @@ MATCH_CASES = [
          m=dict(force_masks=True, force_cls=True)),
     dict(name="wide16_force", kw=dict(G=120, Q=40, H=32, W=32, grid=True), p={}, m=dict(force_masks=True)),
     dict(name="wide16", kw=dict(G=120, Q=130, H=32, W=32, grid=True), p={}, m={}),
+    # images in all three column-tile classes (10, 60, 120 GTs), two layers:
+    # the widest class's finalize and assignment run on the side stream
+    dict(name="mixed_classes_l2", kw=dict(L=2, B=3, G=120, Q=130, H=32, W=32, grid=True,
+                                          grid_sizes=(10, 60, 120)), p={}, m={}),
+    dict(name="mixed_classes_round_K2", kw=dict(B=3, G=120, Q=130, H=32, W=32, grid=True,
+                                                grid_sizes=(120, 25, 70)), p=dict(use_softmax=True),
+         m=dict(K=2, strategy=1, force_cls=True, void=8)),
     # bf16 with forced-empty masks runs without the table: slot sums in bf16
     dict(name="bf16_wide7_force", kw=dict(G=40, Q=50, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True),
          p={}, m=dict(force_masks=True, force_cls=True)),
@@ -358,6 +366,12 @@ BWD_CASES = [
     dict(name="f32_grid40", kw=dict(G=40, Q=50, H=32, W=32, grid=True), p={}, m=dict(force_cls=True, void=8)),
     dict(name="bf16_grid120", kw=dict(G=120, Q=130, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True),
          p={}, m=dict(force_cls=True, void=8)),
+    # the widest class's images assigned on the side stream, the gradient
+    # fill with the other images' launches
+    dict(name="f32_mixed_classes_l2", kw=dict(L=2, B=3, G=120, Q=130, H=32, W=32, grid=True,
+                                              grid_sizes=(10, 60, 120)), p={}, m=dict(force_cls=True, void=8)),
+    dict(name="bf16_mixed_classes", kw=dict(B=3, G=120, Q=130, H=32, W=32, dtype="bfloat16", sigma=3.0,
+                                            grid=True, grid_sizes=(120, 8, 120)), p={}, m={}),
     dict(name="f32_grid120_forcemasks", kw=dict(G=120, Q=40, H=32, W=32, grid=True), p={},
          m=dict(force_masks=True)),
 ]

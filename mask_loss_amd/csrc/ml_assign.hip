@@ -525,49 +525,46 @@ __device__ __forceinline__ double wave_min_f64(double v) {
   v = min_f64(v, mov_dpp_d<0x143, 0xC>(v));  // row_bcast:31
   return readlane_d(v, 63);
 }
-// Index of the lowest set bit of a 64-bit lane mask, -1 (all ones) when the
-// mask is empty (s_ff1_i32_b64).
-__device__ __forceinline__ uint32_t first_lane(uint64_t m) {
-  return m ? (uint32_t)__builtin_ctzll(m) : 0xFFFFFFFFu;
+// Index of the lowest set bit of a wave-uniform 64-bit lane mask, -1 (all
+// ones) when the mask is empty: s_ff1_i32_b64 itself.
+__device__ __forceinline__ uint32_t first_lane_s(uint64_t m) {
+  uint32_t r;
+  asm("s_ff1_i32_b64 %0, %1" : "=s"(r) : "s"(m));
+  return r;
 }
-// Register slot t (wave-uniform) of lane l: the slot is selected in every
-// lane first, then one readlane fetches lane l's.  SlotMask's comparisons
-// t == k each take their own opaque copy of t, and an empty volatile asm
-// statement separates the steps of a select chain: otherwise the compiler
-// turns the chain into a dynamically indexed array (which it places in
-// scratch memory).
-template <int NJ>
-struct SlotMask {
-  bool is[NJ];
-  __device__ __forceinline__ explicit SlotMask(int t) {
-    t = __builtin_amdgcn_readfirstlane(t);
-#pragma unroll
-    for (int k = 0; k < NJ; ++k) {
-      int c = t;
-      asm volatile("" : "+s"(c));
-      is[k] = c == k;
-    }
-  }
-};
-template <int NJ>
-__device__ __forceinline__ int sel_i(const int (&x)[NJ], const SlotMask<NJ>& m, int l) {
-  int r = x[0];
-#pragma unroll
-  for (int k = 1; k < NJ; ++k) {
-    asm volatile("");
-    r = m.is[k] ? x[k] : r;
-  }
-  return __builtin_amdgcn_readlane(r, l);
+// Scalar unsigned minimum and exponent bits of wave-uniform values (kept on
+// the scalar unit: the compiler would otherwise move them to vector ops and
+// read the result back).
+__device__ __forceinline__ uint32_t min_s(uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("s_min_u32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b));
+  return r;
 }
+__device__ __forceinline__ uint32_t exp_bits_s(double x) {
+  uint32_t r;
+  asm("s_and_b32 %0, %1, 0x7ff00000" : "=s"(r) : "s"(hi_word(x)));
+  return r;
+}
+// The solver's per-slot state that is read or written at a wave-uniform slot
+// (matched rows, their potentials, the predecessors) as vectors: the
+// compiler then accesses slot t with VGPR index mode (s_set_gpr_idx_on, one
+// v_mov per dword, s_set_gpr_idx_off) instead of a compare-and-select chain
+// over every slot.  It picks the index mode for vectors whose select chain
+// would take more than 16 instructions, hence 16 ints and at least 8
+// doubles whatever NJ; slots NJ and up are never touched.
+typedef int SlotsI __attribute__((ext_vector_type(16)));
 template <int NJ>
-__device__ __forceinline__ double sel_d(const double (&x)[NJ], const SlotMask<NJ>& m, int l) {
-  double r = x[0];
-#pragma unroll
-  for (int k = 1; k < NJ; ++k) {
-    asm volatile("");
-    r = m.is[k] ? x[k] : r;
-  }
-  return readlane_d(r, l);
+using SlotsD = double __attribute__((ext_vector_type(NJ <= 8 ? 8 : 16)));
+// Slot t (wave-uniform) of x.
+template <int NJ, class V>
+__device__ __forceinline__ auto slot_at(const V& x, int t) {
+  if constexpr (NJ == 1) return x[0];
+  else return x[__builtin_amdgcn_readfirstlane(t)];
+}
+template <int NJ, class V, class E>
+__device__ __forceinline__ void slot_set(V& x, int t, E e) {
+  if constexpr (NJ == 1) x[0] = e;
+  else x[__builtin_amdgcn_readfirstlane(t)] = e;
 }
 
 // ---------------------------------------------------------------------------
@@ -665,10 +662,12 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
   wave_sync();
   if (M == 0 || n == 0 || n < M) return true;
   const double kQNaN = __longlong_as_double(0x7FF8000000000000ll);
-  double v[NJ], ucol[NJ];
+  double v[NJ];
+  SlotsD<NJ> ucol = {};
   // pr: the column's matched row p (0 = free) in the low 16 bits and that
   // row's cost-matrix row in the high 16 (rows <= 1024, columns <= 256)
-  int pr[NJ], predj[NJ];
+  SlotsI pr = {};
+  int predj[NJ];
   bool valid[NJ];
 #pragma unroll
   for (int t = 0; t < NJ; ++t) {
@@ -691,7 +690,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     // minv: a quiet NaN marks a column in the tree (and an unused slot);
     // f: 1.0 for a column in the tree, else 0.0 (its low word stays 0)
     double minv[NJ], f[NJ];
-    int wy[NJ];
+    SlotsI wy = {};
 #pragma unroll
     for (int t = 0; t < NJ; ++t) {
       minv[t] = valid[t] ? INFINITY : kQNaN;
@@ -715,29 +714,20 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         lmin = min_f64(lmin, minv[t]);
       }
       const double delta = wave_min_f64(lmin);
-      if (!(delta < INFINITY)) {  // unreachable with finite costs (n >= M free columns)
+      // !(delta < inf), tested on the scalar high word: delta is +inf or a
+      // NaN (no column left, unreachable with finite costs and n >= M free
+      // columns); it is never -inf
+      if (exp_bits_s(delta) == 0x7FF00000u) {
         ok = false;
         break;
       }
       // key = j1 - 1 of the entering column: the lowest (slot, lane) whose
-      // minv equals delta.  ls: this lane's lowest such slot (NJ if none).
-      // When one lane holds delta, that lane and its slot; otherwise (equal
-      // minima in several lanes) the lowest slot's lowest lane, from one
-      // ballot per slot (an empty slot gives all ones).
-      int ls = NJ;
+      // minv equals delta, the minimum over the slots of the first lane of
+      // each slot's ballot (an empty ballot gives all ones)
+      uint32_t key = first_lane_s(__builtin_amdgcn_ballot_w64(minv[0] == delta));
 #pragma unroll
-      for (int t = NJ - 1; t >= 0; --t) ls = minv[t] == delta ? t : ls;
-      const uint64_t hit = __builtin_amdgcn_ballot_w64(ls < NJ);
-      uint32_t key;
-      if (__builtin_popcountll(hit) == 1) {
-        const int l = __builtin_ctzll(hit);
-        key = (uint32_t)(64 * __builtin_amdgcn_readlane(ls, l) + l);
-      } else {
-        key = 0xFFFFFFFFu;
-#pragma unroll
-        for (int t = 0; t < NJ; ++t)
-          key = min(key, first_lane(__builtin_amdgcn_ballot_w64(minv[t] == delta)) | (uint32_t)(64 * t));
-      }
+      for (int t = 1; t < NJ; ++t)
+        key = min_s(key, first_lane_s(__builtin_amdgcn_ballot_w64(minv[t] == delta)) | (uint32_t)(64 * t));
       // potentials: columns in the tree (and column 0 = row i) move by delta
       // (f = 1), the others' minv by -delta; then column j1 enters the tree
 #pragma unroll
@@ -751,12 +741,11 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       ucur += delta;
       j0 = (int)key + 1;
       const int ol = (int)(key & 63u), ot = (int)(key >> 6);
-      const SlotMask<NJ> sm(ot);
-      const int pr1 = sel_i<NJ>(pr, sm, ol);
+      const int pr1 = __builtin_amdgcn_readlane(slot_at<NJ>(pr, ot), ol);
       if ((pr1 & 0xFFFF) == 0) break;  // j1 is free: augment
       // next row of the tree: the one matched to column j1 (its potential
       // took no delta above: j1 was outside the tree)
-      ui0 = sel_d<NJ>(ucol, sm, ol);
+      ui0 = readlane_d(slot_at<NJ>(ucol, ot), ol);
       read_cost_row<NJ, CM>(cost, pr1 >> 16, predj, rawf);
     }
     if (!ok) break;
@@ -767,8 +756,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     // row) of the column it was reached from; column 0 holds row i.
     for (int steps = 0; j0 != 0 && steps <= n; ++steps) {
       const int ol = (j0 - 1) & 63, ot = (j0 - 1) >> 6;
-      const SlotMask<NJ> sm(ot);
-      const int jp = sel_i<NJ>(wy, sm, ol);
+      const int jp = __builtin_amdgcn_readlane(slot_at<NJ>(wy, ot), ol);
       int npr;
       double nu;
       if (jp == 0) {
@@ -776,17 +764,12 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         nu = ucur;
       } else {
         const int pl = (jp - 1) & 63, pt = (jp - 1) >> 6;
-        const SlotMask<NJ> pm(pt);
-        npr = sel_i<NJ>(pr, pm, pl);
-        nu = sel_d<NJ>(ucol, pm, pl);
+        npr = __builtin_amdgcn_readlane(slot_at<NJ>(pr, pt), pl);
+        nu = readlane_d(slot_at<NJ>(ucol, pt), pl);
       }
       const bool me = lane == ol;
-#pragma unroll
-      for (int t = 0; t < NJ; ++t) {
-        const bool mine = me & sm.is[t];
-        pr[t] = mine ? npr : pr[t];
-        ucol[t] = mine ? nu : ucol[t];
-      }
+      slot_set<NJ>(pr, ot, me ? npr : slot_at<NJ>(pr, ot));
+      slot_set<NJ>(ucol, ot, me ? nu : slot_at<NJ>(ucol, ot));
       j0 = jp;
     }
     colcur = cn;

@@ -485,6 +485,9 @@ def main():
     roofline["practical_read_ceiling_GBs"] = rc_["median_GBs"]
     if achieved:
         roofline["frac_of_practical_read_ceiling"] = round(achieved / rc_["median_GBs"], 4)
+    if dom_bytes is None:
+        roofline["note"] = ("the dominant launch is bound by the serial float64 assignment chains "
+                            "(one wave per image), not by HBM or MFMA")
     step_roof = {
         "algorithmic_bytes": step_bytes,
         "hbm_floor_us": round(step_bytes / HBM_PEAK_GBS / 1e3, 1),

@@ -139,12 +139,13 @@ __device__ __forceinline__ RowCoef row_coef(const BwdArgs& a, float S, float P, 
 }
 
 // d(loss)/dz of one cell with target count tk
+template <int EM = 0>
 __device__ __forceinline__ float grad_elem(float z, float tk, const ElemParams& ep, float N2,
                                            const RowCoef& r) {
   const Sig s = sig_terms(z);
-  const float w = unc_weight(s, ep);
+  const float w = unc_weight_m<EM>(s, ep);
   float mn, mp;
-  focal_mods(s, ep, mn, mp);
+  focal_mods_m<EM>(s, ep, mn, mp);
   const float g = ep.gamma;
   const float negc = fmaxf(N2 - tk, 0.f);
   const float gpos = -w * ep.ap * tk * mp * (g * s.p * s.cp + s.q1);
@@ -271,8 +272,14 @@ __device__ __forceinline__ void bwd_chunk(const BwdArgs& a, int64_t row, int64_t
     const int64_t cell0 = c0 + u * 256 * 8;
     if (cell0 < a.HW) {
       float gr[8];
+      // one branch on the modes per 8 cells (wave-uniform), not per cell
+      if (default_modes(ep)) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) gr[k] = grad_elem(z[u][k], matched ? t[u][k] : 0.f, ep, a.N2, rc);
+        for (int k = 0; k < 8; ++k) gr[k] = grad_elem<1>(z[u][k], matched ? t[u][k] : 0.f, ep, a.N2, rc);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) gr[k] = grad_elem(z[u][k], matched ? t[u][k] : 0.f, ep, a.N2, rc);
+      }
       store8(a.grad, a.dtype, rbase + cell0, gr, a.HW - cell0, vec);
     }
   }

@@ -141,6 +141,34 @@ __device__ __forceinline__ void focal_mods(const Sig& s, const ElemParams& ep, f
   }
 }
 
+// The same terms with the modes fixed at compile time where EM = 1: no
+// focal modulation (gamma = 0) and the uncertainty weight H(p)^1, the
+// operator's default arguments.  The arithmetic is that of unc_weight /
+// focal_mods for those modes, without a branch on the modes per logit;
+// EM = 0 is the general form.  Callers pick EM once per group of logits
+// (default_modes).
+__device__ __forceinline__ bool default_modes(const ElemParams& ep) {
+  return ep.gamma_mode == 0 && ep.ug_mode == 1;
+}
+template <int EM>
+__device__ __forceinline__ float unc_weight_m(const Sig& s, const ElemParams& ep) {
+  if constexpr (EM == 1) {
+    const float h = fmaf(s.p, s.cp, s.q1 * s.cn) * kLog2e;
+    return __builtin_amdgcn_fmed3f(h, ep.ug_min, 1.0f);
+  } else {
+    return unc_weight(s, ep);
+  }
+}
+template <int EM>
+__device__ __forceinline__ void focal_mods_m(const Sig& s, const ElemParams& ep, float& mn, float& mp) {
+  if constexpr (EM == 1) {
+    mn = 1.f;
+    mp = 1.f;
+  } else {
+    focal_mods(s, ep, mn, mp);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // wave reductions (wave64)
 // ---------------------------------------------------------------------------

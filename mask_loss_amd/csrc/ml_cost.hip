@@ -30,6 +30,7 @@
 // products keep float32 accuracy.
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "ml_internal.h"
 
@@ -76,13 +77,14 @@ __device__ __forceinline__ uint32_t bfi32(uint32_t m, uint32_t a, uint32_t b) {
 
 // The four planes of one logit from the float32 formulas (+ the unweighted
 // terms of the unmatched-mask penalty).
+template <int EM = 0>
 __device__ __forceinline__ void planes_formula(float z, const ElemParams& ep, float& neg,
                                                float& pos, float& wp, float& w, float& negu,
                                                float& pu) {
   const Sig s = sig_terms(z);
-  w = unc_weight(s, ep);
+  w = unc_weight_m<EM>(s, ep);
   float mn, mp;
-  focal_mods(s, ep, mn, mp);
+  focal_mods_m<EM>(s, ep, mn, mp);
   negu = ep.an * mn * s.cn;
   pu = s.p;
   neg = w * negu;
@@ -198,10 +200,9 @@ __device__ __forceinline__ void planes8_formula(const Raw8<DT>& r, const ElemPar
   float z[8];
   raw_to_f32<DT>(r, z);
   float v[4][8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
+  auto cell = [&](auto em, int k) {
     float neg, pos, wp, w, nu, pu;
-    planes_formula(z[k], ep, neg, pos, wp, w, nu, pu);
+    planes_formula<decltype(em)::value>(z[k], ep, neg, pos, wp, w, nu, pu);
     const bool ok = !MASK || k < nvalid;
     v[0][k] = ok ? neg : 0.f;
     v[1][k] = ok ? pos : 0.f;
@@ -211,6 +212,14 @@ __device__ __forceinline__ void planes8_formula(const Raw8<DT>& r, const ElemPar
       ub += ok ? nu : 0.f;
       up += ok ? pu : 0.f;
     }
+  };
+  // one branch on the modes per 8 logits (wave-uniform), not per logit
+  if (default_modes(ep)) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cell(std::integral_constant<int, 1>(), k);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) cell(std::integral_constant<int, 0>(), k);
   }
 #pragma unroll
   for (int pl = 0; pl < 4; ++pl) split_pack<NS>(v[pl], A[pl]);

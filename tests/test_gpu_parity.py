@@ -218,6 +218,12 @@ MATCH_CASES = [
     # the widest class's finalize and assignment run on the side stream
     dict(name="mixed_classes_l2", kw=dict(L=2, B=3, G=120, Q=130, H=32, W=32, grid=True,
                                           grid_sizes=(10, 60, 120)), p={}, m={}),
+    # only wide images (115-130 GTs), one and two layers
+    dict(name="wide_parts", kw=dict(B=4, G=130, Q=140, H=32, W=32, grid=True,
+                                    grid_sizes=(115, 130, 120, 125)), p={}, m={}),
+    dict(name="bf16_wide_parts_l2", kw=dict(L=2, B=4, G=130, Q=140, H=32, W=32, dtype="bfloat16", sigma=3.0,
+                                            grid=True, grid_sizes=(125, 40, 130, 118)), p={},
+         m=dict(force_cls=True, void=8)),
     dict(name="mixed_classes_round_K2", kw=dict(B=3, G=120, Q=130, H=32, W=32, grid=True,
                                                 grid_sizes=(120, 25, 70)), p=dict(use_softmax=True),
          m=dict(K=2, strategy=1, force_cls=True, void=8)),
@@ -367,11 +373,13 @@ BWD_CASES = [
     dict(name="bf16_grid120", kw=dict(G=120, Q=130, H=32, W=32, dtype="bfloat16", sigma=3.0, grid=True),
          p={}, m=dict(force_cls=True, void=8)),
     # the widest class's images assigned on the side stream, the gradient
-    # fill with the other images' launches
+    # fill with the other images' launches (the mixed cases); only wide images
     dict(name="f32_mixed_classes_l2", kw=dict(L=2, B=3, G=120, Q=130, H=32, W=32, grid=True,
                                               grid_sizes=(10, 60, 120)), p={}, m=dict(force_cls=True, void=8)),
     dict(name="bf16_mixed_classes", kw=dict(B=3, G=120, Q=130, H=32, W=32, dtype="bfloat16", sigma=3.0,
                                             grid=True, grid_sizes=(120, 8, 120)), p={}, m={}),
+    dict(name="f32_wide_parts", kw=dict(B=4, G=130, Q=140, H=32, W=32, grid=True,
+                                        grid_sizes=(115, 130, 120, 125)), p={}, m=dict(force_cls=True, void=8)),
     dict(name="f32_grid120_forcemasks", kw=dict(G=120, Q=40, H=32, W=32, grid=True), p={},
          m=dict(force_masks=True)),
 ]

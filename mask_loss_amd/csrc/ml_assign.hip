@@ -987,8 +987,11 @@ __global__ __launch_bounds__(256) void assign_kernel(AssignArgs a) {
   // fill workgroups should they share the CU.
   __builtin_amdgcn_s_setprio(3);
   const int64_t lb = blockIdx.x, b = lb % a.B;
-  // another launch's image: no work, no count
-  if (!in_phase(a.phase_class, a.phase_in, __builtin_amdgcn_readfirstlane(a.ncols[b]))) return;
+  // another launch's image: no work, no count (the column count is read only
+  // for a launch restricted to a subset)
+  if (a.phase_class >= 0 &&
+      !in_phase(a.phase_class, a.phase_in, __builtin_amdgcn_readfirstlane(a.ncols[b])))
+    return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t Q = a.Q, GTo = a.GT_out;
   float* costL = (float*)(smem + L.costL);

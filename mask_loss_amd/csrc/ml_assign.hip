@@ -630,9 +630,18 @@ __device__ __forceinline__ void read_cost_row(const CostRows<CM>& cost, int col,
 #pragma unroll
     for (int t = 0; t < NJ; ++t) raw[t] = crow[predj[t]];
   } else {
-    const double* crow = cost.glb64 + (uint32_t)(col * cost.ldq);
+    // buffer loads over the image's rows: the row's byte offset is a scalar
+    // operand and the lane's query offset a loop-invariant 32-bit register,
+    // so a row read needs no per-lane address arithmetic (reads past the
+    // rows return 0: the rows are [rows][ldq] doubles, rows < 256)
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)cost.glb64, (short)0, 256 * cost.ldq * 8, 0x00020000);
+    const int rowoff = col * cost.ldq * 8;
 #pragma unroll
-    for (int t = 0; t < NJ; ++t) raw[t] = crow[predj[t]];
+    for (int t = 0; t < NJ; ++t) {
+      const u32x2_t w = __builtin_amdgcn_raw_buffer_load_b64(rsrc, predj[t] * 8, rowoff, 0);
+      raw[t] = __builtin_bit_cast(double, w);
+    }
   }
 }
 // c(i, j) of the reference (src/cpu/matching.cpp:497-511): the cost, or BIG
@@ -703,7 +712,7 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
     for (;;) {
       // relax every column outside the tree (no branches: the NJ chains
       // interleave) and keep this lane's minimum
-      double lmin = INFINITY;
+      double lm[NJ];
 #pragma unroll
       for (int t = 0; t < NJ; ++t) {
         const double cij = cij_of<CM>(rawf[t], thr, BIG);
@@ -711,9 +720,15 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         const bool upd = cur < minv[t];
         minv[t] = upd ? cur : minv[t];
         wy[t] = upd ? j0 : wy[t];
-        lmin = min_f64(lmin, minv[t]);
+        lm[t] = minv[t];
       }
-      const double delta = wave_min_f64(lmin);
+      // the lane's minimum as a tree (a lane whose slots all hold the NaN
+      // marker gives NaN, which the wave minimum ignores like the markers)
+#pragma unroll
+      for (int w = 1; w < NJ; w *= 2)
+#pragma unroll
+        for (int t = 0; t + w < NJ; t += 2 * w) lm[t] = min_f64(lm[t], lm[t + w]);
+      const double delta = wave_min_f64(lm[0]);
       // !(delta < inf), tested on the scalar high word: delta is +inf or a
       // NaN (no column left, unreachable with finite costs and n >= M free
       // columns); it is never -inf

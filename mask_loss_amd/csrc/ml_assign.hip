@@ -739,10 +739,15 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
       // key = j1 - 1 of the entering column: the lowest (slot, lane) whose
       // minv equals delta, the minimum over the slots of the first lane of
       // each slot's ballot (an empty ballot gives all ones)
-      uint32_t key = first_lane_s(__builtin_amdgcn_ballot_w64(minv[0] == delta));
+      // (every ballot is issued before the first scan, so the compares do
+      // not wait for each other's mask registers)
+      uint64_t bal[NJ];
 #pragma unroll
-      for (int t = 1; t < NJ; ++t)
-        key = min_s(key, first_lane_s(__builtin_amdgcn_ballot_w64(minv[t] == delta)) | (uint32_t)(64 * t));
+      for (int t = 0; t < NJ; ++t) bal[t] = __builtin_amdgcn_ballot_w64(minv[t] == delta);
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t key = first_lane_s(bal[0]);
+#pragma unroll
+      for (int t = 1; t < NJ; ++t) key = min_s(key, first_lane_s(bal[t]) | (uint32_t)(64 * t));
       // potentials: columns in the tree (and column 0 = row i) move by delta
       // (f = 1), the others' minv by -delta; then column j1 enters the tree
 #pragma unroll
@@ -782,9 +787,14 @@ __device__ bool hungarian_wave(const CostRows<CM>& cost, const int* preds, int n
         npr = __builtin_amdgcn_readlane(slot_at<NJ>(pr, pt), pl);
         nu = readlane_d(slot_at<NJ>(ucol, pt), pl);
       }
+      // the slot's old values read by every lane (kept unconditional, so the
+      // new slot is one select, not an exec-masked read)
+      int opr = slot_at<NJ>(pr, ot);
+      double ou = slot_at<NJ>(ucol, ot);
+      asm("" : "+v"(opr), "+v"(ou));
       const bool me = lane == ol;
-      slot_set<NJ>(pr, ot, me ? npr : slot_at<NJ>(pr, ot));
-      slot_set<NJ>(ucol, ot, me ? nu : slot_at<NJ>(ucol, ot));
+      slot_set<NJ>(pr, ot, me ? npr : opr);
+      slot_set<NJ>(ucol, ot, me ? nu : ou);
       j0 = jp;
     }
     colcur = cn;

@@ -290,15 +290,33 @@ __global__ __launch_bounds__(256) void bwd_mask_chunk_kernel(BwdArgs a, int64_t 
   bwd_chunk(a, (int64_t)blockIdx.x / nchunk, (int64_t)blockIdx.x % nchunk);
 }
 
+template <int MAXR>
+__device__ __forceinline__ void cls_row(const BwdArgs& a, int64_t row);
+
 // Only the rows of the forward's matched list (the rest of the gradient
 // already holds zeros); the grid strides over (list entry, chunk) items, so
-// its size does not depend on the device-side match count.
+// its size does not depend on the device-side match count.  With cls_fused,
+// the class-logit gradients follow, one row per wave, on the workgroups that
+// had the fewest mask items (items are dealt out round robin: the last
+// total % grid ones, all of them when the items divide evenly), so they run
+// in the mask work's last round instead of in a launch of their own.
 __global__ __launch_bounds__(256) void bwd_mask_list_kernel(BwdArgs a, int64_t nchunk) {
   const int64_t rows = a.L * a.B * a.Q;
   const int64_t n = min((int64_t)a.list[0], rows);
-  for (int64_t it = blockIdx.x; it < n * nchunk; it += gridDim.x) {
+  const int64_t total = n * nchunk;
+  for (int64_t it = blockIdx.x; it < total; it += gridDim.x) {
     const int64_t row = a.list[1 + it / nchunk];
     if (row >= 0 && row < rows) bwd_chunk(a, row, it % nchunk);
+  }
+  if (a.cls_fused) {
+    constexpr int kWaves = 4;
+    const int wave = threadIdx.x >> 6;
+    const int64_t G = gridDim.x, extra = total % G;
+    const int64_t nlight = extra == 0 ? G : G - extra;
+    const int64_t rank = (int64_t)blockIdx.x - (G - nlight);
+    if (rank >= 0)
+      for (int64_t r0 = rank * kWaves; r0 < rows; r0 += nlight * kWaves)
+        if (r0 + wave < rows) cls_row<24>(a, r0 + wave);
   }
 }
 
@@ -380,7 +398,7 @@ __device__ __forceinline__ void cls_softmax_regs(const BwdArgs& a, int64_t base,
 // MAXR: the largest register form (logits per lane) this caller holds; the
 // persistent mask kernel keeps it small so its own registers are not squeezed
 template <int MAXR>
-__device__ void cls_row(const BwdArgs& a, int64_t row) {
+__device__ __forceinline__ void cls_row(const BwdArgs& a, int64_t row) {
   const int lane = threadIdx.x & 63;
   const int64_t lb = row / a.Q, l = lb / a.B, b = lb % a.B;
   const int64_t C = a.C;
@@ -767,8 +785,12 @@ int launch_bwd(const BwdArgs& a, const Dims& d, hipStream_t st) {
                            st, b, nchunk);
     } else if (a.stats && a.list) {
       const int64_t nchunk = ceil_div(d.HW, kBwdChunk);
-      const int64_t grid = std::min<int64_t>(rows * nchunk, kBwdListGrid);
-      hipLaunchKernelGGL(bwd_mask_list_kernel, dim3((unsigned)grid), dim3(256), 0, st, a, nchunk);
+      const int64_t grid = std::max<int64_t>(
+          1, std::min<int64_t>(std::max(rows * nchunk, ceil_div(rows, 4)), kBwdListGrid));
+      BwdArgs b = a;
+      b.cls_fused = d.C > 0 ? 1 : 0;
+      cls_done = true;
+      hipLaunchKernelGGL(bwd_mask_list_kernel, dim3((unsigned)grid), dim3(256), 0, st, b, nchunk);
     } else if (a.stats) {
       const int64_t nchunk = ceil_div(d.HW, kBwdChunk);
       hipLaunchKernelGGL(bwd_mask_chunk_kernel, dim3((unsigned)(rows * nchunk)), dim3(256), 0, st,

@@ -360,9 +360,15 @@ BWD_CASES = [
     dict(name="bf16_softmax", kw=dict(dtype="bfloat16", sigma=3.0), p=dict(use_softmax=True),
          m=dict(force_cls=True, void=8)),
     dict(name="f32_odd", kw=dict(Q=37, H=7, W=5, B=3), p={}, m=dict(void=8)),
-    # class rows longer than 256 logits: the class-gradient launch holds 8 or
-    # 16 logits per lane (f32 masks), the bf16 table kernel streams them
+    # class rows longer than 256 logits: held 8 or 16 logits per lane by the
+    # f32 masks' kernels (the matched-row kernel, which also writes the class
+    # gradients in the prefilled mode, and the class launch of the other
+    # modes), streamed by the bf16 table kernel
     dict(name="f32_softmax_C300", kw=dict(C=300, Q=24), p=dict(use_softmax=True),
+         m=dict(force_cls=True, void=299)),
+    # every query matched (more GTs than queries): the matched-row items fill
+    # the whole grid, so every workgroup takes class rows after its mask items
+    dict(name="f32_all_matched_C300", kw=dict(C=300, Q=12, G=20), p=dict(use_softmax=True),
          m=dict(force_cls=True, void=299)),
     dict(name="f32_softmax_C700", kw=dict(C=700, Q=24), p=dict(use_softmax=True),
          m=dict(force_cls=True, void=699)),

@@ -529,7 +529,7 @@ __device__ __forceinline__ double wave_min_f64(double v) {
 // ones) when the mask is empty: s_ff1_i32_b64 itself.
 __device__ __forceinline__ uint32_t first_lane_s(uint64_t m) {
   uint32_t r;
-  asm("s_ff1_i32_b64 %0, %1" : "=s"(r) : "s"(m));
+  asm("s_ff1_i32_b64 %0, %1" : "=s"(r) : "s"(m) : "scc");
   return r;
 }
 // Scalar unsigned minimum and exponent bits of wave-uniform values (kept on
@@ -537,12 +537,12 @@ __device__ __forceinline__ uint32_t first_lane_s(uint64_t m) {
 // read the result back).
 __device__ __forceinline__ uint32_t min_s(uint32_t a, uint32_t b) {
   uint32_t r;
-  asm("s_min_u32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b));
+  asm("s_min_u32 %0, %1, %2" : "=s"(r) : "s"(a), "s"(b) : "scc");
   return r;
 }
 __device__ __forceinline__ uint32_t exp_bits_s(double x) {
   uint32_t r;
-  asm("s_and_b32 %0, %1, 0x7ff00000" : "=s"(r) : "s"(hi_word(x)));
+  asm("s_and_b32 %0, %1, 0x7ff00000" : "=s"(r) : "s"(hi_word(x)) : "scc");
   return r;
 }
 // The solver's per-slot state that is read or written at a wave-uniform slot

@@ -430,7 +430,11 @@ int forward_impl(const ml_shape* s, const ml_params* p, int mask_dtype,
     f.blocks = f.n16 ? (int)std::min<int64_t>(kFillBlocks, ceil_div(f.n16, 1024)) : 0;
     return f;
   };
-  const FillSlice prep_fill = slice(0, kPrepFillBytes);
+  // with three column-tile classes the polled forward may split the images
+  // (the widest class's assignment on a side stream, the critical path): the
+  // column pass, which that path waits for, then leaves its share to the
+  // other images' assignment launch
+  const FillSlice prep_fill = slice(0, plan.nclass == kClasses ? 0 : kPrepFillBytes);
   const FillSlice fin_fill = slice(prep_fill.n16, kFinFillBytes);
   const int64_t assign_from = prep_fill.n16 + fin_fill.n16;
 

@@ -37,6 +37,8 @@ constexpr int kFillBlocks = 64;
 // the finalize launch, as extra workgroups beside their own work: both are
 // short, latency-bound launches that leave HBM nearly idle, so these bytes
 // come off the assignment launch, where the fill outlasts a short assignment.
+// (The column pass takes none when the shape allows three column-tile
+// classes: the split forward's critical path waits for that pass.)
 constexpr int64_t kPrepFillBytes = (int64_t)56 << 20;
 constexpr int64_t kFinFillBytes = (int64_t)16 << 20;
 
